@@ -1,0 +1,42 @@
+// capi_common.h -- host-side helpers shared by the C-ABI translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include "../../include/jllm_hip.h"
+
+namespace jllm_hip {
+
+// Resolve a weight pointer the GPU can read: a registered mapped region's
+// device alias, else the pointer itself when HIP reports device or managed
+// memory (resolve_weight_device_ptr, gemv_q4.cu:105-128).  nullptr if
+// neither.
+const void* resolve_weight(const void* W);
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+inline int launch_status(hipError_t e, const char* tag) {
+    if (e == hipSuccess) return JLLM_OK;
+    fprintf(stderr, "[%s] launch failed: %s\n", tag, hipGetErrorString(e));
+    return JLLM_ERR_LAUNCH;
+}
+
+// Per-device, lazily grown device scratch that is never freed (the
+// reference's static scratch semantics, e.g. gemv_q4.cu:1309-1321).
+struct DeviceScratch {
+    void* ptr[64] = {};
+    size_t cap[64] = {};
+    void* get(size_t bytes) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+        if (bytes > cap[dev]) {
+            if (ptr[dev]) (void)hipFree(ptr[dev]);
+            ptr[dev] = nullptr; cap[dev] = 0;
+            if (hipMalloc(&ptr[dev], bytes) != hipSuccess) { ptr[dev] = nullptr; return nullptr; }
+            cap[dev] = bytes;
+        }
+        return ptr[dev];
+    }
+};
+
+}  // namespace jllm_hip

@@ -1,0 +1,89 @@
+// kq_common.h -- block formats and small device helpers shared by the
+// gfx950 kernels (GEMV, MMQ, attention).  wave64 only.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace jllm_hip {
+
+constexpr int QK_K = 256;
+constexpr int Q4K_BYTES = 144;   // u16 d, u16 dmin, u8 scales[12], u8 qs[128]
+constexpr int Q6K_BYTES = 210;   // u8 ql[128], u8 qh[64], i8 scales[16], u16 d
+constexpr int TYPE_Q4_K = 12;
+constexpr int TYPE_Q6_K = 14;
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);   // v_cvt_f16_f32, RNE
+}
+__device__ __forceinline__ float round_to_f16(float f) {
+    return (float)(_Float16)f;
+}
+__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t h2_bits(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// byte i (0..11) of the Q4_K scales[12], given as three little-endian words
+__device__ __forceinline__ uint32_t sc_byte(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
+    const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
+    return (w >> (8 * (i & 3))) & 0xFFu;
+}
+
+// 6-bit (scale, min) of sub-block j of a Q4_K super-block (the packing of
+// get_scale_min_k4, gemv_q4.cu:185-195).
+__device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j,
+                                              uint32_t& sc, uint32_t& m) {
+    if (j < 4) {
+        sc = sc_byte(s0, s1, s2, j) & 63u;
+        m  = sc_byte(s0, s1, s2, j + 4) & 63u;
+    } else {
+        const uint32_t b = sc_byte(s0, s1, s2, j + 4);
+        sc = (b & 0xFu) | ((sc_byte(s0, s1, s2, j - 4) >> 6) << 4);
+        m  = (b >> 4)   | ((sc_byte(s0, s1, s2, j) >> 6) << 4);
+    }
+}
+
+// 8 bytes starting at a 2-byte-aligned address, from three aligned dword
+// loads.  Reads [floor4(p), floor4(p)+12) which lies inside [p-2, p+10).
+__device__ __forceinline__ uint2 load8_a2(const uint8_t* p) {
+    const uintptr_t a = (uintptr_t)p;
+    const uint32_t* w = (const uint32_t*)(a & ~(uintptr_t)3);
+    const uint32_t sh = (uint32_t)(a & 3) * 8u;
+    const uint32_t w0 = __builtin_nontemporal_load(w + 0);
+    const uint32_t w1 = __builtin_nontemporal_load(w + 1);
+    const uint32_t w2 = __builtin_nontemporal_load(w + 2);
+    uint2 r;
+    r.x = __builtin_amdgcn_alignbit(w1, w0, sh);
+    r.y = __builtin_amdgcn_alignbit(w2, w1, sh);
+    return r;
+}
+
+// per-byte (v - 32) for bytes v in [0, 63] without cross-byte borrows
+__device__ __forceinline__ uint32_t sub32_bytes(uint32_t v) {
+    return ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+__device__ __forceinline__ float fdot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
+}
+
+// swap with the neighbouring lane (lane ^ 1) through DPP quad_perm [1,0,3,2]
+__device__ __forceinline__ int swap_lane1(int v) {
+    return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+}
+
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+}  // namespace jllm_hip

@@ -1,0 +1,120 @@
+"""ctypes binding of libjllm_hip.so (the C ABI declared in include/jllm_hip.h).
+
+Python is only the test/bench harness here: device buffers are torch
+tensors on the GPU, passed by data_ptr(); every call goes through the C ABI
+into the HIP kernels.  There is no fallback: if the library is missing,
+loading raises.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libjllm_hip.so")
+
+_lib = None
+P = ctypes.c_void_p
+I = ctypes.c_int
+I64 = ctypes.c_int64
+F = ctypes.c_float
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "jllm_hip_status_string": (ctypes.c_char_p, [I]),
+    "jllm_hip_register_mapped_weight_region": (I, [P, P, I64]),
+    "jllm_hip_clear_mapped_weight_region": (None, [P]),
+    "jllm_hip_resolve_mapped_weight_device_ptr": (P, [P]),
+    "jllm_hip_gemv_quant": (I, [P, P, I, P, I, I, P]),
+    "jllm_hip_gemv_quant_add": (I, [P, P, I, P, P, I, I, P]),
+    "jllm_hip_gemv_quant_pair": (I, [P, P, I, I, P, P, I, I, P, I, P]),
+    "jllm_hip_gemv_quant_triple": (I, [P, P, I, I, P, P, I, I, P, P, I, I, P, I, P]),
+    "jllm_hip_gemv_quant_f32": (I, [P, P, I, P, I, I, P]),
+    "jllm_hip_gemv_quant_dequant_f32": (I, [P, P, I, P, I, I, P]),
+    "jllm_hip_quantize_q8_1": (I, [P, P, I, P]),
+    "jllm_hip_gemm_quant_batched": (I, [P, P, I, P, I, I, I, P]),
+    "jllm_hip_gemm_quant_batched_f32": (I, [P, P, I, P, I, I, I, P]),
+    "jllm_hip_quantize_mmq_q8_1": (I, [P, P, I, I, I, I, P]),
+    "jllm_hip_mmq_subdots": (I, [P, P, I, P, I, I, I, I, P]),
+    "jllm_hip_flash_attention_decode": (I, [P, P, P, P, I, I, I, I, I, F, I, P, P, I, P]),
+    "jllm_hip_flash_attention_decode_splits": (I, [P, P, P, P, I, I, I, I, I, F, I, P, P, I, I, P]),
+    "jllm_hip_decode_attn_splits": (I, [I]),
+    "jllm_hip_get_splitk_partials": (P, [I, I, I]),
+    "jllm_hip_fp16_to_int8": (I, [P, P, P, I, I, P]),
+}
+
+
+class JllmError(RuntimeError):
+    pass
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise JllmError(f"{LIB_PATH} is not built; run genie-ai-runtime_amd/build.py")
+        l = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            if hasattr(l, name):
+                fn = getattr(l, name)
+                fn.restype = res
+                fn.argtypes = args
+        _lib = l
+    return _lib
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return ctypes.c_void_p(stream)
+
+
+def check(status, what):
+    if status != 0:
+        msg = lib().jllm_hip_status_string(status).decode()
+        raise JllmError(f"{what}: {msg} ({status})")
+
+
+def call(name, *args, stream=None):
+    conv = []
+    for a in args:
+        if hasattr(a, "data_ptr"):
+            conv.append(_ptr(a))
+        else:
+            conv.append(a)
+    st = getattr(lib(), name)(*conv, _stream(stream))
+    check(st, name)
+
+
+# convenience wrappers (tensor arguments)
+def gemv_quant(y, W, t, x, M, K, stream=None):
+    call("jllm_hip_gemv_quant", y, W, t, x, M, K, stream=stream)
+
+
+def gemv_quant_f32(y, W, t, x, M, K, stream=None):
+    call("jllm_hip_gemv_quant_f32", y, W, t, x, M, K, stream=stream)
+
+
+def gemv_quant_dequant_f32(y, W, t, x, M, K, stream=None):
+    call("jllm_hip_gemv_quant_dequant_f32", y, W, t, x, M, K, stream=stream)
+
+
+def gemv_quant_add(y, W, t, x, res, M, K, stream=None):
+    call("jllm_hip_gemv_quant_add", y, W, t, x, res, M, K, stream=stream)
+
+
+def gemv_quant_pair(y0, W0, t0, M0, y1, W1, t1, M1, x, K, stream=None):
+    call("jllm_hip_gemv_quant_pair", y0, W0, t0, M0, y1, W1, t1, M1, x, K, stream=stream)
+
+
+def gemv_quant_triple(y0, W0, t0, M0, y1, W1, t1, M1, y2, W2, t2, M2, x, K, stream=None):
+    call("jllm_hip_gemv_quant_triple", y0, W0, t0, M0, y1, W1, t1, M1, y2, W2, t2, M2, x, K, stream=stream)
+
+
+def quantize_q8_1(x, y, K, stream=None):
+    call("jllm_hip_quantize_q8_1", x, y, K, stream=stream)

@@ -1,0 +1,146 @@
+"""ctypes wrapper of oracle/liboracle.so -- TEST INFRASTRUCTURE ONLY.
+
+The CPU restatement of the reference algorithms (kquant_oracle.c).  Only
+tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use it,
+and only as the checker / reported CPU baseline, never as a product path.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE, "-B", "liboracle.so"], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(LIB_PATH)
+        P, I, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+        sig = {
+            "orc_f16_to_f32": (F, [ctypes.c_uint16]),
+            "orc_f32_to_f16": (ctypes.c_uint16, [F]),
+            "orc_dequant_q4k": (None, [P, P, ctypes.c_int64]),
+            "orc_dequant_q6k": (None, [P, P, ctypes.c_int64]),
+            "orc_gemv_quant_cpu": (I, [P, P, I, P, I, I]),
+            "orc_gemv_quant_cpu_mt": (I, [P, P, I, P, I, I, I]),
+            "orc_quantize_q8_1": (None, [P, P, I]),
+            "orc_quantize_mmq": (None, [P, P, I, I, I, I]),
+            "orc_mmvq": (None, [P, P, I, P, I, I]),
+            "orc_mmq_subdots": (None, [P, P, I, P, I, I, I, I]),
+            "orc_mmq_q4k": (None, [P, P, P, I, I, I, I]),
+            "orc_mmq_q6k": (None, [P, P, P, I, I, I, I]),
+            "orc_fp16_to_int8": (None, [P, P, P, I, I]),
+            "orc_decode_attn_splits": (I, [I]),
+            "orc_attn_decode_int8": (None, [P, P, P, P, I, I, I, I, I, F, P, P, I, I]),
+        }
+        for n, (r, a) in sig.items():
+            f = getattr(_lib, n)
+            f.restype, f.argtypes = r, a
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+
+def _c(a, dtype):
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a
+
+
+def f32_to_f16_bits(f):
+    return lib().orc_f32_to_f16(float(f))
+
+
+def f16_bits_to_f32(h):
+    return lib().orc_f16_to_f32(int(h))
+
+
+def dequant(W, ggml_type, rows, K):
+    W = _c(W, np.uint8)
+    out = np.empty((rows, K), dtype=np.float32)
+    fn = lib().orc_dequant_q4k if ggml_type == 12 else lib().orc_dequant_q6k
+    fn(_p(out), _p(W), rows * (K // 256))
+    return out
+
+
+def gemv_quant_cpu(W, ggml_type, x, M, K, threads=1):
+    W, x = _c(W, np.uint8), _c(x, np.uint16)
+    y = np.empty(M, dtype=np.float32)
+    if threads == 1:
+        st = lib().orc_gemv_quant_cpu(_p(y), _p(W), ggml_type, _p(x), M, K)
+    else:
+        st = lib().orc_gemv_quant_cpu_mt(_p(y), _p(W), ggml_type, _p(x), M, K, threads)
+    if st != 0:
+        raise ValueError(f"unsupported ggml type {ggml_type}")
+    return y
+
+
+def quantize_q8_1(x, K):
+    x = _c(x, np.uint16)
+    y = np.zeros(K // 32 * 36, dtype=np.uint8)
+    lib().orc_quantize_q8_1(_p(x), _p(y), K)
+    return y
+
+
+def quantize_mmq(x, N, K, Npad, ds4):
+    x = _c(x, np.uint16)
+    y = np.zeros((K // 128) * Npad * 144, dtype=np.uint8)
+    lib().orc_quantize_mmq(_p(x), _p(y), N, K, Npad, 1 if ds4 else 0)
+    return y
+
+
+def mmvq(W, ggml_type, xq, M, K):
+    W, xq = _c(W, np.uint8), _c(xq, np.uint8)
+    y = np.empty(M, dtype=np.float32)
+    lib().orc_mmvq(_p(y), _p(W), ggml_type, _p(xq), M, K)
+    return y
+
+
+def mmq_subdots(W, ggml_type, q8, M, N, K, Npad):
+    W, q8 = _c(W, np.uint8), _c(q8, np.uint8)
+    G = 32 if ggml_type == 12 else 16
+    out = np.empty((N, M, K // G), dtype=np.int32)
+    lib().orc_mmq_subdots(_p(out), _p(W), ggml_type, _p(q8), M, N, K, Npad)
+    return out
+
+
+def mmq(W, ggml_type, q8, M, N, K, Npad):
+    W, q8 = _c(W, np.uint8), _c(q8, np.uint8)
+    y = np.empty((N, M), dtype=np.float32)
+    fn = lib().orc_mmq_q4k if ggml_type == 12 else lib().orc_mmq_q6k
+    fn(_p(y), _p(W), _p(q8), M, N, K, Npad)
+    return y
+
+
+def fp16_to_int8(src, rows, cols):
+    src = _c(src, np.uint16)
+    dst = np.empty((rows, cols), dtype=np.int8)
+    sc = np.empty(rows, dtype=np.float32)
+    lib().orc_fp16_to_int8(_p(dst), _p(sc), _p(src), rows, cols)
+    return dst, sc
+
+
+def decode_attn_splits(seq):
+    return lib().orc_decode_attn_splits(seq)
+
+
+def attn_decode_int8(q, k, v, n_heads, n_kv, hd, chd, seq, scale, ks, vs, window, n_splits):
+    q, k, v = _c(q, np.uint16), _c(k, np.int8), _c(v, np.int8)
+    ks = _c(ks, np.float32) if ks is not None else None
+    vs = _c(vs, np.float32) if vs is not None else None
+    out = np.empty(n_heads * hd, dtype=np.uint16)
+    lib().orc_attn_decode_int8(_p(out), _p(q), _p(k), _p(v), n_heads, n_kv, hd, chd, seq, float(scale),
+                               _p(ks), _p(vs), window, n_splits)
+    return out

@@ -1,0 +1,142 @@
+"""GPU parity of the GEMV family (through the C ABI) against the CPU oracle.
+
+Tolerance: rel_inf = max|y - y_oracle| / max|y_oracle| <= 1e-3 for fp32
+outputs; fp16 outputs are compared after the oracle result is rounded to
+fp16 with the same bound plus one fp16 ulp.  The activation quantiser is
+compared bit-exactly.
+"""
+import numpy as np
+import pytest
+import torch
+
+import jllm
+import oracle
+import synth
+from gpu_util import empty_f16, empty_f32, f16_to_f64, from_dev, print_case, rel_inf, to_dev
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+SHAPES = [  # (rows, K) -- BASELINE config 1/2 shapes, trimmed rows, plus odd row counts
+    (9728, 2560), (4096, 2560), (1024, 2560), (2560, 4096), (2560, 9728), (37, 256), (1, 512), (203, 1280),
+]
+
+
+def _case(t, rows, K, seed):
+    g = synth.rng(seed)
+    return synth.weights(g, t, rows, K), synth.x_f16(g, K)
+
+
+def _close_f16(got_bits, want_f32):
+    got = f16_to_f64(got_bits)
+    want = np.asarray(want_f32, np.float64)
+    err = np.abs(got - want)
+    bound = TOL * np.abs(want).max() + np.abs(want) * 2 ** -10
+    return bool(np.all(err <= bound)), float(err.max())
+
+
+@pytest.mark.parametrize("t", [12, 14])
+def test_quantize_q8_1_bit_exact(dev, t):
+    for K in (256, 2560, 9728):
+        print_case("q8_1", K)
+        x = synth.x_f16(synth.rng(K), K)
+        x[:32] = 0                                  # an all-zero block
+        xd = to_dev(x)
+        y = torch.zeros(K // 32 * 36, dtype=torch.uint8, device=dev)
+        jllm.quantize_q8_1(xd, y, K)
+        assert np.array_equal(from_dev(y), oracle.quantize_q8_1(x, K))
+
+
+@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("rows,K", SHAPES)
+def test_gemv_dequant_f32_vs_host_scalar(dev, t, rows, K):
+    """float-dequant fp32 GEMV vs gemv_quant_cpu (the reference host path)."""
+    print_case("dequant_f32", t, rows, K)
+    W, x = _case(t, rows, K, 100 + rows)
+    y = empty_f32(rows)
+    jllm.gemv_quant_dequant_f32(y, to_dev(W), t, to_dev(x), rows, K)
+    want = oracle.gemv_quant_cpu(W, t, x, rows, K)
+    assert rel_inf(from_dev(y), want) <= TOL
+
+
+@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("rows,K", SHAPES)
+def test_gemv_f32(dev, t, rows, K):
+    """gemv_quant_f32: Q4_K via MMVQ (oracle mmvq), Q6_K via float dequant."""
+    print_case("gemv_f32", t, rows, K)
+    W, x = _case(t, rows, K, 200 + rows)
+    y = empty_f32(rows)
+    jllm.gemv_quant_f32(y, to_dev(W), t, to_dev(x), rows, K)
+    if t == 12:
+        want = oracle.mmvq(W, t, oracle.quantize_q8_1(x, K), rows, K)
+    else:
+        want = oracle.gemv_quant_cpu(W, t, x, rows, K)
+    assert rel_inf(from_dev(y), want) <= TOL
+
+
+@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("rows,K", SHAPES)
+def test_gemv_half_mmvq(dev, t, rows, K):
+    print_case("gemv_half", t, rows, K)
+    W, x = _case(t, rows, K, 300 + rows)
+    y = empty_f16(rows)
+    jllm.gemv_quant(y, to_dev(W), t, to_dev(x), rows, K)
+    want = oracle.mmvq(W, t, oracle.quantize_q8_1(x, K), rows, K)
+    ok, err = _close_f16(from_dev(y, np.uint16), want)
+    assert ok, err
+
+
+@pytest.mark.parametrize("t", [12, 14])
+def test_gemv_add(dev, t):
+    rows, K = 2560, 4096 if t == 12 else 9728
+    print_case("gemv_add", t, rows, K)
+    W, x = _case(t, rows, K, 400)
+    res = synth.x_f16(synth.rng(401), rows)
+    y = empty_f16(rows)
+    jllm.gemv_quant_add(y, to_dev(W), t, to_dev(x), to_dev(res), rows, K)
+    proj = oracle.gemv_quant_cpu(W, t, x, rows, K).astype(np.float16).astype(np.float32)
+    want = proj + f16_to_f64(res).astype(np.float32)
+    ok, err = _close_f16(from_dev(y, np.uint16), want)
+    assert ok, err
+
+
+def test_gemv_pair_and_triple(dev):
+    K = 2560
+    g = synth.rng(500)
+    x = synth.x_f16(g, K)
+    Wg, Wu = synth.q4k(g, 9728, K), synth.q4k(g, 9728, K)
+    xq = oracle.quantize_q8_1(x, K)
+    y0, y1 = empty_f16(9728), empty_f16(9728)
+    print_case("pair q4k/q4k")
+    jllm.gemv_quant_pair(y0, to_dev(Wg), 12, 9728, y1, to_dev(Wu), 12, 9728, to_dev(x), K)
+    for y, W in ((y0, Wg), (y1, Wu)):
+        ok, err = _close_f16(from_dev(y, np.uint16), oracle.mmvq(W, 12, xq, 9728, K))
+        assert ok, err
+    # mixed pair -> float dequant
+    Wm = synth.q6k(g, 1000, K)
+    print_case("pair q4k/q6k")
+    y2 = empty_f16(1000)
+    jllm.gemv_quant_pair(y0, to_dev(Wg), 12, 9728, y2, to_dev(Wm), 14, 1000, to_dev(x), K)
+    ok, err = _close_f16(from_dev(y2, np.uint16), oracle.gemv_quant_cpu(Wm, 14, x, 1000, K))
+    assert ok, err
+    # QKV triple, Q4_K / Q4_K / Q6_K (Qwen3 Q4_K_M layout)
+    Wq, Wk, Wv = synth.q4k(g, 4096, K), synth.q4k(g, 1024, K), synth.q6k(g, 1024, K)
+    yq, yk, yv = empty_f16(4096), empty_f16(1024), empty_f16(1024)
+    print_case("triple q4k/q4k/q6k")
+    jllm.gemv_quant_triple(yq, to_dev(Wq), 12, 4096, yk, to_dev(Wk), 12, 1024, yv, to_dev(Wv), 14, 1024, to_dev(x), K)
+    for y, W, t, M in ((yq, Wq, 12, 4096), (yk, Wk, 12, 1024), (yv, Wv, 14, 1024)):
+        ok, err = _close_f16(from_dev(y, np.uint16), oracle.mmvq(W, t, xq, M, K))
+        assert ok, (t, M, err)
+
+
+def test_gemv_errors(dev):
+    x = to_dev(synth.x_f16(synth.rng(1), 512))
+    W = to_dev(synth.q4k(synth.rng(2), 4, 512))
+    y = empty_f16(4)
+    with pytest.raises(jllm.JllmError, match="unsupported"):
+        jllm.gemv_quant(y, W, 13, x, 4, 512)
+    with pytest.raises(jllm.JllmError, match="invalid"):
+        jllm.gemv_quant(y, W, 12, x, 4, 300)
+    host = torch.zeros(4 * 2 * 144, dtype=torch.uint8)           # plain host memory: no fallback
+    with pytest.raises(jllm.JllmError, match="visible"):
+        jllm.gemv_quant(y, host, 12, x, 4, 512)
