@@ -38,19 +38,24 @@ def _compile(src):
     return obj
 
 
-def build(jobs=None):
+def build(jobs=None, extra_flags=(), lib_path=None, obj_dir=None):
+    global OBJ
+    if obj_dir:
+        OBJ = obj_dir
+    FLAGS.extend(extra_flags)
     os.makedirs(OBJ, exist_ok=True)
     srcs = _sources()
     jobs = jobs or min(len(srcs), int(os.environ.get("MAX_JOBS", "8")))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile, srcs))
-    tmp = LIB + ".tmp"
+    lib = lib_path or LIB
+    tmp = lib + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stderr)
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":

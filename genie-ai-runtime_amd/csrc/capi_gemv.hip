@@ -104,7 +104,7 @@ int lpr_override() {
     static const int v = [] {
         const char* e = getenv("JLLM_GEMV_LPR");
         int r = e ? atoi(e) : 0;
-        return (r == 8 || r == 16 || r == 32 || r == 64) ? r : 0;
+        return (r == 4 || r == 8 || r == 16 || r == 32 || r == 64) ? r : 0;
     }();
     return v;
 }

@@ -23,7 +23,11 @@ struct GemvArgs {
     int nseg;
     int K;
     const uint16_t* x;     // fp16 activation [K]
-    int total_rows;        // filled by gemv_launch
+    int lpr;               // lanes per row (filled by gemv_launch)
+    int gend[3];           // cumulative row-group ends per segment (filled by gemv_launch)
+    int per_q;             // blocks per quad and row (filled by gemv_launch)
+    int g_split;           // row groups of Q4_K segments (filled by gemv_launch)
+    int wg_split;          // workgroups serving Q4_K (filled by gemv_launch)
 };
 
 size_t gemv_lds_bytes(bool mmvq, int K);

@@ -9,7 +9,7 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libjllm_hip.so")
+LIB_PATH = os.environ.get("JLLM_HIP_LIB") or os.path.join(HERE, "libjllm_hip.so")
 
 _lib = None
 P = ctypes.c_void_p
