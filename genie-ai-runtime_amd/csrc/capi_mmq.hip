@@ -1,0 +1,84 @@
+// capi_mmq.hip -- C ABI for the batched (prefill) GEMM: activation
+// quantiser, int8 MFMA MMQ, and the routing of gemm_quant_batched
+// (gemv_q4.cu:2478-2517).
+#include "capi_common.h"
+#include "mmq.h"
+
+using namespace jllm_hip;
+
+namespace {
+DeviceScratch g_q8;     // q8 activations [K/128][Npad] x 144 B, grown on demand, never freed
+
+int npad_of(int N) { return ((N + MMQ_TILE_N - 1) / MMQ_TILE_N) * MMQ_TILE_N; }
+
+int check_gemm(const char* tag, const void* y, int type, const uint16_t* x, int M, int N, int K) {
+    if (type != 12 && type != 14) {
+        fprintf(stderr, "[%s] FATAL: unsupported GPU GGML type %d\n", tag, type);
+        return JLLM_ERR_UNSUPPORTED;
+    }
+    if (M < 0 || N < 0 || K <= 0 || K % 256 != 0) {
+        fprintf(stderr, "[%s] bad shape M=%d N=%d K=%d (K must be a positive multiple of 256)\n", tag, M, N, K);
+        return JLLM_ERR_INVALID;
+    }
+    if ((M > 0 && N > 0) && (!y || !x || !aligned16(x))) {
+        fprintf(stderr, "[%s] output and 16-byte aligned activation pointers are required\n", tag);
+        return JLLM_ERR_INVALID;
+    }
+    return JLLM_OK;
+}
+
+int run_mmq(const char* tag, void* y, const void* W, int type, const uint16_t* x, int M, int N, int K,
+            int out_kind, void* stream) {
+    const void* Wd = resolve_weight(W);
+    if (!Wd) {
+        fprintf(stderr, "[%s] weight pointer %p is not device-visible (no host fallback)\n", tag, W);
+        return JLLM_ERR_POINTER;
+    }
+    if (!aligned16(Wd)) return JLLM_ERR_INVALID;
+    const int Npad = npad_of(N);
+    void* q8 = g_q8.get((size_t)(K / 128) * Npad * 144);
+    if (!q8) {
+        fprintf(stderr, "[%s] q8 scratch allocation failed\n", tag);
+        return JLLM_ERR_NOMEM;
+    }
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e = quantize_mmq_launch(x, q8, N, K, Npad, type == 12, st);
+    if (e == hipSuccess) e = mmq_launch(y, (const uint8_t*)Wd, type, q8, M, N, K, Npad, out_kind, st);
+    return launch_status(e, tag);
+}
+}  // namespace
+
+extern "C" {
+
+int jllm_hip_gemm_quant_batched(uint16_t* y, const void* W, int type, const uint16_t* x,
+                                int M, int N, int K, void* stream) {
+    int st = check_gemm("GEMM", y, type, x, M, N, K); if (st) return st;
+    if (M == 0 || N == 0) return JLLM_OK;
+    if (N == 1) return jllm_hip_gemv_quant(y, W, type, x, M, K, stream);
+    return run_mmq("GEMM", y, W, type, x, M, N, K, 0, stream);
+}
+
+int jllm_hip_gemm_quant_batched_f32(float* y, const void* W, int type, const uint16_t* x,
+                                    int M, int N, int K, void* stream) {
+    int st = check_gemm("GEMM", y, type, x, M, N, K); if (st) return st;
+    if (M == 0 || N == 0) return JLLM_OK;
+    return run_mmq("GEMM", y, W, type, x, M, N, K, 1, stream);
+}
+
+int jllm_hip_quantize_mmq_q8_1(const uint16_t* x, void* q8, int N, int K, int Npad, int ds4, void* stream) {
+    if (!x || !q8 || N < 0 || K <= 0 || K % 128 != 0 || Npad < N || Npad % MMQ_TILE_N != 0) return JLLM_ERR_INVALID;
+    if (Npad == 0) return JLLM_OK;
+    return launch_status(quantize_mmq_launch(x, q8, N, K, Npad, ds4 != 0, (hipStream_t)stream), "GEMM");
+}
+
+int jllm_hip_mmq_subdots(int32_t* out, const void* W, int type, const void* q8, int M, int N, int K, int Npad,
+                         void* stream) {
+    if (type != 12 && type != 14) return JLLM_ERR_UNSUPPORTED;
+    if (!out || !q8 || M <= 0 || N <= 0 || K <= 0 || K % 256 != 0 || Npad < N || Npad % MMQ_TILE_N != 0)
+        return JLLM_ERR_INVALID;
+    const void* Wd = resolve_weight(W);
+    if (!Wd) return JLLM_ERR_POINTER;
+    return launch_status(mmq_launch(out, (const uint8_t*)Wd, type, q8, M, N, K, Npad, 2, (hipStream_t)stream), "GEMM");
+}
+
+}  // extern "C"

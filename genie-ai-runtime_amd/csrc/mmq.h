@@ -1,0 +1,20 @@
+// mmq.h -- internal interface of the gfx950 int8 MFMA prefill GEMM (MMQ).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+namespace jllm_hip {
+
+constexpr int MMQ_TILE_N = 64;    // tokens per workgroup tile (and Npad granularity)
+
+// activation quantiser: x [N x K] fp16 -> [K/128][Npad] blocks of 144 B
+// (ds4 = 1: half2 (d, sum x) per 32; ds4 = 0: float d per 32)
+hipError_t quantize_mmq_launch(const uint16_t* x, void* q8, int N, int K, int Npad, bool ds4, hipStream_t st);
+
+// out_kind: 0 = fp16 y[N x M], 1 = fp32 y[N x M], 2 = raw int32 sub-block
+// dots [N][M][K/G] (G = 32 for Q4_K, 16 for Q6_K)
+hipError_t mmq_launch(void* y, const uint8_t* W, int type, const void* q8, int M, int N, int K, int Npad,
+                      int out_kind, hipStream_t st);
+
+}  // namespace jllm_hip

@@ -80,6 +80,37 @@ int jllm_hip_gemv_quant_dequant_f32(float* y, const void* W, int ggml_type, cons
  * (36 B per 32 values).  Replaces quantize_q8_1, gemv_q4.cu:468. */
 int jllm_hip_quantize_q8_1(const uint16_t* x, void* y, int K, void* stream);
 
+/* Batched GEMM y[N x M] (fp16, token-major) = x[N x K] . W^T.  N == 1 routes
+ * to jllm_hip_gemv_quant; otherwise the activation is quantised to q8_1 and
+ * multiplied with int8 matrix cores (Q4_K: DS4 layout, exact int32 dot per
+ * 32-weight sub-block; Q6_K: D4 layout, per 16-weight group).  Uses a
+ * library-owned q8 scratch buffer (grown on demand, never freed); calls on
+ * one device must be serialised (one stream), as in the reference.
+ * Replaces gemm_quant_batched, jllm_kernels.h:135 (gemv_q4.cu:2478-2517),
+ * and the internal gemm_q4k_mmq_llama / gemm_q6k_mmq_llama
+ * (mmq_q4k_llama.cu:479, mmq_q6k_llama.cu:497). */
+int jllm_hip_gemm_quant_batched(uint16_t* y, const void* W, int ggml_type, const uint16_t* x,
+                                int M, int N, int K, void* stream);
+
+/* Same computation with fp32 output (no fp16 rounding of y).  No reference
+ * counterpart (the reference writes fp16); for callers that keep fp32. */
+int jllm_hip_gemm_quant_batched_f32(float* y, const void* W, int ggml_type, const uint16_t* x,
+                                    int M, int N, int K, void* stream);
+
+/* The MMQ activation quantiser on its own: x [N x K] fp16 -> q8 [K/128][Npad]
+ * blocks of 144 B.  ds4 != 0: DS4 layout {half2 (d, sum x)[4], i8 qs[128]}
+ * (quantize_mmq_q8_1_ds4, mmq_q4k_llama.cu:383); ds4 == 0: D4 layout
+ * {float d[4], i8 qs[128]} (quantize_mmq_q8_1_d4, mmq_q6k_llama.cu:424).
+ * Npad is a multiple of 64 and >= N; columns >= N are written as zeros. */
+int jllm_hip_quantize_mmq_q8_1(const uint16_t* x, void* q8, int N, int K, int Npad, int ds4, void* stream);
+
+/* Test hook: the raw int32 dots the MMQ kernels compute, out [N][M][K/G]
+ * (G = 32 for Q4_K sub-blocks, 16 for Q6_K groups), from a q8 buffer made by
+ * jllm_hip_quantize_mmq_q8_1.  No reference counterpart (the reference keeps
+ * these in registers); exists so the int32 dots can be checked bit-exactly. */
+int jllm_hip_mmq_subdots(int32_t* out, const void* W, int ggml_type, const void* q8,
+                         int M, int N, int K, int Npad, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

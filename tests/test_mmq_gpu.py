@@ -1,0 +1,103 @@
+"""GPU parity of the prefill path: MMQ activation quantiser (bit-exact), the
+int32 sub-block dots of the int8 MFMA kernels (bit-exact) and the fp32 /
+fp16 GEMM outputs (rel_inf <= 1e-3 against the CPU oracle; BASELINE
+config 3 shapes are checked on a sampled row subset at full token count)."""
+import numpy as np
+import pytest
+import torch
+
+import jllm
+import oracle
+import synth
+from gpu_util import f16_to_f64, from_dev, print_case, rel_inf, to_dev
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _npad(n):
+    return (n + 63) // 64 * 64
+
+
+def _quantize_dev(x, N, K, Npad, ds4, dev):
+    q8 = torch.zeros((K // 128) * Npad * 144, dtype=torch.uint8, device=dev)
+    jllm.call("jllm_hip_quantize_mmq_q8_1", to_dev(x), q8, N, K, Npad, 1 if ds4 else 0)
+    return q8
+
+
+@pytest.mark.parametrize("ds4", [True, False])
+@pytest.mark.parametrize("N,K", [(1, 256), (5, 512), (64, 2560), (100, 2560), (130, 9728)])
+def test_quantize_mmq_bit_exact(dev, ds4, N, K):
+    print_case("quantize_mmq", ds4, N, K)
+    x = synth.x_f16(synth.rng(N * 7 + K), (N, K))
+    x[0, :32] = 0                                        # an all-zero block
+    Npad = _npad(N)
+    got = from_dev(_quantize_dev(x, N, K, Npad, ds4, dev))
+    want = oracle.quantize_mmq(x, N, K, Npad, ds4)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("M,N,K", [(128, 64, 256), (200, 70, 512), (33, 5, 2560)])
+def test_mmq_int32_dots_bit_exact(dev, t, M, N, K):
+    print_case("mmq_subdots", t, M, N, K)
+    g = synth.rng(M + N + K + t)
+    W = synth.weights(g, t, M, K)
+    x = synth.x_f16(g, (N, K))
+    Npad = _npad(N)
+    q8 = _quantize_dev(x, N, K, Npad, t == 12, dev)
+    G = 32 if t == 12 else 16
+    out = torch.zeros(N * M * (K // G), dtype=torch.int32, device=dev)
+    jllm.call("jllm_hip_mmq_subdots", out, to_dev(W), t, q8, M, N, K, Npad)
+    got = from_dev(out).reshape(N, M, K // G)
+    want = oracle.mmq_subdots(W, t, from_dev(q8), M, N, K, Npad)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("M,N,K", [(300, 70, 2560), (128, 64, 1024), (97, 130, 512), (256, 2, 256)])
+def test_mmq_f32_and_f16(dev, t, M, N, K):
+    print_case("mmq", t, M, N, K)
+    g = synth.rng(1000 + M + N + K + t)
+    W = synth.weights(g, t, M, K)
+    x = synth.x_f16(g, (N, K))
+    Wd, xd = to_dev(W), to_dev(x)
+    y32 = torch.empty(N * M, dtype=torch.float32, device=dev)
+    jllm.call("jllm_hip_gemm_quant_batched_f32", y32, Wd, t, xd, M, N, K)
+    want = oracle.mmq(W, t, oracle.quantize_mmq(x, N, K, _npad(N), t == 12), M, N, K, _npad(N))
+    assert rel_inf(from_dev(y32).reshape(N, M), want) <= TOL
+    y16 = torch.empty(N * M, dtype=torch.int16, device=dev)
+    jllm.call("jllm_hip_gemm_quant_batched", y16, Wd, t, xd, M, N, K)
+    got = f16_to_f64(from_dev(y16, np.uint16)).reshape(N, M)
+    err = np.abs(got - want)
+    assert np.all(err <= TOL * np.abs(want).max() + np.abs(want) * 2 ** -10)
+
+
+@pytest.mark.parametrize("t,M,K", [(12, 9728, 2560), (14, 2560, 9728)])
+@pytest.mark.parametrize("N", [64, 512, 1261])
+def test_mmq_baseline_shapes_sampled(dev, t, M, K, N):
+    """full GEMM on the GPU, oracle on 48 sampled rows."""
+    print_case("mmq_full", t, M, N, K)
+    g = synth.rng(2000 + N + t)
+    W = synth.weights(g, t, M, K)
+    x = synth.x_f16(g, (N, K))
+    y32 = torch.empty(N * M, dtype=torch.float32, device=dev)
+    jllm.call("jllm_hip_gemm_quant_batched_f32", y32, to_dev(W), t, to_dev(x), M, N, K)
+    got = from_dev(y32).reshape(N, M)
+    rows = np.sort(g.choice(M, 48, replace=False))
+    rows[-1] = M - 1
+    q8 = oracle.quantize_mmq(x, N, K, _npad(N), t == 12)
+    want = oracle.mmq(W[rows], t, q8, len(rows), N, K, _npad(N))
+    assert rel_inf(got[:, rows], want) <= TOL
+
+
+def test_gemm_n1_routes_to_gemv(dev):
+    K, M = 2560, 512
+    g = synth.rng(3)
+    W = synth.q4k(g, M, K)
+    x = synth.x_f16(g, K)
+    y = torch.empty(M, dtype=torch.int16, device=dev)
+    jllm.call("jllm_hip_gemm_quant_batched", y, to_dev(W), 12, to_dev(x), M, 1, K)
+    want = oracle.mmvq(W, 12, oracle.quantize_q8_1(x, K), M, K)
+    got = f16_to_f64(from_dev(y, np.uint16))
+    assert np.all(np.abs(got - want) <= TOL * np.abs(want).max() + np.abs(want) * 2 ** -10)
