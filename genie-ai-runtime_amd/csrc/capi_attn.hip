@@ -1,0 +1,79 @@
+// capi_attn.hip -- C ABI for decode attention, the split-K partials buffer
+// and the KV quantiser (attention.cu:975-1075, convert.cu:71-75).
+#include "capi_common.h"
+#include "attention.h"
+#include "convert.h"
+
+using namespace jllm_hip;
+
+namespace {
+DeviceScratch g_part;    // split-K partials, grown on demand, never freed
+
+int attn_check(const void* out, const void* q, const void* k, const void* v, int n_heads, int n_kv, int hd,
+               int chd, int seq, int kv_int8, int window) {
+    if (!out || !q || (seq > 0 && (!k || !v))) return JLLM_ERR_INVALID;
+    if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0 || n_heads / n_kv > 16) {
+        fprintf(stderr, "[attention] n_heads=%d n_kv_heads=%d: need n_heads %% n_kv == 0 and <= 16 q heads per kv head\n", n_heads, n_kv);
+        return JLLM_ERR_INVALID;
+    }
+    if (hd <= 0 || hd % 32 != 0 || hd > 128 || chd < hd || seq < 0 || window < 0) {
+        fprintf(stderr, "[attention] head_dim=%d cache_head_dim=%d: need head_dim %% 32 == 0, <= 128, cache_head_dim >= head_dim\n", hd, chd);
+        return JLLM_ERR_INVALID;
+    }
+    const int eb = kv_int8 ? 1 : 2;
+    if ((chd * eb) % 16 != 0 || !aligned16(k) || !aligned16(v) || !aligned16(q)) {
+        fprintf(stderr, "[attention] KV rows and q must be 16-byte aligned\n");
+        return JLLM_ERR_INVALID;
+    }
+    return JLLM_OK;
+}
+
+int attn_run(uint16_t* out, const uint16_t* q, const void* k, const void* v, int n_heads, int n_kv, int hd, int chd,
+             int seq, float scale, int kv_int8, const float* ks, const float* vs, int window, int n_splits,
+             void* stream) {
+    int st = attn_check(out, q, k, v, n_heads, n_kv, hd, chd, seq, kv_int8, window);
+    if (st) return st;
+    if (n_splits < 1) n_splits = 1;
+    if (n_splits > 64) n_splits = 64;
+    float* part = (float*)g_part.get(attn_partials_floats(n_heads, n_splits, hd) * sizeof(float));
+    if (!part) return JLLM_ERR_NOMEM;
+    AttnArgs a;
+    a.out = out; a.q = q; a.k = k; a.v = v; a.ks = ks; a.vs = vs; a.part = part;
+    a.n_heads = n_heads; a.n_kv = n_kv; a.head_dim = hd; a.cache_head_dim = chd;
+    a.seq = seq; a.window = window; a.n_splits = n_splits; a.scale = scale;
+    return launch_status(attn_launch(a, kv_int8 != 0, (hipStream_t)stream), "attention");
+}
+}  // namespace
+
+extern "C" {
+
+int jllm_hip_decode_attn_splits(int seq_len) { return attn_splits(seq_len, 8); }
+
+float* jllm_hip_get_splitk_partials(int n_heads, int n_splits, int head_dim) {
+    if (n_heads <= 0 || n_splits <= 0 || head_dim <= 0) return nullptr;
+    return (float*)g_part.get(attn_partials_floats(n_heads, n_splits, head_dim) * sizeof(float));
+}
+
+int jllm_hip_flash_attention_decode(uint16_t* out, const uint16_t* q, const void* k, const void* v,
+                                    int n_heads, int n_kv_heads, int head_dim, int cache_head_dim, int seq_len,
+                                    float scale, int kv_int8, const float* k_scales, const float* v_scales,
+                                    int window, void* stream) {
+    return attn_run(out, q, k, v, n_heads, n_kv_heads, head_dim, cache_head_dim, seq_len, scale, kv_int8,
+                    k_scales, v_scales, window, attn_splits(seq_len, n_kv_heads), stream);
+}
+
+int jllm_hip_flash_attention_decode_splits(uint16_t* out, const uint16_t* q, const void* k, const void* v,
+                                           int n_heads, int n_kv_heads, int head_dim, int cache_head_dim,
+                                           int seq_len, float scale, int kv_int8, const float* k_scales,
+                                           const float* v_scales, int window, int n_splits, void* stream) {
+    return attn_run(out, q, k, v, n_heads, n_kv_heads, head_dim, cache_head_dim, seq_len, scale, kv_int8,
+                    k_scales, v_scales, window, n_splits, stream);
+}
+
+int jllm_hip_fp16_to_int8(int8_t* dst, float* scale_out, const uint16_t* src, int rows, int cols, void* stream) {
+    if (rows < 0 || cols <= 0 || (rows > 0 && (!dst || !src))) return JLLM_ERR_INVALID;
+    if (rows == 0) return JLLM_OK;
+    return launch_status(fp16_to_int8_launch(dst, scale_out, src, rows, cols, (hipStream_t)stream), "convert");
+}
+
+}  // extern "C"

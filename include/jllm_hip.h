@@ -111,6 +111,43 @@ int jllm_hip_quantize_mmq_q8_1(const uint16_t* x, void* q8, int N, int K, int Np
 int jllm_hip_mmq_subdots(int32_t* out, const void* W, int ggml_type, const void* q8,
                          int M, int N, int K, int Npad, void* stream);
 
+/* Single-query (decode) attention over an INT8 (kv_int8 != 0) or FP16 KV
+ * cache, split-K: the keys are cut into slices processed in parallel, each
+ * with an online softmax, then combined.  Layouts: q and out fp16
+ * [n_heads x head_dim]; k/v [seq][n_kv_heads * cache_head_dim] (int8 or
+ * fp16); k_scales/v_scales fp32 [seq][n_kv_heads] (INT8 only; NULL = 1.0).
+ * window > 0 attends to the last `window` keys only.  head_dim is a multiple
+ * of 32 and <= 128; n_heads/n_kv_heads <= 16.  Uses the library's partials
+ * buffer (see jllm_hip_get_splitk_partials).
+ * Replaces flash_attention_decode, jllm_kernels.h:323 (attention.cu:1036-1075,
+ * kernels :837-969). */
+int jllm_hip_flash_attention_decode(uint16_t* out, const uint16_t* q, const void* k, const void* v,
+                                    int n_heads, int n_kv_heads, int head_dim, int cache_head_dim, int seq_len,
+                                    float scale, int kv_int8, const float* k_scales, const float* v_scales,
+                                    int window, void* stream);
+
+/* Same with an explicit split count (1..64) instead of the policy of
+ * jllm_hip_decode_attn_splits.  Replaces the n_splits argument of
+ * flash_attention_decode_dyn, jllm_kernels.h:380 (attention.cu:1007-1034). */
+int jllm_hip_flash_attention_decode_splits(uint16_t* out, const uint16_t* q, const void* k, const void* v,
+                                           int n_heads, int n_kv_heads, int head_dim, int cache_head_dim,
+                                           int seq_len, float scale, int kv_int8, const float* k_scales,
+                                           const float* v_scales, int window, int n_splits, void* stream);
+
+/* Split-count policy and partials buffer.  Replace decode_attn_splits and
+ * get_splitk_partials, jllm_kernels.h:402-403 (attention.cu:975-1005).  The
+ * MI355X policy is ceil(seq/64) splits capped at 32 (so 8 KV heads fill 256
+ * CUs), not the reference's 1/4/8.  The buffer (floats: m[H*S] | l[H*S] |
+ * acc[H*S*head_dim]) is allocated on first use and never freed; call
+ * jllm_hip_get_splitk_partials before graph capture.  NULL on failure. */
+int    jllm_hip_decode_attn_splits(int seq_len);
+float* jllm_hip_get_splitk_partials(int n_heads, int n_splits, int head_dim);
+
+/* Per-row fp16 -> int8 quantiser for the KV cache: scale_out[r] =
+ * absmax/127, q = rn(v * 127/absmax) clamped to +-127.  Replaces
+ * fp16_to_int8, jllm_kernels.h:413 (convert.cu:26-75). */
+int jllm_hip_fp16_to_int8(int8_t* dst, float* scale_out, const uint16_t* src, int rows, int cols, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
