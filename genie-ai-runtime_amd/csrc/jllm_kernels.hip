@@ -1,0 +1,116 @@
+// jllm_kernels.hip -- the namespace jllm C++ entry points (the reference's
+// include/jllm_kernels.h signatures) as thin forwards to the C ABI.
+#include "jllm_kernels.h"
+#include "jllm_hip.h"
+#include "kq_common.h"
+#include <cstdio>
+
+namespace {
+
+__global__ void zero_fill_kernel(uint16_t* p, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
+// zero `bytes` (a multiple of 2) at p on the stream, with a kernel (no memset
+// node, so a captured graph replays it correctly)
+void zero_fill(void* p, size_t bytes, hipStream_t st) {
+    const size_t n = bytes / 2;
+    if (!p || n == 0) return;
+    const size_t blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
+    hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (uint16_t*)p, n);
+}
+
+void report(int st, const char* fn, void* out, size_t bytes, hipStream_t stream) {
+    if (st == JLLM_OK) return;
+    fprintf(stderr, "[jllm] %s failed: %s; output zero-filled\n", fn, jllm_hip_status_string(st));
+    zero_fill(out, bytes, stream);
+}
+
+inline const uint16_t* H(const half* p) { return reinterpret_cast<const uint16_t*>(p); }
+inline uint16_t* H(half* p) { return reinterpret_cast<uint16_t*>(p); }
+
+}  // namespace
+
+namespace jllm {
+
+const void* resolve_mapped_weight_device_ptr(const void* host_ptr) {
+    return jllm_hip_resolve_mapped_weight_device_ptr(host_ptr);
+}
+void register_mapped_weight_region(const void* host_base, const void* device_base, int64_t bytes) {
+    (void)jllm_hip_register_mapped_weight_region(host_base, device_base, bytes);
+}
+void clear_mapped_weight_region(const void* host_base) { jllm_hip_clear_mapped_weight_region(host_base); }
+
+void gemv_q4(half* y, const void* W_q4, const half*, const half* x, int M, int K, int, hipStream_t stream) {
+    gemv_quant(y, W_q4, 12, x, M, K, stream);
+}
+
+void gemv_quant(half* y, const void* W, int type, const half* x, int M, int K, hipStream_t stream) {
+    report(jllm_hip_gemv_quant(H(y), W, type, H(x), M, K, stream), "gemv_quant", y, (size_t)M * 2, stream);
+}
+
+void gemv_quant_add(half* y, const void* W, int type, const half* x, const half* residual, int M, int K,
+                    hipStream_t stream) {
+    report(jllm_hip_gemv_quant_add(H(y), W, type, H(x), H(residual), M, K, stream), "gemv_quant_add", y,
+           (size_t)M * 2, stream);
+}
+
+void gemv_quant_pair(half* y0, const void* W0, int t0, int M0, half* y1, const void* W1, int t1, int M1,
+                     const half* x, int K, hipStream_t stream) {
+    const int st = jllm_hip_gemv_quant_pair(H(y0), W0, t0, M0, H(y1), W1, t1, M1, H(x), K, stream);
+    report(st, "gemv_quant_pair", y0, (size_t)M0 * 2, stream);
+    if (st) zero_fill(y1, (size_t)M1 * 2, stream);
+}
+
+void gemv_quant_triple(half* y0, const void* W0, int t0, int M0, half* y1, const void* W1, int t1, int M1,
+                       half* y2, const void* W2, int t2, int M2, const half* x, int K, hipStream_t stream) {
+    const int st = jllm_hip_gemv_quant_triple(H(y0), W0, t0, M0, H(y1), W1, t1, M1, H(y2), W2, t2, M2, H(x), K,
+                                              stream);
+    report(st, "gemv_quant_triple", y0, (size_t)M0 * 2, stream);
+    if (st) { zero_fill(y1, (size_t)M1 * 2, stream); zero_fill(y2, (size_t)M2 * 2, stream); }
+}
+
+void gemv_quant_f32(float* y, const void* W, int type, const half* x, int M, int K, hipStream_t stream) {
+    report(jllm_hip_gemv_quant_f32(y, W, type, H(x), M, K, stream), "gemv_quant_f32", y, (size_t)M * 4, stream);
+}
+
+void gemm_quant_batched(half* y, const void* W, int type, const half* x, int M, int N, int K, hipStream_t stream) {
+    report(jllm_hip_gemm_quant_batched(H(y), W, type, H(x), M, N, K, stream), "gemm_quant_batched", y,
+           (size_t)M * (N > 0 ? N : 0) * 2, stream);
+}
+
+void quantize_q8_1(const half* x, void* y, int K, hipStream_t stream) {
+    report(jllm_hip_quantize_q8_1(H(x), y, K, stream), "quantize_q8_1", y, (size_t)(K / 32) * 36, stream);
+}
+
+void gemm_q4k_mmq_llama(half* y, const void* W, const half* x, int M, int N, int K, hipStream_t stream) {
+    gemm_quant_batched(y, W, 12, x, M, N, K, stream);
+}
+
+void gemm_q6k_mmq_llama(half* y, const void* W, const half* x, int M, int N, int K, hipStream_t stream) {
+    gemm_quant_batched(y, W, 14, x, M, N, K, stream);
+}
+
+void flash_attention_decode(half* output, const half* q, const void* k_cache, const void* v_cache, int n_heads,
+                            int n_kv_heads, int head_dim, int cache_head_dim, int seq_len, float scale,
+                            bool kv_int8, const float* k_scales, const float* v_scales, int window,
+                            hipStream_t stream) {
+    report(jllm_hip_flash_attention_decode(H(output), H(q), k_cache, v_cache, n_heads, n_kv_heads, head_dim,
+                                           cache_head_dim, seq_len, scale, kv_int8 ? 1 : 0, k_scales, v_scales,
+                                           window, stream),
+           "flash_attention_decode", output, (size_t)n_heads * head_dim * 2, stream);
+}
+
+int decode_attn_splits(int seq_len) { return jllm_hip_decode_attn_splits(seq_len); }
+
+float* get_splitk_partials(int n_heads, int n_splits, int head_dim) {
+    return jllm_hip_get_splitk_partials(n_heads, n_splits, head_dim);
+}
+
+void fp16_to_int8(int8_t* dst, float* scale_out, const half* src, int rows, int cols, hipStream_t stream) {
+    report(jllm_hip_fp16_to_int8(dst, scale_out, H(src), rows, cols, stream), "fp16_to_int8", dst,
+           (size_t)rows * cols & ~(size_t)1, stream);
+}
+
+}  // namespace jllm

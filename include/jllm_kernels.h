@@ -1,0 +1,60 @@
+// jllm_kernels.h -- drop-in C++ interface of the MI355X quantized-matmul hot
+// path, with the names, argument order and meaning of genie-ai-runtime's
+// include/jllm_kernels.h (namespace jllm, C++ linkage) for the subset this
+// library implements.  hipStream_t replaces cudaStream_t; half is HIP's
+// IEEE binary16 type.  Each function forwards to the C ABI in jllm_hip.h.
+//
+// Error behaviour: the reference functions return void and, when the GPU
+// path cannot run, compute on the host or zero-fill the output for an
+// unsupported type.  Here there is no host path: any failure is reported on
+// stderr and the output is zero-filled on the stream.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <cstdint>
+
+namespace jllm {
+
+// mapped-weight registry (jllm_kernels.h:40-43 of the reference)
+const void* resolve_mapped_weight_device_ptr(const void* host_ptr);
+void register_mapped_weight_region(const void* host_base, const void* device_base, int64_t bytes);
+void clear_mapped_weight_region(const void* host_base);
+
+// legacy Q4 entry: forwards to gemv_quant with type 12 (reference :51)
+void gemv_q4(half* y, const void* W_q4, const half* scales, const half* x, int M, int K, int group_size,
+             hipStream_t stream);
+
+// K-quant GEMV family (reference :64, :78, :92, :106, :148)
+void gemv_quant(half* y, const void* W, int ggml_type, const half* x, int M, int K, hipStream_t stream);
+void gemv_quant_add(half* y, const void* W, int ggml_type, const half* x, const half* residual, int M, int K,
+                    hipStream_t stream);
+void gemv_quant_pair(half* y0, const void* W0, int ggml_type0, int M0, half* y1, const void* W1, int ggml_type1,
+                     int M1, const half* x, int K, hipStream_t stream);
+void gemv_quant_triple(half* y0, const void* W0, int ggml_type0, int M0, half* y1, const void* W1, int ggml_type1,
+                       int M1, half* y2, const void* W2, int ggml_type2, int M2, const half* x, int K,
+                       hipStream_t stream);
+void gemv_quant_f32(float* y, const void* W, int ggml_type, const half* x, int M, int K, hipStream_t stream);
+
+// batched prefill GEMM y[N x M] = x[N x K] . W^T (reference :135)
+void gemm_quant_batched(half* y, const void* W, int ggml_type, const half* x, int M, int N, int K,
+                        hipStream_t stream);
+
+// entry points the reference dispatcher calls without declaring them in its
+// header (gemv_q4.cu:468, :2462, :2470)
+void quantize_q8_1(const half* x, void* y, int K, hipStream_t stream);
+void gemm_q4k_mmq_llama(half* y, const void* W, const half* x, int M, int N, int K, hipStream_t stream);
+void gemm_q6k_mmq_llama(half* y, const void* W, const half* x, int M, int N, int K, hipStream_t stream);
+
+// decode attention (reference :323, :402-403)
+void flash_attention_decode(half* output, const half* q, const void* k_cache, const void* v_cache, int n_heads,
+                            int n_kv_heads, int head_dim, int cache_head_dim, int seq_len, float scale,
+                            bool kv_int8, const float* k_scales, const float* v_scales, int window,
+                            hipStream_t stream);
+int decode_attn_splits(int seq_len);
+float* get_splitk_partials(int n_heads, int n_splits, int head_dim);
+
+// KV quantiser (reference :413)
+void fp16_to_int8(int8_t* dst, float* scale_out, const half* src, int rows, int cols, hipStream_t stream);
+
+}  // namespace jllm

@@ -1,0 +1,80 @@
+"""CPU checks of the boundary: the C-ABI library loads without a GPU and
+exports every entry point that include/*.h declares (C symbols of
+jllm_hip.h and the namespace jllm C++ functions of jllm_kernels.h); plus the
+host-side pieces that need no device (status strings, mapped-weight
+registry, split policy)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import jllm
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _exports():
+    out = subprocess.run(["nm", "-DC", "--defined-only", jllm.LIB_PATH], capture_output=True, text=True, check=True)
+    return out.stdout
+
+
+def test_library_loads():
+    assert jllm.lib() is not None
+
+
+def test_every_c_declaration_exported():
+    hdr = open(os.path.join(ROOT, "include", "jllm_hip.h")).read()
+    names = set(re.findall(r"\b(jllm_hip_\w+)\s*\(", hdr))
+    assert len(names) >= 20
+    exp = _exports()
+    missing = [n for n in sorted(names) if not re.search(rf"\bT {n}\b", exp)]
+    assert not missing, missing
+    for n in names:                       # and the ctypes binding knows every one
+        assert n in jllm.SIGNATURES, n
+
+
+def test_every_cpp_declaration_exported():
+    hdr = open(os.path.join(ROOT, "include", "jllm_kernels.h")).read()
+    body = hdr[hdr.index("namespace jllm {"):]
+    names = set(re.findall(r"^\s*(?:const\s+)?[\w\*]+\*?\s+\**(\w+)\s*\(", body, re.M))
+    assert {"gemv_quant", "gemm_quant_batched", "flash_attention_decode", "fp16_to_int8"} <= names
+    exp = _exports()
+    missing = [n for n in sorted(names) if f"jllm::{n}(" not in exp]
+    assert not missing, missing
+
+
+def test_status_strings():
+    l = jllm.lib()
+    assert l.jllm_hip_status_string(0) == b"ok"
+    assert b"unsupported" in l.jllm_hip_status_string(-2)
+    assert l.jllm_hip_status_string(-99) == b"unknown status"
+
+
+def test_mapped_weight_registry():
+    # model.cpp:24-66 semantics: a pointer inside a registered host range maps
+    # to the device alias at the same offset; outside -> NULL; clear removes.
+    l = jllm.lib()
+    host = ctypes.create_string_buffer(4096)
+    hb = ctypes.addressof(host)
+    dev = 0x7F0000000000
+    assert l.jllm_hip_register_mapped_weight_region(hb, dev, 4096) == 0
+    assert l.jllm_hip_resolve_mapped_weight_device_ptr(hb + 100) == dev + 100
+    assert l.jllm_hip_resolve_mapped_weight_device_ptr(hb + 4096) is None
+    assert l.jllm_hip_register_mapped_weight_region(None, dev, 10) == -1
+    l.jllm_hip_clear_mapped_weight_region(hb)
+    assert l.jllm_hip_resolve_mapped_weight_device_ptr(hb + 100) is None
+
+
+def test_split_policy_host_only():
+    l = jllm.lib()
+    assert [l.jllm_hip_decode_attn_splits(s) for s in (0, 1, 64, 65, 512, 2048, 8192)] == [1, 1, 1, 2, 8, 32, 32]
+
+
+def test_argument_validation_without_gpu():
+    # shape / type checks happen before any HIP call
+    l = jllm.lib()
+    assert l.jllm_hip_gemv_quant(None, None, 13, None, 4, 256, None) != 0
+    assert l.jllm_hip_gemm_quant_batched(None, None, 12, None, 4, 4, 300, None) == -1
+    assert l.jllm_hip_quantize_mmq_q8_1(None, None, 1, 128, 64, 1, None) == -1
