@@ -13,12 +13,18 @@ struct AttnArgs {
     const float* ks;          // fp32 [pos][n_kv] (int8 only; may be null -> 1)
     const float* vs;
     float* part;              // partials: m [H*S] | l [H*S] | acc [H*S*hd]
+    int* counters;            // [n_kv] split-completion counters, zero between calls
     int n_heads, n_kv, head_dim, cache_head_dim, seq, window, n_splits;
     float scale;
 };
 
 int attn_splits(int seq_len, int n_kv);
 size_t attn_partials_floats(int n_heads, int n_splits, int head_dim);
+// Scratch layout: ATTN_COUNTER_BYTES of per-KV-head counters (fixed offset,
+// zero before the first call, reset by every call) followed by the partials.
+constexpr int ATTN_MAX_KV = 256;
+constexpr size_t ATTN_COUNTER_BYTES = ATTN_MAX_KV * sizeof(int);
+size_t attn_scratch_bytes(int n_heads, int n_splits, int head_dim);
 hipError_t attn_launch(const AttnArgs& a, bool kv_int8, hipStream_t st);
 
 }  // namespace jllm_hip

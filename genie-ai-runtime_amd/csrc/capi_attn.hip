@@ -7,12 +7,12 @@
 using namespace jllm_hip;
 
 namespace {
-DeviceScratch g_part;    // split-K partials, grown on demand, never freed
+DeviceScratch g_part;    // split-K partials + counters, grown on demand (zeroed), never freed
 
 int attn_check(const void* out, const void* q, const void* k, const void* v, int n_heads, int n_kv, int hd,
                int chd, int seq, int kv_int8, int window) {
     if (!out || !q || (seq > 0 && (!k || !v))) return JLLM_ERR_INVALID;
-    if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0 || n_heads / n_kv > 16) {
+    if (n_kv <= 0 || n_kv > ATTN_MAX_KV || n_heads <= 0 || n_heads % n_kv != 0 || n_heads / n_kv > 16) {
         fprintf(stderr, "[attention] n_heads=%d n_kv_heads=%d: need n_heads %% n_kv == 0 and <= 16 q heads per kv head\n", n_heads, n_kv);
         return JLLM_ERR_INVALID;
     }
@@ -35,10 +35,12 @@ int attn_run(uint16_t* out, const uint16_t* q, const void* k, const void* v, int
     if (st) return st;
     if (n_splits < 1) n_splits = 1;
     if (n_splits > 64) n_splits = 64;
-    float* part = (float*)g_part.get(attn_partials_floats(n_heads, n_splits, hd) * sizeof(float));
-    if (!part) return JLLM_ERR_NOMEM;
+    uint8_t* scratch = (uint8_t*)g_part.get(attn_scratch_bytes(n_heads, n_splits, hd));
+    if (!scratch) return JLLM_ERR_NOMEM;
     AttnArgs a;
-    a.out = out; a.q = q; a.k = k; a.v = v; a.ks = ks; a.vs = vs; a.part = part;
+    a.out = out; a.q = q; a.k = k; a.v = v; a.ks = ks; a.vs = vs;
+    a.counters = (int*)scratch;
+    a.part = (float*)(scratch + ATTN_COUNTER_BYTES);
     a.n_heads = n_heads; a.n_kv = n_kv; a.head_dim = hd; a.cache_head_dim = chd;
     a.seq = seq; a.window = window; a.n_splits = n_splits; a.scale = scale;
     return launch_status(attn_launch(a, kv_int8 != 0, (hipStream_t)stream), "attention");
@@ -51,7 +53,8 @@ int jllm_hip_decode_attn_splits(int seq_len) { return attn_splits(seq_len, 8); }
 
 float* jllm_hip_get_splitk_partials(int n_heads, int n_splits, int head_dim) {
     if (n_heads <= 0 || n_splits <= 0 || head_dim <= 0) return nullptr;
-    return (float*)g_part.get(attn_partials_floats(n_heads, n_splits, head_dim) * sizeof(float));
+    uint8_t* scratch = (uint8_t*)g_part.get(attn_scratch_bytes(n_heads, n_splits, head_dim));
+    return scratch ? (float*)(scratch + ATTN_COUNTER_BYTES) : nullptr;
 }
 
 int jllm_hip_flash_attention_decode(uint16_t* out, const uint16_t* q, const void* k, const void* v,

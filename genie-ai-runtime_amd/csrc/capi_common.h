@@ -33,6 +33,9 @@ struct DeviceScratch {
             if (ptr[dev]) (void)hipFree(ptr[dev]);
             ptr[dev] = nullptr; cap[dev] = 0;
             if (hipMalloc(&ptr[dev], bytes) != hipSuccess) { ptr[dev] = nullptr; return nullptr; }
+            // zeroed once, synchronously, at allocation (never inside a
+            // stream, so graph capture never records it)
+            if (hipMemset(ptr[dev], 0, bytes) != hipSuccess) { (void)hipFree(ptr[dev]); ptr[dev] = nullptr; return nullptr; }
             cap[dev] = bytes;
         }
         return ptr[dev];

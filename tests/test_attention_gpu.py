@@ -114,7 +114,7 @@ def test_attention_empty_sequence(dev):
 
 
 def test_splits_policy_and_partials(dev):
-    assert [jllm.lib().jllm_hip_decode_attn_splits(s) for s in (1, 64, 65, 512, 2048, 8192)] == [1, 1, 2, 8, 32, 32]
+    assert [jllm.lib().jllm_hip_decode_attn_splits(s) for s in (1, 128, 129, 512, 8192, 20000)] == [1, 1, 2, 4, 64, 128]
     assert jllm.lib().jllm_hip_get_splitk_partials(32, 32, 128)
 
 
