@@ -150,7 +150,7 @@ def main():
     achieved = pair_bytes / (us_launch * 1e-6) / 1e9
     out["roofline"] = {"kernel": "gemv_kernel<MMVQ, half out> (gate/up pair, Q4_K 2x9728x2560)",
                        "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                        "bytes_per_launch": pair_bytes, "us_per_launch": round(us_launch, 3)}
 
     if not args.skip_extras:
@@ -158,6 +158,18 @@ def main():
         out["attention"] = bench_attention(np, torch, jllm, synth, up, dev, g)
     out["cpu_baseline"] = cpu_baseline(np, synth, args.cpu_seconds)
     print(json.dumps(out), flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per pair launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (profiles/gemv_pair_traffic.md), or None if it is absent."""
+    try:
+        for line in open(os.path.join(ROOT, "profiles", "gemv_pair_traffic.md")):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def bench_mmq(np, torch, jllm, synth, up, dev, g):

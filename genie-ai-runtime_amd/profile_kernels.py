@@ -1,0 +1,54 @@
+"""Workloads for rocprofv3 counter runs (run under `rocprofv3 --pmc ... -- python3 ...`).
+
+  pair  : the decode gate/up pair GEMV (Q4_K 2 x 9728 x 2560) over 36 distinct
+          layers' weights, 3 passes -- the dominant kernel of bench.py
+  lmhead: the Q6_K lm_head GEMV (151936 x 2560, fp32 out), 4 distinct copies
+  copy  : a plain device-to-device copy of 256 MiB (calibrates FETCH_SIZE /
+          WRITE_SIZE against a known byte count)
+"""
+import os
+import sys
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+
+
+def main(mode):
+    import numpy as np
+    import torch
+    import jllm
+    import synth
+    dev = torch.device("cuda:0")
+    g = synth.rng(99)
+
+    def up(a):
+        a = np.ascontiguousarray(a)
+        return torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a).to(dev)
+
+    if mode == "pair":
+        gate, upw = up(synth.q4k(g, 9728, 2560)), up(synth.q4k(g, 9728, 2560))
+        layers = [(gate.clone(), upw.clone()) for _ in range(36)]
+        x = up(synth.x_f16(g, 2560))
+        y0 = torch.empty(9728, dtype=torch.int16, device=dev)
+        y1 = torch.empty(9728, dtype=torch.int16, device=dev)
+        for _ in range(3):
+            for gw, uw in layers:
+                jllm.gemv_quant_pair(y0, gw, 12, 9728, y1, uw, 12, 9728, x, 2560)
+    elif mode == "lmhead":
+        w = up(synth.q6k(g, 151936, 2560))
+        ws = [w] + [w.clone() for _ in range(3)]
+        x = up(synth.x_f16(g, 2560))
+        y = torch.empty(151936, dtype=torch.float32, device=dev)
+        for _ in range(3):
+            for wi in ws:
+                jllm.gemv_quant_f32(y, wi, 14, x, 151936, 2560)
+    elif mode == "copy":
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+    torch.cuda.synchronize()
+    print("done", mode)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "pair")
