@@ -148,7 +148,7 @@ def main():
     torch.cuda.synchronize()
     us_launch = e0.elapsed_time(e1) * 1e3 / (reps * L)
     achieved = pair_bytes / (us_launch * 1e-6) / 1e9
-    out["roofline"] = {"kernel": "gemv_kernel<MMVQ, half out> (gate/up pair, Q4_K 2x9728x2560)",
+    out["roofline"] = {"kernel": "gemv_stream_kernel<MMVQ, half out> (gate/up pair, Q4_K 2x9728x2560)",
                        "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                        "bytes_per_launch": pair_bytes, "us_per_launch": round(us_launch, 3)}

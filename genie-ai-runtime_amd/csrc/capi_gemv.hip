@@ -100,17 +100,8 @@ int make_seg(const char* tag, GemvSeg& s, void* y, const void* W, int type, int 
     return JLLM_OK;
 }
 
-int lpr_override() {
-    static const int v = [] {
-        const char* e = getenv("JLLM_GEMV_LPR");
-        int r = e ? atoi(e) : 0;
-        return (r == 4 || r == 8 || r == 16 || r == 32 || r == 64) ? r : 0;
-    }();
-    return v;
-}
-
 int run(const char* tag, GemvArgs& a, bool mmvq, int out, void* stream) {
-    return launch_status(gemv_launch(a, mmvq, out, lpr_override(), (hipStream_t)stream), tag);
+    return launch_status(gemv_launch(a, mmvq, out, (hipStream_t)stream), tag);
 }
 
 }  // namespace

@@ -23,15 +23,26 @@ struct GemvArgs {
     int nseg;
     int K;
     const uint16_t* x;     // fp16 activation [K]
-    int lpr;               // lanes per row (filled by gemv_launch)
-    int gend[3];           // cumulative row-group ends per segment (filled by gemv_launch)
-    int per_q;             // blocks per quad and row (filled by gemv_launch)
-    int g_split;           // row groups of Q4_K segments (filled by gemv_launch)
-    int wg_split;          // workgroups serving Q4_K (filled by gemv_launch)
+};
+
+// Arguments of the streaming kernel (filled by gemv_launch).  Segments
+// are ordered Q4_K first; their rows form one sequence.
+struct StreamArgs {
+    GemvSeg seg[3];
+    int K;
+    int nb;                 // K / 256
+    int xlds_bytes;         // LDS bytes of the staged activation
+    const uint16_t* x;
+    int row_off[4];         // first row of each segment in the row sequence
+    int row_split;          // rows of Q4_K segments
+    int wave_split;         // waves (over the grid) serving the Q4_K rows
+    int rows_q[2], rows_r[2];       // rows per wave (quotient, remainder) per type
+    int slots_per_wave;     // LDS block slots per wave (max rows per wave * nb)
+    int wg_rows;            // residual rows staged per workgroup (waves * max rows per wave)
 };
 
 size_t gemv_lds_bytes(bool mmvq, int K);
-hipError_t gemv_launch(const GemvArgs& a, bool mmvq, int out_kind, int lpr_override, hipStream_t st);
+hipError_t gemv_launch(const GemvArgs& a, bool mmvq, int out_kind, hipStream_t st);
 hipError_t quantize_q8_1_aos_launch(const uint16_t* x, void* y, int K, hipStream_t st);
 
 }  // namespace jllm_hip

@@ -5,29 +5,20 @@
 //   * MMVQ: the fp16 activation is quantised to q8_1 (32-value blocks,
 //     gemv_q4.cu:445-466) and dotted as int8 (v_dot4_i32_i8) against the
 //     weight codes, one exact int32 per 32-weight Q4_K sub-block or per
-//     4-weight Q6_K group, then scaled in fp32 (gemv_q4.cu:474-618).
+//     16-weight Q6_K group, then scaled in fp32 (gemv_q4.cu:474-618).
 //   * float dequant: weights dequantised in registers and dotted with the
 //     fp16 activation in fp32 (gemv_q4.cu:266-398).
 //
-// Layout of the work: every workgroup (256 lanes) first stages the whole
-// activation vector in LDS -- for MMVQ it quantises it there, so no q8_1
-// scratch buffer and no separate quantiser launch are needed.  Then groups
-// of LPR lanes own one output row; inside a group, each 8-lane octet streams
-// one super-block per step (Q4_K: two 16 B loads per lane, Q6_K: three
-// 8 B loads per lane), so a wave's load instruction touches whole 144/210 B
-// blocks.  Rows are reduced with lane shuffles at the end.
+// Layout of the work (streaming kernel below): the rows of a launch are
+// split between waves; each wave streams its rows' bytes (contiguous in
+// memory) in rounds of 4 KiB -- every lane loads 16-byte chunks, so a wave's
+// load instruction covers 1 KiB of consecutive bytes -- through registers
+// into its own LDS buffer, from which one quad of lanes per super-block does
+// the arithmetic.  The activation is staged once per workgroup in LDS (for
+// MMVQ quantised there, so no q8_1 buffer and no extra launch).
 #include "kq_common.h"
 #include "gemv.h"
-
-#ifndef JLLM_GEMV_NT
-#define JLLM_GEMV_NT 0
-#endif
-// Weight loads: streaming (non-temporal) or ordinary cached loads.
-#if JLLM_GEMV_NT
-#define WLOAD(p) __builtin_nontemporal_load(p)
-#else
-#define WLOAD(p) (*(p))
-#endif
+#include <algorithm>
 
 // Native clang vector types (not HIP's struct-based uint4 & co.), so that
 // values in them stay in registers.
@@ -85,111 +76,34 @@ __device__ __forceinline__ int q6_group_slot(int n) {
     return b * 16 + h * 8 + lh * 4 + g;
 }
 
-// MMVQ staging: q8 codes [K] | d8 fp32 [K/32] | s8 fp32 [K/32] | q6 group
-// code sums int [K/16] (lane order).
-__device__ __forceinline__ void stage_q8_1(const uint16_t* __restrict__ x, int K, uint8_t* lds) {
-    int8_t* s_q = (int8_t*)lds;
-    float* s_d8 = (float*)(lds + K);
-    float* s_s8 = s_d8 + K / 32;
-    int* s_sx = (int*)(s_s8 + K / 32);
-    const int n = (K / 32) * 8;
-    for (int t = threadIdx.x; t < n; t += GEMV_THREADS) {
-        const int blk = t >> 3, sub = t & 7;
-        const u32x2 raw = *(const u32x2*)(x + blk * 32 + sub * 4);
-        float d; int sall, shalf;
-        const uint32_t packed = quant_q8_1_x4(raw, d, sall, shalf);
-        *(uint32_t*)(s_q + blk * 32 + sub * 4) = packed;
-        if (sub == 0) {
-            // s = d*sum(q) rounded through fp16 like the stored block_q8_1 field
-            s_d8[blk] = round_to_f16(d);
-            s_s8[blk] = round_to_f16(d * (float)sall);
-        }
-        if ((sub & 3) == 0) s_sx[q6_group_slot(blk * 2 + (sub >> 2))] = shalf;
-    }
-}
-
 // x index -> LDS half index: 8 halves of padding after every 128, so that the
 // quads' reads 256 B apart land in different banks.
+//
+// Staged activation in LDS (gemv_lds_bytes):
+//   MMVQ : q8 codes i8 [K] | d8 f32 [K/32] | s8 f32 [K/32] (both rounded
+//          through fp16 like the block_q8_1 fields) | per-16 code sums i32
+//          [K/16] in Q6_K lane order (q6_group_slot)
+//   float: x f16 [K + K/16] (xpad) | per-32 sums f32 [K/32] | 32 * per-16
+//          sums f32 [K/16] in Q6_K lane order
 __device__ __forceinline__ int xpad(int k) { return k + ((k >> 7) << 3); }
 
-// float staging: x fp16 [K + K/16 padded] | per-32 fp32 sums [K/32] |
-// 32 * per-16 fp32 sums [K/16] (Q6_K lane order).
-__device__ __forceinline__ void stage_f16(const uint16_t* __restrict__ x, int K, uint8_t* lds) {
-    uint16_t* s_x = (uint16_t*)lds;
-    float* s_x32 = (float*)(lds + 2 * K + K / 8);
-    float* s_x16 = s_x32 + K / 32;
-    const int n = K / 16;
-    const uint32_t one = 0x3C003C00u;
-    for (int t = threadIdx.x; t < n; t += GEMV_THREADS) {
-        const u32x4 a = *(const u32x4*)(x + t * 16);
-        const u32x4 b = *(const u32x4*)(x + t * 16 + 8);
-        *(u32x4*)(s_x + xpad(t * 16)) = a;
-        *(u32x4*)(s_x + xpad(t * 16) + 8) = b;
-        float s = 0.0f;
-        s = fdot2(a.x, one, s); s = fdot2(a.y, one, s); s = fdot2(a.z, one, s); s = fdot2(a.w, one, s);
-        s = fdot2(b.x, one, s); s = fdot2(b.y, one, s); s = fdot2(b.z, one, s); s = fdot2(b.w, one, s);
-        s_x16[q6_group_slot(t)] = 32.0f * s;
-        const float s2 = s + __shfl_xor(s, 1, 64);
-        if ((t & 1) == 0) s_x32[t >> 1] = s2;
-    }
-}
-
-// ---- raw weight loads ------------------------------------------------------
+// ---- block slices ------------------------------------------------------------
 
 // Quad lane layout: 4 lanes per super-block; lane q (0..3) owns 64 weights.
 //   Q4_K: qs bytes [32q, 32q+32): low nibbles = sub-block 2q, high = 2q+1.
 //   Q6_K: half h = q/2 of the block, positions l0..l0+15 (l0 = 16*(q&1)) of
 //         each 32-wide quarter g = 0..3: elements h*128 + 32g + l0 + [0,16).
-// One register layout for both types (Q4_K uses a = header, b/c = qs) so a
-// wave can keep prefetched blocks of either type in the same registers.
-// Q6_K pieces are loaded dword-aligned from 2 bytes early when the block is
-// only 2-byte aligned (sh = 16); the funnel shift that realigns them is
-// applied at use, so no load has to be waited for before the next is issued.
+// One register layout for both types (Q4_K uses a = header, b/c = qs).
+// Q6_K blocks are only 2-byte aligned: their pieces are read dword-aligned
+// from up to 2 bytes early (sh = 16 when so) and realigned with a funnel
+// shift.
 struct Raw { u32x4 a, b, c; uint32_t a4, b4, c4; u32x2 sc; uint32_t sc2, d, sh; };
-template <int TYPE> struct RawT { Raw r; };
-typedef RawT<TYPE_Q4_K> RawQ4;
-typedef RawT<TYPE_Q6_K> RawQ6;
-
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
-
-__device__ __forceinline__ u32x4 ld_nt16(const uint8_t* p) {
-    const u32x4 v = WLOAD((const u32x4*)p);
-    return u32x4_make(v.x, v.y, v.z, v.w);
-}
-
-// A piece of a Q6_K block that starts at a 2-byte-aligned address p: load the
-// dword-aligned window [p - pad, p - pad + 20) (pad = p & 2), realign later.
-__device__ __forceinline__ void ld16_window(const uint8_t* p, u32x4& v, uint32_t& w4) {
-    const uint8_t* base = p - ((uintptr_t)p & 3u);   // keeps the global address space
-    const u32x4_a4 t = WLOAD((const u32x4_a4*)base);
-    v = u32x4_make(t.x, t.y, t.z, t.w);
-    w4 = WLOAD((const uint32_t*)(base + 16));
-}
 
 __device__ __forceinline__ u32x4 realign16(const u32x4& v, uint32_t w4, uint32_t sh) {
     return u32x4_make(__builtin_amdgcn_alignbit(v.y, v.x, sh), __builtin_amdgcn_alignbit(v.z, v.y, sh),
                       __builtin_amdgcn_alignbit(v.w, v.z, sh), __builtin_amdgcn_alignbit(w4, v.w, sh));
-}
-
-template <int TYPE>
-__device__ __forceinline__ void load_raw(const uint8_t* __restrict__ blk, int q, Raw& r) {
-    if (TYPE == TYPE_Q4_K) {
-        r.a = ld_nt16(blk);                  // d, dmin, scales[12]
-        r.b = ld_nt16(blk + 16 + 32 * q);
-        r.c = ld_nt16(blk + 32 + 32 * q);
-    } else {
-        const int h = q >> 1, l0 = 16 * (q & 1);
-        r.sh = (uint32_t)((uintptr_t)blk & 2u) * 8u;
-        ld16_window(blk + h * 64 + l0, r.a, r.a4);        // ql, quarters 0 / 2
-        ld16_window(blk + h * 64 + 32 + l0, r.b, r.b4);   // ql, quarters 1 / 3
-        ld16_window(blk + 128 + h * 32 + l0, r.c, r.c4);  // qh
-        const uint8_t* sb = blk + 192 + 8 * h - ((uintptr_t)blk & 3u);
-        const u32x2_a4 t = WLOAD((const u32x2_a4*)sb);
-        r.sc = u32x2_make(t.x, t.y);
-        r.sc2 = WLOAD((const uint32_t*)(sb + 8));
-        r.d = WLOAD((const uint16_t*)(blk + 208));
-    }
 }
 
 // ---- per-lane constants ------------------------------------------------------
@@ -381,73 +295,18 @@ __device__ __forceinline__ float f16_block<TYPE_Q6_K>(const Raw& raw, int b, int
     return f16_bits_to_f32(r.d) * acc;
 }
 
+// Row result: fp32, fp16, or fp16 of fp16(W x) + residual (the residual row
+// staged in LDS).
 template <int OUT>
-__device__ __forceinline__ void store_row(const GemvSeg& s, int r, float acc) {
+__device__ __forceinline__ void store_row(const GemvSeg& s, int r, float acc, const uint16_t* res_lds, int lrow) {
     if (OUT == OUT_F32) {
         ((float*)s.y)[r] = acc;
     } else if (OUT == OUT_HALF) {
         ((uint16_t*)s.y)[r] = f32_to_f16_bits(acc);
     } else {   // y = half(half(W x) + residual), gemv_q4.cu:1001-1004
         const float proj = round_to_f16(acc);
-        ((uint16_t*)s.y)[r] = f32_to_f16_bits(proj + f16_bits_to_f32(s.res[r]));
+        ((uint16_t*)s.y)[r] = f32_to_f16_bits(proj + f16_bits_to_f32(res_lds[lrow]));
     }
-}
-
-__device__ __forceinline__ float row_reduce(float v, int lpr) {
-    if (lpr > 32) v += __shfl_xor(v, 32, 64);
-    if (lpr > 16) v += __shfl_xor(v, 16, 64);
-    if (lpr > 8)  v += __shfl_xor(v, 8, 64);
-    if (lpr > 4)  v += __shfl_xor(v, 4, 64);
-    v += __shfl_xor(v, 2, 64);
-    v += __shfl_xor(v, 1, 64);
-    return v;
-}
-
-// Work of one wave: a sequence of row groups (rpw = 64/lpr rows of one
-// segment each, so the weight type is wave-uniform), each split into `spg`
-// steps of U blocks per lane.  Quad qi of a row owns the contiguous blocks
-// [qi*per_q, (qi+1)*per_q); per_q is even for Q6_K so that all quads of a
-// wave touch blocks of the same 4-byte alignment at every step.
-struct WaveWork {
-    int grp0, gstride, ngrp_end;   // groups grp0, grp0+gstride, ... < ngrp_end
-    int spg;                       // steps per group
-};
-
-struct StepPos {
-    const uint8_t* blk0;  // address of the step's first block (clamped to a valid block)
-    const uint8_t* blk1;  // address of the step's second block (clamped)
-    int s;                // wave-uniform segment
-    int r;                // row within the segment
-    bool live;            // row exists
-    bool v0, v1;          // the two blocks belong to this lane
-    int b_first;          // block index of the first block
-};
-
-// grp is wave-uniform; it is made explicitly so (readfirstlane) so that the
-// segment lookups below are scalar loads from the kernel arguments.  Block
-// addresses are clamped to valid blocks of the matrix so that every lane
-// issues the same loads (exact wait counts, no branches around loads); the
-// data of blocks that are not the lane's is never used.
-template <int TYPE>
-__device__ __forceinline__ StepPos step_pos(const GemvArgs& a, int grp, int step, int lane, int lpr, int rpw,
-                                            int qi, int per_q, int nb) {
-    constexpr int BB = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
-    StepPos p;
-    grp = __builtin_amdgcn_readfirstlane(grp);
-    const int s = grp >= a.gend[0] ? (grp >= a.gend[1] ? 2 : 1) : 0;
-    const int gstart = s == 0 ? 0 : a.gend[s - 1];
-    p.s = s;
-    p.r = (grp - gstart) * rpw + lane / lpr;
-    p.live = p.r < a.seg[s].M;
-    const int q0 = qi * per_q;
-    const int b_end = min(q0 + per_q, nb);
-    p.b_first = q0 + step * 2;
-    p.v0 = p.live && p.b_first < b_end;
-    p.v1 = p.live && p.b_first + 1 < b_end;
-    const uint8_t* rowp = a.seg[s].W + (int64_t)(p.live ? p.r : 0) * nb * BB;
-    p.blk0 = rowp + (int64_t)(p.v0 ? p.b_first : 0) * BB;
-    p.blk1 = rowp + (int64_t)(p.v1 ? p.b_first + 1 : 0) * BB;
-    return p;
 }
 
 template <bool MMVQ, int TYPE>
@@ -455,85 +314,88 @@ __device__ __forceinline__ float block_dot(const Raw& r, int b, int q, const Q4C
     return MMVQ ? mmvq_block<TYPE>(r, b, q, c, lds, K) : f16_block<TYPE>(r, b, q, c, lds, K);
 }
 
-template <bool MMVQ, int TYPE>
-__device__ __forceinline__ float compute_step(const StepPos& p, int q, const Q4Consts& c,
-                                              const uint8_t* lds, int K, const Raw& r0, const Raw& r1) {
-    float acc = 0.0f;
-    if (p.v0) acc += block_dot<MMVQ, TYPE>(r0, p.b_first, q, c, lds, K);
-    __builtin_amdgcn_sched_barrier(0);
-    if (p.v1) acc += block_dot<MMVQ, TYPE>(r1, p.b_first + 1, q, c, lds, K);
-    return acc;
-}
+// ---- streaming kernel ----------------------------------------------------
+//
+// All segments of a launch share K, so their rows form one sequence of
+// rows x nb blocks.  The waves of the grid (4 per workgroup, up to 4
+// workgroups per CU) split the Q4_K rows and the Q6_K rows between them in
+// proportion to bytes; a wave's rows are contiguous bytes per segment and are
+// streamed in rounds of up to 4 KiB: each lane loads 4 aligned 16-byte chunks
+// (buffer loads: chunks past the round's end are not fetched), two rounds
+// ahead of the one being computed, and the wave moves a round into its own
+// LDS buffer -- no workgroup barrier in the loop.  A round is computed with
+// one quad per block (the per-block arithmetic above, reading the block from
+// LDS); the quad's sum lands in the block's slot, and at the end each row
+// adds its nb slots in block order and is stored.  The activation and the
+// residual rows are loaded before any weight bytes, behind a barrier, so
+// that they do not queue behind the CU's weight traffic.
 
-#ifndef JLLM_GEMV_WAVES_PER_EU
-#define JLLM_GEMV_WAVES_PER_EU 2
-#endif
+constexpr int ST_T = GEMV_THREADS;
+constexpr int ST_W = ST_T / 64;        // waves per workgroup
 
-// The waves of the workgroups assigned to one weight type walk that type's
-// row groups [g_begin, g_end) grid-stride; steps of two blocks per lane run
-// through a two-stage register pipeline (loads of step i+1 in flight while
-// step i is computed).  The first step is issued before x is staged.
-template <bool MMVQ, int OUT, int TYPE>
-__device__ __forceinline__ void gemv_body(const GemvArgs& a, uint8_t* lds, int g_begin, int g_end,
-                                          int wg, int nwg) {
-    const int K = a.K, nb = K / QK_K, lpr = a.lpr;
-    const int rpw = 64 / lpr;
-    const int lane = threadIdx.x & 63;
-    const int qi = (lane & (lpr - 1)) >> 2, q = lane & 3;
-    const int wave0 = g_begin + __builtin_amdgcn_readfirstlane((wg * GEMV_THREADS + threadIdx.x) >> 6);
-    const int nwaves = nwg * (GEMV_THREADS / 64);
-    const Q4Consts c = q4_consts(q);
-    const int per_q = a.per_q;
-    const int spg = (per_q + 1) / 2;
-    const int my_groups = wave0 < g_end ? (g_end - wave0 + nwaves - 1) / nwaves : 0;
-    const int total = my_groups * spg;
+// lane ^ 1 and lane ^ 2 through DPP quad_perm (no LDS round trip)
+__device__ __forceinline__ int dpp_x1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int dpp_x2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
+__device__ __forceinline__ float dpp_x1(float v) { return __builtin_bit_cast(float, dpp_x1(__builtin_bit_cast(int, v))); }
+__device__ __forceinline__ float dpp_x2(float v) { return __builtin_bit_cast(float, dpp_x2(__builtin_bit_cast(int, v))); }
 
-    Raw A0, A1, B0, B1;
-    StepPos pa, pb;
-    if (total > 0) {
-        pa = step_pos<TYPE>(a, wave0, 0, lane, lpr, rpw, qi, per_q, nb);
-        load_raw<TYPE>(pa.blk0, q, A0);
-        load_raw<TYPE>(pa.blk1, q, A1);
+// q8_1 of one 8-value chunk c of x (4 lanes per 32-value block): d = amax/127,
+// q = rn(v*(1/d)) clamped to +-127, s = d*sum(q) (quantize_q8_1_kernel,
+// gemv_q4.cu:445-466), into the MMVQ staging layout.
+__device__ __forceinline__ void xstage_q8_1(const u32x4& raw, int c, int K, uint8_t* lds) {
+    int8_t* s_q = (int8_t*)lds;
+    float* s_d8 = (float*)(lds + K);
+    float* s_s8 = s_d8 + K / 32;
+    int* s_sx = (int*)(s_s8 + K / 32);
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) { v[2 * i] = f16_bits_to_f32(w[i] & 0xFFFFu); v[2 * i + 1] = f16_bits_to_f32(w[i] >> 16); }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, dpp_x1(amax));
+    amax = fmaxf(amax, dpp_x2(amax));
+    const float d = amax / 127.0f;
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    uint32_t p0 = 0, p1 = 0;
+    int sumq = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        int q = (int)__builtin_rintf(v[i] * id);
+        q = q > 127 ? 127 : (q < -127 ? -127 : q);
+        sumq += q;
+        if (i < 4) p0 |= ((uint32_t)q & 0xFFu) << (8 * i);
+        else       p1 |= ((uint32_t)q & 0xFFu) << (8 * (i - 4));
     }
-    if (MMVQ) stage_q8_1(a.x, K, lds);
-    else      stage_f16(a.x, K, lds);
-    __syncthreads();
-
-    float acc = 0.0f;
-    auto finish = [&](const StepPos& p, int i) {
-        if ((i % spg) == spg - 1) {
-            const float v = row_reduce(acc, lpr);
-            if (p.live && (threadIdx.x & (lpr - 1)) == 0) store_row<OUT>(a.seg[p.s], p.r, v);
-            acc = 0.0f;
+    const int shalf = sumq + dpp_x1(sumq);
+    const int sall = shalf + dpp_x2(shalf);
+    if (c < K / 8) {
+        *(u32x2*)(s_q + 8 * c) = u32x2_make(p0, p1);
+        const int blk = c >> 2, sub = c & 3;
+        if (sub == 0) {
+            s_d8[blk] = round_to_f16(d);
+            s_s8[blk] = round_to_f16(d * (float)sall);
         }
-    };
-    for (int i = 0; i < total; i += 2) {
-        if (i + 1 < total) {
-            pb = step_pos<TYPE>(a, wave0 + ((i + 1) / spg) * nwaves, (i + 1) % spg, lane, lpr, rpw, qi, per_q, nb);
-            load_raw<TYPE>(pb.blk0, q, B0);
-            load_raw<TYPE>(pb.blk1, q, B1);
-        }
-        acc += compute_step<MMVQ, TYPE>(pa, q, c, lds, K, A0, A1);
-        finish(pa, i);
-        if (i + 1 >= total) break;
-        if (i + 2 < total) {
-            pa = step_pos<TYPE>(a, wave0 + ((i + 2) / spg) * nwaves, (i + 2) % spg, lane, lpr, rpw, qi, per_q, nb);
-            load_raw<TYPE>(pa.blk0, q, A0);
-            load_raw<TYPE>(pa.blk1, q, A1);
-        }
-        acc += compute_step<MMVQ, TYPE>(pb, q, c, lds, K, B0, B1);
-        finish(pb, i + 1);
+        if ((sub & 1) == 0) s_sx[q6_group_slot(blk * 2 + (sub >> 1))] = shalf;
     }
 }
 
-// Segments are ordered Q4_K first; workgroups [0, wg_split) serve the Q4_K
-// row groups [0, g_split), the rest serve the Q6_K groups [g_split, gend[2]).
-template <bool MMVQ, int OUT>
-__global__ __launch_bounds__(GEMV_THREADS) __attribute__((amdgpu_waves_per_eu(JLLM_GEMV_WAVES_PER_EU)))
-void gemv_kernel(GemvArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    if ((int)blockIdx.x < a.wg_split) gemv_body<MMVQ, OUT, TYPE_Q4_K>(a, lds, 0, a.g_split, blockIdx.x, a.wg_split);
-    else gemv_body<MMVQ, OUT, TYPE_Q6_K>(a, lds, a.g_split, a.gend[2], blockIdx.x - a.wg_split, gridDim.x - a.wg_split);
+// fp16 copy and sums of one 8-value chunk, into the float staging layout.
+__device__ __forceinline__ void xstage_f16(const u32x4& a, int c, int K, uint8_t* lds) {
+    uint16_t* s_x = (uint16_t*)lds;
+    float* s_x32 = (float*)(lds + 2 * K + K / 8);
+    float* s_x16 = s_x32 + K / 32;
+    const uint32_t one = 0x3C003C00u;
+    float s = fdot2(a.x, one, 0.0f);
+    s = fdot2(a.y, one, s); s = fdot2(a.z, one, s); s = fdot2(a.w, one, s);
+    const float s16 = s + dpp_x1(s);
+    const float s32 = s16 + dpp_x2(s16);
+    if (c < K / 8) {
+        *(u32x4*)(s_x + xpad(8 * c)) = a;
+        if ((c & 1) == 0) s_x16[q6_group_slot(c >> 1)] = 32.0f * s16;
+        if ((c & 3) == 0) s_x32[c >> 2] = s32;
+    }
 }
 
 // Standalone q8_1 quantiser in the reference's AoS block layout
@@ -555,10 +417,6 @@ void quantize_q8_1_aos_kernel(const uint16_t* __restrict__ x, uint8_t* __restric
 
 // ---- host launchers ----------------------------------------------------
 
-#ifndef JLLM_GEMV_WAVES_PER_CU
-#define JLLM_GEMV_WAVES_PER_CU 12
-#endif
-
 size_t gemv_lds_bytes(bool mmvq, int K) {
     return mmvq ? (size_t)K + (size_t)(K / 32) * 8 + (size_t)(K / 16) * 4
                 : (size_t)K * 2 + (size_t)(K / 8) + (size_t)(K / 32) * 4 + (size_t)(K / 16) * 4;
@@ -574,77 +432,370 @@ static int device_cus() {
     return cus;
 }
 
-// Lanes per row: one quad per row unless the row groups are too few to give
-// every resident wave two of them; then more quads share each row.
-static int pick_lpr(int64_t rows, int nb, int64_t resident_waves) {
-    int lpr = 4;
-    while (lpr < 64 && lpr < 4 * nb && rows * lpr / 64 < 2 * resident_waves) lpr *= 2;
-    return lpr;
+// The rows [r0, r1) (segment-relative) a wave owns inside one segment, its
+// first slot and its rounds.
+struct Piece { int r0, r1, slot0, rounds; };
+
+// A round: up to WGeom::NBLK blocks of one piece (contiguous bytes).
+struct RoundDesc {
+    const uint8_t* base;   // 16-byte-aligned start of the round's bytes
+    int nrec;              // bytes to fetch (multiple of 16; 0 for no round)
+    int delta;             // offset of the first block in the fetched bytes
+    int nblk;              // blocks in the round
+    int col0;              // block column of the first block
+    int slot0;             // slot of the first block
+};
+
+template <int TYPE, int L>
+struct WGeom {
+    static constexpr int BB = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    static constexpr int BYTES = 64 * 16 * L;                                  // one wave's round
+    static constexpr int NBLK = TYPE == TYPE_Q4_K ? BYTES / BB : (BYTES - 14) / BB;
+};
+
+template <int TYPE, int L>
+__device__ __forceinline__ RoundDesc round_desc(const StreamArgs& a, const Piece (&pc)[3], int k) {
+    constexpr int BB = WGeom<TYPE, L>::BB, NB = WGeom<TYPE, L>::NBLK;
+    const int nb = a.nb;
+    RoundDesc d;
+    d.base = a.seg[0].W; d.nrec = 0; d.delta = 0; d.nblk = 0; d.col0 = 0; d.slot0 = 0;
+    int r = k;
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        if (r >= 0 && r < pc[i].rounds) {
+            const int f = r * NB;                                   // block offset in the piece
+            d.nblk = min(NB, (pc[i].r1 - pc[i].r0) * nb - f);
+            const uint8_t* start = a.seg[i].W + ((int64_t)pc[i].r0 * nb + f) * BB;
+            d.delta = (int)((uintptr_t)start & 15u);
+            d.base = start - d.delta;
+            d.nrec = (d.delta + d.nblk * BB + 15) & ~15;
+            d.col0 = f % nb;
+            d.slot0 = pc[i].slot0 + f;
+        }
+        r -= pc[i].rounds;
+    }
+    return d;
 }
 
-template <bool MMVQ, int OUT>
-static hipError_t launch_k(const GemvArgs& a, int grid, size_t lds, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_kernel<MMVQ, OUT>), dim3(grid), dim3(GEMV_THREADS), lds, st, a);
+template <int L>
+__device__ __forceinline__ void issue_round(const RoundDesc& d, u32x4 (&v)[L], int lane) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)d.base, (short)0, d.nrec, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < L; i++) v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane + 64 * i) * 16, 0, 0);
+}
+
+template <int L>
+__device__ __forceinline__ void write_round(uint8_t* buf, const u32x4 (&v)[L], int lane) {
+#pragma unroll
+    for (int i = 0; i < L; i++) *(u32x4*)(buf + (lane + 64 * i) * 16) = v[i];
+}
+
+// Raw lane slice of the block at byte offset `off` of an LDS round buffer
+// (16-byte aligned).  Same register layout as load_raw.
+template <int TYPE>
+__device__ __forceinline__ void load_raw_lds(const uint8_t* buf, int off, int q, Raw& r) {
+    if (TYPE == TYPE_Q4_K) {
+        const uint8_t* blk = buf + off;          // 16-byte aligned
+        r.a = *(const u32x4*)blk;
+        r.b = *(const u32x4*)(blk + 16 + 32 * q);
+        r.c = *(const u32x4*)(blk + 32 + 32 * q);
+    } else {
+        const int h = q >> 1, l0 = 16 * (q & 1);
+        r.sh = (uint32_t)(off & 2) * 8u;
+        const uint8_t* b4 = buf + (off & ~3);    // dword-aligned, up to 2 bytes before the block
+        const u32x4_a4 ta = *(const u32x4_a4*)(b4 + h * 64 + l0);
+        const u32x4_a4 tb = *(const u32x4_a4*)(b4 + h * 64 + 32 + l0);
+        const u32x4_a4 tc = *(const u32x4_a4*)(b4 + 128 + h * 32 + l0);
+        r.a = u32x4_make(ta.x, ta.y, ta.z, ta.w); r.a4 = *(const uint32_t*)(b4 + h * 64 + l0 + 16);
+        r.b = u32x4_make(tb.x, tb.y, tb.z, tb.w); r.b4 = *(const uint32_t*)(b4 + h * 64 + 32 + l0 + 16);
+        r.c = u32x4_make(tc.x, tc.y, tc.z, tc.w); r.c4 = *(const uint32_t*)(b4 + 128 + h * 32 + l0 + 16);
+        const u32x2_a4 t = *(const u32x2_a4*)(b4 + 192 + 8 * h);
+        r.sc = u32x2_make(t.x, t.y);
+        r.sc2 = *(const uint32_t*)(b4 + 192 + 8 * h + 8);
+        r.d = *(const uint16_t*)(buf + off + 208);
+    }
+}
+
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dpp_x1(v);
+    return v + dpp_x2(v);
+}
+
+// One quad per block: quad j (0..15) of the wave takes blocks j, j+16, ... of
+// the round; the quad sum of a block lands in its slot.
+template <bool MMVQ, int TYPE>
+__device__ __forceinline__ void compute_round(const RoundDesc& d, const uint8_t* buf, const uint8_t* xlds,
+                                              float* slots, int K, int nb, int lane) {
+    constexpr int BB = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    const int quad = lane >> 2, q = lane & 3;
+    const Q4Consts c = q4_consts(q);
+    int col = d.col0 + quad;
+    while (col >= nb) col -= nb;
+    const int step = 16 % nb;
+    for (int i = quad; i < d.nblk; i += 16) {
+        Raw r;
+        load_raw_lds<TYPE>(buf, d.delta + i * BB, q, r);
+        const float v = quad_sum(block_dot<MMVQ, TYPE>(r, col, q, c, xlds, K));
+        if (q == 0) slots[d.slot0 + i] = v;
+        col += step;
+        if (col >= nb) col -= nb;
+    }
+}
+
+// Rows of a wave: waves [0, wave_split) (over the whole grid) serve the Q4_K
+// rows, the rest the Q6_K rows; each type's rows are split evenly.
+__device__ __forceinline__ void wave_rows(const StreamArgs& a, int gw, int& g0, int& g1, bool& q4) {
+    q4 = gw < a.wave_split;
+    const int w = q4 ? gw : gw - a.wave_split;
+    const int q = q4 ? a.rows_q[0] : a.rows_q[1], rr = q4 ? a.rows_r[0] : a.rows_r[1];
+    g0 = (q4 ? 0 : a.row_split) + w * q + min(w, rr);
+    g1 = g0 + q + (w < rr ? 1 : 0);
+}
+
+template <int TYPE, int L>
+__device__ __forceinline__ int make_pieces(const StreamArgs& a, int g0, int g1, Piece (&pc)[3]) {
+    constexpr int NB = WGeom<TYPE, L>::NBLK;
+    int nr = 0, slot = 0;
+#pragma unroll
+    for (int s = 0; s < 3; s++) {
+        pc[s].r0 = max(g0, a.row_off[s]) - a.row_off[s];
+        pc[s].r1 = max(min(g1, a.row_off[s + 1]) - a.row_off[s], pc[s].r0);
+        pc[s].slot0 = slot;
+        const int nblk = (pc[s].r1 - pc[s].r0) * a.nb;
+        slot += nblk;
+        pc[s].rounds = (nblk + NB - 1) / NB;
+        nr += pc[s].rounds;
+    }
+    return nr;
+}
+
+// One wave's rows: rounds stream through two register stages and the wave's
+// own LDS buffer; the slots of its rows are added up and stored at the end.
+// Both weight types run the same two workgroup barriers (activation staging).
+template <bool MMVQ, int OUT, int TYPE, int L, int NX>
+__device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int g0, int g1, int lane, int wv,
+                                          uint16_t* res_lds, int wg_g0) {
+    const int nb = a.nb, K = a.K;
+    Piece pc[3];
+    const int nr = make_pieces<TYPE, L>(a, g0, g1, pc);
+    u32x4 R0[L], R1[L];
+    {
+        // activation (and residual) loads first, on every wave, then a barrier,
+        // then the weight loads: the CU's memory pipeline returns them first
+        const int nch = K / 8;
+        u32x4 xv[NX];
+#pragma unroll
+        for (int i = 0; i < NX; i++) {
+            const int c = (int)threadIdx.x + ST_T * i;
+            xv[i] = *(const u32x4*)(a.x + 8 * (c < nch ? c : 0));
+        }
+        uint16_t rv = 0;
+        const int nres = OUT == OUT_ADD ? min(a.wg_rows, a.row_off[3] - wg_g0) : 0;   // nres <= ST_T
+        if (OUT == OUT_ADD && (int)threadIdx.x < nres) rv = a.seg[0].res[wg_g0 + threadIdx.x];
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        issue_round<L>(round_desc<TYPE, L>(a, pc, 0), R0, lane);
+        issue_round<L>(round_desc<TYPE, L>(a, pc, 1), R1, lane);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NX; i++) {
+            const int c = (int)threadIdx.x + ST_T * i;
+            if (MMVQ) xstage_q8_1(xv[i], c, K, lds);
+            else      xstage_f16(xv[i], c, K, lds);
+        }
+        // K beyond NX chunks per lane (K > 10240): the rest after the weights
+        for (int c0 = NX * ST_T; c0 < nch; c0 += NX * ST_T) {
+#pragma unroll
+            for (int i = 0; i < NX; i++) {
+                const int c = c0 + (int)threadIdx.x + ST_T * i;
+                xv[i] = *(const u32x4*)(a.x + 8 * (c < nch ? c : 0));
+            }
+#pragma unroll
+            for (int i = 0; i < NX; i++) {
+                const int c = c0 + (int)threadIdx.x + ST_T * i;
+                if (MMVQ) xstage_q8_1(xv[i], c, K, lds);
+                else      xstage_f16(xv[i], c, K, lds);
+            }
+        }
+        if (OUT == OUT_ADD && (int)threadIdx.x < nres) res_lds[threadIdx.x] = rv;
+    }
+    // LDS-only barrier: the weight loads in flight are not waited for
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    const uint8_t* xlds = lds;
+    uint8_t* buf = lds + a.xlds_bytes + wv * (64 * 16 * L);
+    float* slots = (float*)(lds + a.xlds_bytes + ST_W * (64 * 16 * L)) + wv * a.slots_per_wave;
+    // Round r travels in register stage r mod 2.  Step k: compute round k
+    // from the wave's LDS buffer, move round k+1 from its registers into the
+    // buffer, and reuse those registers for round k+3 (round k+2 stays in
+    // flight in the other stage).  Descriptors are recomputed where needed
+    // (scalar arithmetic) rather than kept per stage.
+    write_round<L>(buf, R0, lane);
+    __builtin_amdgcn_wave_barrier();
+    issue_round<L>(round_desc<TYPE, L>(a, pc, 2), R0, lane);
+    auto step = [&](int k, u32x4 (&nxt)[L]) {
+        compute_round<MMVQ, TYPE>(round_desc<TYPE, L>(a, pc, k), buf, xlds, slots, K, nb, lane);
+        __builtin_amdgcn_wave_barrier();
+        write_round<L>(buf, nxt, lane);
+        __builtin_amdgcn_wave_barrier();
+        issue_round<L>(round_desc<TYPE, L>(a, pc, k + 3), nxt, lane);
+    };
+    int k = 0;
+    for (; k + 2 <= nr; k += 2) {
+        step(k, R1);
+        step(k + 1, R0);
+    }
+    if (k < nr) step(k, R1);
+    // rows: 8 lanes per row add the row's slots (lane j the blocks b = j mod 8,
+    // in order), then a fixed butterfly
+    const int nrow = g1 - g0, j = lane & 7;
+    for (int t0 = 0; t0 < nrow; t0 += 8) {
+        const int t = t0 + (lane >> 3);
+        float v = 0.0f;
+        if (t < nrow) {
+            const float* p = slots + t * nb;
+            for (int b = j; b < nb; b += 8) v += p[b];
+        }
+        v += dpp_x1(v);
+        v += dpp_x2(v);
+        v += __shfl_xor(v, 4, 64);
+        if (j == 0 && t < nrow) {
+            const int g = g0 + t;
+            const int s = g >= a.row_off[1] ? (g >= a.row_off[2] ? 2 : 1) : 0;
+            store_row<OUT>(a.seg[s], g - a.row_off[s], v, res_lds, g - wg_g0);
+        }
+    }
+}
+
+// Pin a uniform value into SGPRs here (kernel-argument loads are otherwise
+// issued lazily, one dependent round trip at a time).
+template <class T>
+__device__ __forceinline__ void pin_sgpr(const T& v) { asm volatile("" :: "s"(v)); }
+
+template <bool MMVQ, int OUT, int L, int NX>
+__global__ __launch_bounds__(ST_T) __attribute__((amdgpu_waves_per_eu(4)))
+void gemv_stream_kernel(StreamArgs a_in) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    StreamArgs a = a_in;
+#pragma unroll
+    for (int i = 0; i < 3; i++) pin_sgpr(a.seg[i].W);
+#pragma unroll
+    for (int i = 0; i < 4; i++) pin_sgpr(a.row_off[i]);
+    pin_sgpr(a.x); pin_sgpr(a.K); pin_sgpr(a.nb); pin_sgpr(a.xlds_bytes); pin_sgpr(a.row_split); pin_sgpr(a.wave_split);
+    pin_sgpr(a.slots_per_wave);
+#pragma unroll
+    for (int i = 0; i < 2; i++) { pin_sgpr(a.rows_q[i]); pin_sgpr(a.rows_r[i]); }
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int gw = blockIdx.x * ST_W + wv;
+    int g0, g1;
+    bool q4;
+    wave_rows(a, gw, g0, g1, q4);
+    // rows of the whole workgroup (for the staged residual): waves are in row order per type
+    int wg_g0 = 0;
+    if (OUT == OUT_ADD) {
+        int h0, h1; bool hq;
+        wave_rows(a, blockIdx.x * ST_W, h0, h1, hq);
+        wg_g0 = h0;
+    }
+    uint16_t* res_lds = (uint16_t*)(lds + a.xlds_bytes + ST_W * (64 * 16 * L) + ST_W * 4 * a.slots_per_wave);
+    // (both bodies hold the same two workgroup barriers)
+    if (q4) wave_body<MMVQ, OUT, TYPE_Q4_K, L, NX>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
+    else    wave_body<MMVQ, OUT, TYPE_Q6_K, L, NX>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
+}
+
+template <bool MMVQ, int OUT, int L, int NX>
+static hipError_t launch_s(const StreamArgs& a, int grid, size_t lds, hipStream_t st) {
+    static const hipError_t attr = hipFuncSetAttribute((const void*)gemv_stream_kernel<MMVQ, OUT, L, NX>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((gemv_stream_kernel<MMVQ, OUT, L, NX>), dim3(grid), dim3(ST_T), lds, st, a);
     return hipGetLastError();
 }
 
-hipError_t gemv_launch(const GemvArgs& a_in, bool mmvq, int out_kind, int lpr_override, hipStream_t st) {
-    GemvArgs a = a_in;
-    // Q4_K segments first (stable), then Q6_K; unused slots are empty copies.
-    {
-        GemvSeg tmp[3];
-        int n = 0;
-        for (int i = 0; i < a.nseg; i++) if (a.seg[i].type == TYPE_Q4_K) tmp[n++] = a.seg[i];
-        for (int i = 0; i < a.nseg; i++) if (a.seg[i].type != TYPE_Q4_K) tmp[n++] = a.seg[i];
-        for (int i = 0; i < a.nseg; i++) a.seg[i] = tmp[i];
+template <bool MMVQ, int OUT, int L>
+static hipError_t launch_nx(const StreamArgs& a, int grid, size_t lds, hipStream_t st) {
+    const int nch = a.K / 8;
+    if (nch <= ST_T) return launch_s<MMVQ, OUT, L, 1>(a, grid, lds, st);
+    if (nch <= 2 * ST_T) return launch_s<MMVQ, OUT, L, 2>(a, grid, lds, st);
+    return launch_s<MMVQ, OUT, L, 5>(a, grid, lds, st);
+}
+
+static constexpr size_t LDS_CU = 160 * 1024;
+#ifndef JLLM_GEMV_WG_PER_CU
+#define JLLM_GEMV_WG_PER_CU 4
+#endif
+constexpr int ST_L = 4;
+
+hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t st) {
+    if (out_kind == OUT_ADD && in.nseg != 1) return hipErrorInvalidValue;
+    StreamArgs a;
+    a.K = in.K;
+    a.x = in.x;
+    a.nb = in.K / QK_K;
+    // Q4_K segments first, then Q6_K (stable); unused slots are empty
+    int n = 0;
+    for (int i = 0; i < in.nseg; i++) if (in.seg[i].type == TYPE_Q4_K) a.seg[n++] = in.seg[i];
+    const int nseg4 = n;
+    for (int i = 0; i < in.nseg; i++) if (in.seg[i].type != TYPE_Q4_K) a.seg[n++] = in.seg[i];
+    for (int i = n; i < 3; i++) { a.seg[i] = a.seg[n - 1]; a.seg[i].M = 0; }
+    a.row_off[0] = 0;
+    for (int i = 0; i < 3; i++) a.row_off[i + 1] = a.row_off[i] + a.seg[i].M;
+    const int64_t rows4 = a.row_off[nseg4], rows6 = a.row_off[3] - rows4;
+    if (rows4 + rows6 <= 0) return hipSuccess;
+    a.row_split = (int)rows4;
+    const int64_t bytes4 = rows4 * a.nb * Q4K_BYTES, bytes6 = rows6 * a.nb * Q6K_BYTES;
+    a.xlds_bytes = (int)((gemv_lds_bytes(mmvq, a.K) + 15) & ~(size_t)15);
+    const size_t wbuf = ST_W * (size_t)(64 * 16 * ST_L);
+    // waves: ST_W per workgroup, JLLM_GEMV_WG_PER_CU workgroups per CU when
+    // LDS allows; split between the types by bytes
+    int64_t grid = 0;
+    int64_t w4 = 0, w6 = 0, max_rows = 0;
+    auto split = [&](int64_t g) {
+        const int64_t w = g * ST_W;
+        if (rows6 == 0) { w4 = w; w6 = 0; }
+        else if (rows4 == 0) { w4 = 0; w6 = w; }
+        else {
+            w4 = (w * bytes4 + (bytes4 + bytes6) / 2) / (bytes4 + bytes6);
+            w4 = w4 < 1 ? 1 : (w4 > w - 1 ? w - 1 : w4);
+            w6 = w - w4;
+        }
+        max_rows = std::max(w4 ? (rows4 + w4 - 1) / w4 : 0, w6 ? (rows6 + w6 - 1) / w6 : 0);
+    };
+    auto lds_of = [&]() {
+        const size_t res = out_kind == OUT_ADD ? (size_t)ST_W * max_rows * 2 : 0;
+        return (size_t)a.xlds_bytes + wbuf + (size_t)ST_W * 4 * max_rows * a.nb + res;
+    };
+    // (the residual rows of a workgroup are staged one per lane)
+    auto fits = [&](int per_cu) { return (size_t)per_cu * lds_of() <= LDS_CU && !(out_kind == OUT_ADD && ST_W * max_rows > ST_T); };
+    for (int per_cu = JLLM_GEMV_WG_PER_CU; per_cu >= 1 && grid == 0; per_cu--) {
+        split((int64_t)device_cus() * per_cu);
+        if (fits(per_cu)) grid = (int64_t)device_cus() * per_cu;
     }
-    int64_t rows = 0;
-    for (int i = 0; i < a.nseg; i++) rows += a.seg[i].M;
-    for (int i = a.nseg; i < 3; i++) { a.seg[i] = a.seg[a.nseg - 1]; a.seg[i].M = 0; }
-    if (rows <= 0) return hipSuccess;
-    const int nb = a.K / QK_K;
-    const int waves_per_cu = JLLM_GEMV_WAVES_PER_CU;
-    const int64_t resident = (int64_t)device_cus() * waves_per_cu;
-    const int lpr = lpr_override ? lpr_override : pick_lpr(rows, nb, resident);
-    const int rpw = 64 / lpr, nq = lpr / 4;
-    int g = 0;
-    for (int i = 0; i < 3; i++) { g += (a.seg[i].M + rpw - 1) / rpw; a.gend[i] = g; }
-    a.lpr = lpr;
-    bool any_q6 = false;
-    for (int i = 0; i < a.nseg; i++) any_q6 |= a.seg[i].type == TYPE_Q6_K;
-    int per_q = (nb + nq - 1) / nq;
-    if (any_q6 && nq > 1 && (per_q & 1)) per_q++;
-    a.per_q = per_q;
-    int g4 = 0;
-    int64_t bytes4 = 0, bytes6 = 0;
-    for (int i = 0; i < 3; i++) {
-        if (a.seg[i].type == TYPE_Q4_K) { g4 = a.gend[i]; bytes4 += (int64_t)a.seg[i].M * nb * Q4K_BYTES; }
-        else bytes6 += (int64_t)a.seg[i].M * nb * Q6K_BYTES;
+    if (grid == 0) {      // rows too many for one resident grid: more workgroups, in several waves
+        grid = device_cus();
+        split(grid);
+        while (!fits(1)) {
+            if (grid > (int64_t)1 << 24) return hipErrorInvalidValue;
+            split(grid *= 2);
+        }
     }
-    a.g_split = g4;
-    const int64_t waves = g < resident ? g : resident;
-    int grid = (int)((waves + 3) / 4);
-    if (bytes4 > 0 && bytes6 > 0) {
-        // split the workgroups in proportion to the bytes each type streams
-        if (grid < 2) grid = 2;
-        int w4 = (int)((grid * bytes4 + (bytes4 + bytes6) / 2) / (bytes4 + bytes6));
-        w4 = w4 < 1 ? 1 : (w4 > grid - 1 ? grid - 1 : w4);
-        const int gq4 = (g4 + 3) / 4, gq6 = (g - g4 + 3) / 4;        // WGs needed at one group per wave
-        if (w4 > gq4) w4 = gq4;
-        if (grid - w4 > gq6) grid = w4 + gq6;
-        a.wg_split = w4;
-    } else {
-        a.wg_split = bytes4 > 0 ? grid : 0;
-    }
-    const size_t lds = gemv_lds_bytes(mmvq, a.K);
+    a.wave_split = (int)w4;
+    a.rows_q[0] = w4 > 0 ? (int)(rows4 / w4) : 0; a.rows_r[0] = w4 > 0 ? (int)(rows4 % w4) : 0;
+    a.rows_q[1] = w6 > 0 ? (int)(rows6 / w6) : 0; a.rows_r[1] = w6 > 0 ? (int)(rows6 % w6) : 0;
+    a.slots_per_wave = (int)(max_rows * a.nb);
+    a.wg_rows = (int)(ST_W * max_rows);
+    const size_t lds = lds_of();
+    const int g = (int)grid;
     if (mmvq) {
-        if (out_kind == OUT_HALF) return launch_k<true, OUT_HALF>(a, grid, lds, st);
-        if (out_kind == OUT_F32)  return launch_k<true, OUT_F32>(a, grid, lds, st);
-        return launch_k<true, OUT_ADD>(a, grid, lds, st);
+        if (out_kind == OUT_HALF) return launch_nx<true, OUT_HALF, ST_L>(a, g, lds, st);
+        if (out_kind == OUT_F32)  return launch_nx<true, OUT_F32, ST_L>(a, g, lds, st);
+        return launch_nx<true, OUT_ADD, ST_L>(a, g, lds, st);
     }
-    if (out_kind == OUT_HALF) return launch_k<false, OUT_HALF>(a, grid, lds, st);
-    if (out_kind == OUT_F32)  return launch_k<false, OUT_F32>(a, grid, lds, st);
-    return launch_k<false, OUT_ADD>(a, grid, lds, st);
+    if (out_kind == OUT_HALF) return launch_nx<false, OUT_HALF, ST_L>(a, g, lds, st);
+    if (out_kind == OUT_F32)  return launch_nx<false, OUT_F32, ST_L>(a, g, lds, st);
+    return launch_nx<false, OUT_ADD, ST_L>(a, g, lds, st);
 }
 
 hipError_t quantize_q8_1_aos_launch(const uint16_t* x, void* y, int K, hipStream_t st) {
