@@ -18,6 +18,7 @@ struct AttnArgs {
     float scale;
 };
 
+constexpr int ATTN_MAX_SPLITS = 256;
 int attn_splits(int seq_len, int n_kv);
 size_t attn_partials_floats(int n_heads, int n_splits, int head_dim);
 // Scratch layout: ATTN_COUNTER_BYTES of per-KV-head counters (fixed offset,

@@ -30,11 +30,13 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2a __attribute__((ext_vector_type(2)));
 typedef float f32x4a __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int AT_KEYS = 32;          // keys per tile (one MFMA column block)
 constexpr int AT_MAXHD = 128;
 constexpr int AT_MAXG = 16;          // max query heads per KV head
-constexpr int AT_MAXS = 128;         // max splits
+constexpr int AT_MAXS = ATTN_MAX_SPLITS;   // max splits
 
 // 4 signed int8 (one word) -> 4 exact fp16 values (two words): with u = b ^ 0x80
 // in [1, 255], the half with bits 0x6400 + u is 1024 + u, minus 1152 gives b.
@@ -59,12 +61,13 @@ __device__ __forceinline__ h8 kv8_to_h8(const uint8_t* p) {
 }
 
 int attn_splits(int seq_len, int n_kv) {
-    // one wave per (KV head, split), at least 128 keys (four 32-key tiles)
-    // per split, at most AT_MAXS splits
+    // one wave per (KV head, split): at least 32 keys (one tile) per split,
+    // at most 128 splits (measured on MI355X: short splits keep every SIMD
+    // busy; past 128 the partials and the reduce cost more than they save)
     (void)n_kv;
     if (seq_len <= 0) return 1;
-    const int s = (seq_len + 127) / 128;
-    return s < AT_MAXS ? s : AT_MAXS;
+    const int s = (seq_len + 31) / 32;
+    return s < 128 ? s : 128;
 }
 
 size_t attn_partials_floats(int n_heads, int n_splits, int head_dim) {
@@ -77,27 +80,34 @@ size_t attn_scratch_bytes(int n_heads, int n_splits, int head_dim) {
 
 __host__ __device__ size_t attn_lds_bytes(int n_heads, int n_kv, int head_dim) {
     const int G = n_heads / n_kv;
-    const size_t tile = (size_t)AT_KEYS * head_dim + 32 * AT_KEYS * 2;   // V tile (int8 max) + P rows
-    const size_t outb = (size_t)2 * G * head_dim * 4;
-    return (tile * 2 > outb ? tile * 2 : outb) + 96 * 4;              // fp16 V needs 2x; + corr/ks/vs
+    const size_t loop = (size_t)32 * AT_KEYS * 2 + 96 * 4;            // P' rows (fp16) + corr/ks/vs
+    const size_t outb = (size_t)2 * G * head_dim * 4;                 // final hi/lo rows (fp32)
+    return loop > outb ? loop : outb;
 }
 
 // One wave per (KV head, split).  Lane (li = lane & 31, lg = lane >> 5).
-//   Q.K^T : A = q   (rows = query heads of the group, K = d)
-//           B = K^T (cols = the tile's 32 keys, K = d); lane group lg
-//               covers d in [lg*hd/2, (lg+1)*hd/2), 8 at a time
-//   P.V   : A = P'  (rows = heads, high parts then low parts; K = keys)
-//           B = V   (cols = 32 d, K = keys) read as columns from LDS
+//   Q.K^T : C = K.q^T (rows = the tile's 32 keys, cols = query heads, K = d);
+//           lane group lg covers d in [lg*hd/2, (lg+1)*hd/2), 8 at a time
+//   V^T   : the V rows are turned into columns on the matrix cores: with A =
+//           V rows (K = d) and B = the identity, C = V lands in the MFMA
+//           output layout, i.e. lane (d = li, lg) holds 16 keys of column d
+//           (int8: one v_mfma_i32_32x32x32_i8 per 32 d, exact)
+//   P.V   : A = P'  (rows = heads, high parts then low parts; K = keys in the
+//           order the transpose delivers them), B = those V columns
 // The K and V rows of the next tile are loaded into registers while the
 // current tile is computed.
-template <bool INT8>
+template <bool INT8, int HD>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_partial_kernel(AttnArgs a) {
     constexpr int EB = INT8 ? 1 : 2;
-    constexpr int RW = AT_MAXHD * EB / 2 / 16;          // 16-byte chunks per lane per row half
+    constexpr int hd = HD, half = HD / 2;
+    constexpr int KW = (half * EB + 15) / 16;           // K: 16-byte chunks per lane (half a row)
+    constexpr int NDT = HD / 32;                        // 32-wide d chunks
+    constexpr int VW = NDT * EB;                        // V: 16-byte chunks per lane
+    constexpr int NST = half / 8;                       // Q.K^T MFMA steps
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int kvh = blockIdx.x, split = blockIdx.y;
-    const int G = a.n_heads / a.n_kv, hd = a.head_dim, half = hd / 2;
+    const int G = a.n_heads / a.n_kv;
     const int l = threadIdx.x, li = l & 31, lg = l >> 5;
     const int kv_dim = a.n_kv * a.cache_head_dim, hoff = kvh * a.cache_head_dim;
     const int lo_pos = a.window > 0 ? max(0, a.seq - a.window) : 0;
@@ -107,72 +117,76 @@ void attn_partial_kernel(AttnArgs a) {
     const int kv0 = lo_pos + split * per;
     const int kv1 = min(kv0 + per, a.seq);
 
-    uint8_t* sV = smem;                                          // [32 keys][hd] elements
-    _Float16* sP = (_Float16*)(smem + AT_KEYS * AT_MAXHD * EB);   // [32 rows][32 keys]
-    float* sMisc = (float*)(smem + attn_lds_bytes(a.n_heads, a.n_kv, hd) - 96 * 4);   // corr[32] | ks[32] | vs[32]
+    _Float16* sP = (_Float16*)smem;                              // [32 rows][32 keys]
+    float* sMisc = (float*)(smem + 32 * AT_KEYS * 2);            // corr[32] | ks[32] | vs[32]
 
     // q operand: lane (head li, lg), step st -> d = lg*half + 8*st + [0, 8)
-    h8 qa[AT_MAXHD / 16];
+    h8 qa[NST];
 #pragma unroll
-    for (int st = 0; st < AT_MAXHD / 16; st++) {
-        if (8 * st < half && li < G)
-            qa[st] = __builtin_bit_cast(h8, *(const u32x4a*)(a.q + (int64_t)(kvh * G + li) * hd + lg * half + 8 * st));
-        else
-            qa[st] = h8{};
-    }
+    for (int st = 0; st < NST; st++)
+        qa[st] = li < G ? __builtin_bit_cast(h8, *(const u32x4a*)(a.q + (int64_t)(kvh * G + li) * hd + lg * half + 8 * st))
+                        : h8{};
     for (int i = l; i < 32 * AT_KEYS; i += 64) sP[i] = (_Float16)0.0f;
+
+    // identity operands of the V transpose.  int8: lane (col li, lg) holds
+    // B[16lg + i][li] = (16lg + i == li).  fp16: two K = 16 halves, lane
+    // (col li, lg) holds B_hh[8lg + e][li] = (16hh + 8lg + e == li).
+    i32x4 eye8;
+    h8 eyeh[2];
+    {
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+        const int pos = li - 16 * lg;
+        if (pos >= 0 && pos < 16) w[pos >> 2] = 1u << (8 * (pos & 3));
+        eye8 = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) eyeh[hh][e] = (_Float16)((16 * hh + 8 * lg + e == li) ? 1.0f : 0.0f);
+    }
 
     // running softmax state of head li (meaningful in lanes li < G; both
     // lane halves keep identical copies)
     float run_m = -FLT_MAX, run_l = 0.0f;
-    constexpr int NDT = AT_MAXHD / 32;
     f32x16 acc[NDT];
 #pragma unroll
     for (int i = 0; i < NDT; i++) acc[i] = f32x16{};
 
-    // raw rows of one tile: lane (li, lg) holds K[key li][lg half] and V[key li][lg half]
-    u32x4a rk[RW], rv[RW];
+    // raw rows of one tile: lane (li, lg) holds K[key li][lg half] and the V
+    // pieces of key li its lane group feeds to the transpose: int8
+    // V[32m + 16lg, +16); fp16 V[32m + 8lg, +8) and V[32m + 16 + 8lg, +8)
+    u32x4a rk[KW], rv[VW];
     float ksn = 1.0f, vsn = 1.0f;
-    auto load_tile = [&](int p0, u32x4a (&k_)[RW], u32x4a (&v_)[RW], float& ks_, float& vs_) {
+    auto load_tile = [&](int p0, u32x4a (&k_)[KW], u32x4a (&v_)[VW], float& ks_, float& vs_) {
         const int pos = min(p0 + li, kv1 - 1);
         const uint8_t* kr = (const uint8_t*)a.k + ((int64_t)pos * kv_dim + hoff + lg * half) * EB;
-        const uint8_t* vr = (const uint8_t*)a.v + ((int64_t)pos * kv_dim + hoff + lg * half) * EB;
+        const uint8_t* vr = (const uint8_t*)a.v + ((int64_t)pos * kv_dim + hoff) * EB;
 #pragma unroll
-        for (int c = 0; c < RW; c++) {
-            if (c * 16 < half * EB) {
-                k_[c] = *(const u32x4a*)(kr + 16 * c);
-                v_[c] = *(const u32x4a*)(vr + 16 * c);
+        for (int c = 0; c < KW; c++) k_[c] = *(const u32x4a*)(kr + 16 * c);
+#pragma unroll
+        for (int m = 0; m < NDT; m++) {
+            if (INT8) {
+                v_[m] = *(const u32x4a*)(vr + 32 * m + 16 * lg);
+            } else {
+                v_[2 * m] = *(const u32x4a*)(vr + (32 * m + 8 * lg) * 2);
+                v_[2 * m + 1] = *(const u32x4a*)(vr + (32 * m + 16 + 8 * lg) * 2);
             }
         }
         ks_ = (INT8 && a.ks) ? a.ks[(int64_t)pos * a.n_kv + kvh] : 1.0f;
         vs_ = (INT8 && a.vs) ? a.vs[(int64_t)pos * a.n_kv + kvh] : 1.0f;
     };
 
-    if (kv0 < kv1) load_tile(kv0, rk, rv, ksn, vsn);
-    for (int p0 = kv0; p0 < kv1; p0 += AT_KEYS) {
+    // one tile from the registers (ck, cv; key scales ksc, vsc of key li)
+    auto tile = [&](int p0, const u32x4a (&ck)[KW], const u32x4a (&cv)[VW], float ksc, float vsc) {
         const int n = min(AT_KEYS, kv1 - p0);
-        u32x4a ck[RW], cv[RW];
-#pragma unroll
-        for (int c = 0; c < RW; c++) { ck[c] = rk[c]; cv[c] = rv[c]; }
-        const float ksc = ksn * a.scale, vsc = vsn;   // scales of key li (this lane's load)
-        if (p0 + AT_KEYS < kv1) load_tile(p0 + AT_KEYS, rk, rv, ksn, vsn);
-
-        // V rows -> LDS (read back as columns below)
-#pragma unroll
-        for (int c = 0; c < RW; c++)
-            if (c * 16 < half * EB) *(u32x4a*)(sV + (li * hd + lg * half) * EB + 16 * c) = cv[c];
-
         // 1. transposed scores: C = K.q^T, lane li = head, rows = keys
         //    8*(v/4) + 4*lg + v%4 (v = 0..15): each lane holds 16 of the tile's
         //    32 keys for its head, the other 16 are in lane li ^ 32.
         f32x16 sc = {};
 #pragma unroll
-        for (int st = 0; st < AT_MAXHD / 16; st++) {
-            if (8 * st < half) {
-                const uint8_t* kb8 = (const uint8_t*)&ck[(8 * st * EB) / 16] + (8 * st * EB) % 16;
-                const h8 kb = kv8_to_h8<INT8>(kb8);
-                sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kb, qa[st], sc, 0, 0, 0);
-            }
+        for (int st = 0; st < NST; st++) {
+            const uint8_t* kb8 = (const uint8_t*)&ck[(8 * st * EB) / 16] + (8 * st * EB) % 16;
+            const h8 kb = kv8_to_h8<INT8>(kb8);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kb, qa[st], sc, 0, 0, 0);
         }
         // per-key scales: lane li (lg = 0) loaded key li's; through LDS to the
         // lanes that hold that key's scores (keys 8m + 4lg + [0,4))
@@ -225,44 +239,67 @@ void attn_partial_kernel(AttnArgs a) {
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);           // lgkmcnt(0): this wave's LDS writes are visible
         __builtin_amdgcn_wave_barrier();
-        // 3. acc = acc * corr + P'.V
+        // 3. acc = acc * corr + P'.V.  The transpose delivers keys
+        //    8*(v/4) + 4lg + v%4 in element v; MFMA step st takes v = 8st..8st+7,
+        //    so P' is read at keys 16st + 4lg + [0,4) and 16st + 8 + 4lg + [0,4).
         float cr[16];
 #pragma unroll
         for (int vv = 0; vv < 16; vv++) {
             const int r = 8 * (vv >> 2) + 4 * lg + (vv & 3);
             cr[vv] = r < 2 * G ? sMisc[r < G ? r : r - G] : 1.0f;
         }
+        h8 pa[2];
+#pragma unroll
+        for (int st = 0; st < 2; st++) {
+            const u32x2a lo4 = *(const u32x2a*)&sP[li * AT_KEYS + 16 * st + 4 * lg];
+            const u32x2a hi4 = *(const u32x2a*)&sP[li * AT_KEYS + 16 * st + 8 + 4 * lg];
+            pa[st] = __builtin_bit_cast(h8, u32x4a{lo4.x, lo4.y, hi4.x, hi4.y});
+        }
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
-            if (32 * dt < hd) {
+            {
+                float vt[16];                            // V[key 8(v/4)+4lg+v%4][32dt + li]
+                if (INT8) {
+                    const i32x16 ct = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, cv[dt]), eye8,
+                                                                             i32x16{}, 0, 0, 0);
+#pragma unroll
+                    for (int vv = 0; vv < 16; vv++) vt[vv] = (float)ct[vv];
+                } else {
+                    f32x16 ct = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8, cv[2 * dt]), eyeh[0],
+                                                                      f32x16{}, 0, 0, 0);
+                    ct = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8, cv[2 * dt + 1]), eyeh[1], ct, 0, 0, 0);
+#pragma unroll
+                    for (int vv = 0; vv < 16; vv++) vt[vv] = ct[vv];
+                }
 #pragma unroll
                 for (int vv = 0; vv < 16; vv++) acc[dt][vv] *= cr[vv];
-                const int d = 32 * dt + li;
 #pragma unroll
-                for (int st = 0; st < AT_KEYS / 16; st++) {
-                    const int k0 = 16 * st + 8 * lg;
-                    const h8 pa = *(const h8*)&sP[li * AT_KEYS + k0];
+                for (int st = 0; st < 2; st++) {
                     h8 vb;
-                    if (INT8) {
-                        const uint8_t* col = sV + d;
-                        uint32_t w0 = 0, w1 = 0;
 #pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            w0 |= (uint32_t)col[(k0 + e) * hd] << (8 * e);
-                            w1 |= (uint32_t)col[(k0 + 4 + e) * hd] << (8 * e);
-                        }
-                        const u32x2a lo = i8x4_to_h4(w0), hi = i8x4_to_h4(w1);
-                        vb = __builtin_bit_cast(h8, u32x4a{lo.x, lo.y, hi.x, hi.y});
-                    } else {
-                        const _Float16* col = (const _Float16*)sV + d;
-#pragma unroll
-                        for (int e = 0; e < 8; e++) vb[e] = col[(k0 + e) * hd];
+                    for (int e = 0; e < 8; e += 2) {
+                        const auto h2 = __builtin_amdgcn_cvt_pkrtz(vt[8 * st + e], vt[8 * st + e + 1]);   // exact
+                        vb[e] = h2[0];
+                        vb[e + 1] = h2[1];
                     }
-                    acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, vb, acc[dt], 0, 0, 0);
+                    acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[st], vb, acc[dt], 0, 0, 0);
                 }
             }
         }
         __builtin_amdgcn_wave_barrier();
+    };
+    // the next tile's rows load into (rk, rv) while the current one (a copy)
+    // is computed
+    if (kv0 < kv1) load_tile(kv0, rk, rv, ksn, vsn);
+    for (int p0 = kv0; p0 < kv1; p0 += AT_KEYS) {
+        u32x4a ck[KW], cv[VW];
+#pragma unroll
+        for (int c = 0; c < KW; c++) ck[c] = rk[c];
+#pragma unroll
+        for (int c = 0; c < VW; c++) cv[c] = rv[c];
+        const float ksc = ksn * a.scale, vsc = vsn;
+        if (p0 + AT_KEYS < kv1) load_tile(p0 + AT_KEYS, rk, rv, ksn, vsn);
+        tile(p0, ck, cv, ksc, vsc);
     }
 
     // 4. unnormalised partials: m, l per head; acc = high rows + low rows
@@ -275,15 +312,14 @@ void attn_partial_kernel(AttnArgs a) {
         pl[(int64_t)(pbase + li) * S + split] = run_l;
     }
     float* sO = (float*)smem;                                  // [2G][hd]
+    __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int dt = 0; dt < NDT; dt++) {
-        if (32 * dt < hd) {
 #pragma unroll
-            for (int vv = 0; vv < 16; vv++) {
-                const int r = 8 * (vv >> 2) + 4 * lg + (vv & 3);
-                if (r < 2 * G) sO[r * hd + 32 * dt + li] = acc[dt][vv];
-            }
+        for (int vv = 0; vv < 16; vv++) {
+            const int r = 8 * (vv >> 2) + 4 * lg + (vv & 3);
+            if (r < 2 * G) sO[r * hd + 32 * dt + li] = acc[dt][vv];
         }
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
@@ -295,58 +331,89 @@ void attn_partial_kernel(AttnArgs a) {
 }
 
 // out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M), M = max_s m_s
-// (flash_decode_reduce_kernel, attention.cu:944-969).  One workgroup per head;
-// the split weights are computed once in LDS, then every output element
-// issues its S partial loads together.
-__global__ __launch_bounds__(128)
+// (flash_decode_reduce_kernel, attention.cu:944-969).  One workgroup of 8
+// waves per head: the split weights go to LDS, then wave w sums the splits
+// s = w, w + 8, ... for two d per lane (all its partial loads in flight at
+// once), and the 8 wave sums are added in a fixed order.
+constexpr int AT_RED_THREADS = 512;
+__global__ __launch_bounds__(AT_RED_THREADS)
 void attn_reduce_kernel(uint16_t* __restrict__ out, const float* __restrict__ part, int n_heads, int hd, int S) {
     __shared__ float sW[AT_MAXS];
-    __shared__ float sInv;
-    const int h = blockIdx.x, t = threadIdx.x;
+    __shared__ float sRed[AT_RED_THREADS / 64];
+    __shared__ float sSum[AT_RED_THREADS / 64][AT_MAXHD];
+    const int h = blockIdx.x, t = threadIdx.x, w = t >> 6, l = t & 63;
     const float* pm = part + (int64_t)h * S;
     const float* pl = part + (int64_t)n_heads * S + (int64_t)h * S;
     const float* pacc = part + (int64_t)n_heads * S * 2 + (int64_t)h * S * hd;
-    __shared__ float sRed[2];
-    // blockDim.x == AT_MAXS == 128: thread t owns split t
     const float m = t < S ? pm[t] : -FLT_MAX;
     const float lv = t < S ? pl[t] : 0.0f;
     float mx = m;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    if ((t & 63) == 0) sRed[t >> 6] = mx;
+    if (l == 0) sRed[w] = mx;
     __syncthreads();
-    mx = fmaxf(sRed[0], sRed[1]);
+    mx = sRed[0];
+#pragma unroll
+    for (int i = 1; i < AT_RED_THREADS / 64; i++) mx = fmaxf(mx, sRed[i]);
     const float wgt = t < S ? expf(m - mx) : 0.0f;
-    sW[t] = wgt;
+    if (t < AT_MAXS) sW[t] = wgt;
     float L = lv * wgt;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
     __syncthreads();
-    if ((t & 63) == 0) sRed[t >> 6] = L;
+    if (l == 0) sRed[w] = L;
     __syncthreads();
-    if (t == 0) { const float Lt = sRed[0] + sRed[1]; sInv = Lt > 0.0f ? 1.0f / Lt : 0.0f; }
-    __syncthreads();
-    for (int d = t; d < hd; d += blockDim.x) {
-        float o = 0.0f;
-        for (int s0 = 0; s0 < S; s0 += 16) {
-            float pv[16];
+    float Lt = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 16; i++) pv[i] = s0 + i < S ? pacc[(int64_t)(s0 + i) * hd + d] : 0.0f;
+    for (int i = 0; i < AT_RED_THREADS / 64; i++) Lt += sRed[i];
+    const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
+    // wave w: splits w, w+8, ...; lane l: d = 2l, 2l+1
+    constexpr int NW = AT_RED_THREADS / 64;
+    constexpr int MAXPER = AT_MAXS / NW;
+    float2 o = make_float2(0.0f, 0.0f);
+    if (2 * l < hd) {
+        float2 pv[MAXPER];
 #pragma unroll
-            for (int i = 0; i < 16; i++) o += pv[i] * sW[min(s0 + i, AT_MAXS - 1)];
+        for (int i = 0; i < MAXPER; i++) {
+            const int sp = w + NW * i;
+            pv[i] = sp < S ? *(const float2*)(pacc + (int64_t)sp * hd + 2 * l) : make_float2(0.0f, 0.0f);
         }
-        out[(int64_t)h * hd + d] = f32_to_f16_bits(o * sInv);
+#pragma unroll
+        for (int i = 0; i < MAXPER; i++) {
+            const int sp = w + NW * i;
+            const float wi = sp < S ? sW[sp] : 0.0f;
+            o.x += pv[i].x * wi;
+            o.y += pv[i].y * wi;
+        }
+        sSum[w][2 * l] = o.x;
+        sSum[w][2 * l + 1] = o.y;
+    }
+    __syncthreads();
+    if (t < hd) {
+        float r = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NW; i++) r += sSum[i][t];
+        out[(int64_t)h * hd + t] = f32_to_f16_bits(r * inv);
     }
 }
 
 hipError_t attn_launch(const AttnArgs& a, bool kv_int8, hipStream_t st) {
     dim3 grid(a.n_kv, a.n_splits);
     const size_t lds = attn_lds_bytes(a.n_heads, a.n_kv, a.head_dim);
-    if (kv_int8) hipLaunchKernelGGL(attn_partial_kernel<true>, grid, dim3(64), lds, st, a);
-    else         hipLaunchKernelGGL(attn_partial_kernel<false>, grid, dim3(64), lds, st, a);
+    switch (a.head_dim * 2 + (kv_int8 ? 1 : 0)) {
+    case 64:  hipLaunchKernelGGL((attn_partial_kernel<false, 32>), grid, dim3(64), lds, st, a); break;
+    case 65:  hipLaunchKernelGGL((attn_partial_kernel<true, 32>), grid, dim3(64), lds, st, a); break;
+    case 128: hipLaunchKernelGGL((attn_partial_kernel<false, 64>), grid, dim3(64), lds, st, a); break;
+    case 129: hipLaunchKernelGGL((attn_partial_kernel<true, 64>), grid, dim3(64), lds, st, a); break;
+    case 192: hipLaunchKernelGGL((attn_partial_kernel<false, 96>), grid, dim3(64), lds, st, a); break;
+    case 193: hipLaunchKernelGGL((attn_partial_kernel<true, 96>), grid, dim3(64), lds, st, a); break;
+    case 256: hipLaunchKernelGGL((attn_partial_kernel<false, 128>), grid, dim3(64), lds, st, a); break;
+    case 257: hipLaunchKernelGGL((attn_partial_kernel<true, 128>), grid, dim3(64), lds, st, a); break;
+    default: return hipErrorInvalidValue;
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attn_reduce_kernel, dim3(a.n_heads), dim3(AT_MAXS), 0, st, a.out, (const float*)a.part,
+    hipLaunchKernelGGL(attn_reduce_kernel, dim3(a.n_heads), dim3(AT_RED_THREADS), 0, st, a.out, (const float*)a.part,
                        a.n_heads, a.head_dim, a.n_splits);
     return hipGetLastError();
 }

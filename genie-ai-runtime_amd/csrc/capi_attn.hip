@@ -34,7 +34,7 @@ int attn_run(uint16_t* out, const uint16_t* q, const void* k, const void* v, int
     int st = attn_check(out, q, k, v, n_heads, n_kv, hd, chd, seq, kv_int8, window);
     if (st) return st;
     if (n_splits < 1) n_splits = 1;
-    if (n_splits > 64) n_splits = 64;
+    if (n_splits > ATTN_MAX_SPLITS) n_splits = ATTN_MAX_SPLITS;
     uint8_t* scratch = (uint8_t*)g_part.get(attn_scratch_bytes(n_heads, n_splits, hd));
     if (!scratch) return JLLM_ERR_NOMEM;
     AttnArgs a;

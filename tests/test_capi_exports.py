@@ -69,7 +69,7 @@ def test_mapped_weight_registry():
 
 def test_split_policy_host_only():
     l = jllm.lib()
-    assert [l.jllm_hip_decode_attn_splits(s) for s in (0, 1, 128, 129, 512, 8192, 20000)] == [1, 1, 1, 2, 4, 64, 128]
+    assert [l.jllm_hip_decode_attn_splits(s) for s in (0, 1, 32, 33, 512, 8192, 20000)] == [1, 1, 1, 2, 16, 128, 128]
 
 
 def test_argument_validation_without_gpu():
