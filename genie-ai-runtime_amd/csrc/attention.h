@@ -16,6 +16,10 @@ struct AttnArgs {
     int* counters;            // [n_kv] split-completion counters, zero between calls
     int n_heads, n_kv, head_dim, cache_head_dim, seq, window, n_splits;
     float scale;
+    // query tokens (grid z): token t attends to keys [0, seq + t) and reads
+    // q / writes out at t * n_heads * head_dim.  tokens > 1 needs n_splits 1.
+    int tokens;
+
 };
 
 constexpr int ATTN_MAX_SPLITS = 256;

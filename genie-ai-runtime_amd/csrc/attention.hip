@@ -11,14 +11,22 @@
 // sliding window, positions < seq - window are excluded (they contribute
 // exactly zero in the reference).
 //
-// MI355X mapping: one workgroup per (KV head, split) computes ALL query
-// heads of its GQA group, so each KV byte is read from HBM once.  A 64-key
-// tile of K and V (int8 -> 16 KB) is staged in LDS, the next tile's loads
-// are in flight while the current one is computed.  Q.K^T and P.V run on
-// the matrix cores (v_mfma_f32_32x32x16_f16): int8 keys/values become fp16
-// exactly, q is fp16 already, and the fp32 probabilities (times vs) are
-// split into a high and a low fp16 part stacked as extra rows of the A
-// operand, so the P.V products keep ~22 bits.
+// Prefill (flash_attention_prefill_batched_kernel, attention.cu:382-514)
+// is the same computation per query token t with the causal bound
+// seq = start_pos + t + 1: grid z runs over the tokens, one split each, and
+// the wave writes its normalised output directly (no partials, no reduce);
+// a decode call with a single split does the same.
+//
+// MI355X mapping: one wave64 per (KV head, split[, token]) computes ALL
+// query heads of its GQA group, so each KV byte is read from HBM once.
+// Keys go in 32-key tiles held in registers (the next tile's rows load
+// while the current one is computed).  Q.K^T runs on the matrix cores
+// transposed (C = K.q^T: keys are rows, one lane per head, so the softmax
+// needs one cross-lane step); the V tile is transposed by an identity MFMA
+// (int8: v_mfma_i32_32x32x32_i8 against I, exact) and P.V runs as
+// v_mfma_f32_32x32x16_f16 with the fp32 probabilities (times vs) split into
+// a high and a low fp16 part stacked as extra rows of the A operand, so the
+// P.V products keep ~22 bits.
 #include <float.h>
 #include "kq_common.h"
 #include "attention.h"
@@ -106,16 +114,18 @@ void attn_partial_kernel(AttnArgs a) {
     constexpr int VW = NDT * EB;                        // V: 16-byte chunks per lane
     constexpr int NST = half / 8;                       // Q.K^T MFMA steps
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int kvh = blockIdx.x, split = blockIdx.y;
+    const int kvh = blockIdx.x, split = blockIdx.y, tok = blockIdx.z;
     const int G = a.n_heads / a.n_kv;
+    const int seq = a.seq + tok;
+    const uint16_t* qt = a.q + (int64_t)tok * a.n_heads * hd;
     const int l = threadIdx.x, li = l & 31, lg = l >> 5;
     const int kv_dim = a.n_kv * a.cache_head_dim, hoff = kvh * a.cache_head_dim;
-    const int lo_pos = a.window > 0 ? max(0, a.seq - a.window) : 0;
-    const int span = a.seq - lo_pos;
+    const int lo_pos = a.window > 0 ? max(0, seq - a.window) : 0;
+    const int span = seq - lo_pos;
     const int S = a.n_splits;
     const int per = (span + S - 1) / S;
     const int kv0 = lo_pos + split * per;
-    const int kv1 = min(kv0 + per, a.seq);
+    const int kv1 = min(kv0 + per, seq);
 
     _Float16* sP = (_Float16*)smem;                              // [32 rows][32 keys]
     float* sMisc = (float*)(smem + 32 * AT_KEYS * 2);            // corr[32] | ks[32] | vs[32]
@@ -124,7 +134,7 @@ void attn_partial_kernel(AttnArgs a) {
     h8 qa[NST];
 #pragma unroll
     for (int st = 0; st < NST; st++)
-        qa[st] = li < G ? __builtin_bit_cast(h8, *(const u32x4a*)(a.q + (int64_t)(kvh * G + li) * hd + lg * half + 8 * st))
+        qa[st] = li < G ? __builtin_bit_cast(h8, *(const u32x4a*)(qt + (int64_t)(kvh * G + li) * hd + lg * half + 8 * st))
                         : h8{};
     for (int i = l; i < 32 * AT_KEYS; i += 64) sP[i] = (_Float16)0.0f;
 
@@ -302,15 +312,9 @@ void attn_partial_kernel(AttnArgs a) {
         tile(p0, ck, cv, ksc, vsc);
     }
 
-    // 4. unnormalised partials: m, l per head; acc = high rows + low rows
+    // 4. S == 1: the normalised output straight from this wave; else the
+    //    unnormalised partials m, l per head (acc = high rows + low rows)
     const int pbase = kvh * G;
-    float* pm = a.part;
-    float* pl = a.part + (int64_t)a.n_heads * S;
-    float* pacc = a.part + (int64_t)a.n_heads * S * 2;
-    if (li < G && lg == 0) {
-        pm[(int64_t)(pbase + li) * S + split] = run_m;
-        pl[(int64_t)(pbase + li) * S + split] = run_l;
-    }
     float* sO = (float*)smem;                                  // [2G][hd]
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
@@ -324,6 +328,23 @@ void attn_partial_kernel(AttnArgs a) {
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
+    if (S == 1) {
+        const float inv_l = run_l > 0.0f ? 1.0f / run_l : 0.0f;
+        uint16_t* ot = a.out + (int64_t)tok * a.n_heads * hd + (int64_t)pbase * hd;
+        for (int e = l; e < G * hd; e += 64) {
+            const int h = e / hd, d = e % hd;
+            const float il = __shfl(inv_l, h, 64);
+            ot[e] = f32_to_f16_bits((sO[h * hd + d] + sO[(G + h) * hd + d]) * il);
+        }
+        return;
+    }
+    float* pm = a.part;
+    float* pl = a.part + (int64_t)a.n_heads * S;
+    float* pacc = a.part + (int64_t)a.n_heads * S * 2;
+    if (li < G && lg == 0) {
+        pm[(int64_t)(pbase + li) * S + split] = run_m;
+        pl[(int64_t)(pbase + li) * S + split] = run_l;
+    }
     for (int e = l; e < G * hd; e += 64) {
         const int h = e / hd, d = e % hd;
         pacc[((int64_t)(pbase + h) * S + split) * hd + d] = sO[h * hd + d] + sO[(G + h) * hd + d];
@@ -398,7 +419,8 @@ void attn_reduce_kernel(uint16_t* __restrict__ out, const float* __restrict__ pa
 }
 
 hipError_t attn_launch(const AttnArgs& a, bool kv_int8, hipStream_t st) {
-    dim3 grid(a.n_kv, a.n_splits);
+    if (a.tokens < 1 || (a.tokens > 1 && a.n_splits != 1)) return hipErrorInvalidValue;
+    dim3 grid(a.n_kv, a.n_splits, a.tokens);
     const size_t lds = attn_lds_bytes(a.n_heads, a.n_kv, a.head_dim);
     switch (a.head_dim * 2 + (kv_int8 ? 1 : 0)) {
     case 64:  hipLaunchKernelGGL((attn_partial_kernel<false, 32>), grid, dim3(64), lds, st, a); break;
@@ -412,7 +434,7 @@ hipError_t attn_launch(const AttnArgs& a, bool kv_int8, hipStream_t st) {
     default: return hipErrorInvalidValue;
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || a.n_splits == 1) return e;
     hipLaunchKernelGGL(attn_reduce_kernel, dim3(a.n_heads), dim3(AT_RED_THREADS), 0, st, a.out, (const float*)a.part,
                        a.n_heads, a.head_dim, a.n_splits);
     return hipGetLastError();

@@ -42,7 +42,7 @@ int attn_run(uint16_t* out, const uint16_t* q, const void* k, const void* v, int
     a.counters = (int*)scratch;
     a.part = (float*)(scratch + ATTN_COUNTER_BYTES);
     a.n_heads = n_heads; a.n_kv = n_kv; a.head_dim = hd; a.cache_head_dim = chd;
-    a.seq = seq; a.window = window; a.n_splits = n_splits; a.scale = scale;
+    a.seq = seq; a.window = window; a.n_splits = n_splits; a.scale = scale; a.tokens = 1;
     return launch_status(attn_launch(a, kv_int8 != 0, (hipStream_t)stream), "attention");
 }
 }  // namespace
@@ -71,6 +71,22 @@ int jllm_hip_flash_attention_decode_splits(uint16_t* out, const uint16_t* q, con
                                            const float* v_scales, int window, int n_splits, void* stream) {
     return attn_run(out, q, k, v, n_heads, n_kv_heads, head_dim, cache_head_dim, seq_len, scale, kv_int8,
                     k_scales, v_scales, window, n_splits, stream);
+}
+
+int jllm_hip_flash_attention_prefill_batched(uint16_t* out, const uint16_t* q, const void* k, const void* v,
+                                             int n_heads, int n_kv_heads, int head_dim, int cache_head_dim, int N,
+                                             int start_pos, float scale, int kv_int8, const float* k_scales,
+                                             const float* v_scales, int window, void* stream) {
+    if (N < 0 || start_pos < 0 || N > 65535) return JLLM_ERR_INVALID;
+    if (N == 0) return JLLM_OK;
+    int st = attn_check(out, q, k, v, n_heads, n_kv_heads, head_dim, cache_head_dim, start_pos + 1, kv_int8, window);
+    if (st) return st;
+    AttnArgs a;
+    a.out = out; a.q = q; a.k = k; a.v = v; a.ks = k_scales; a.vs = v_scales;
+    a.counters = nullptr; a.part = nullptr;
+    a.n_heads = n_heads; a.n_kv = n_kv_heads; a.head_dim = head_dim; a.cache_head_dim = cache_head_dim;
+    a.seq = start_pos + 1; a.window = window; a.n_splits = 1; a.scale = scale; a.tokens = N;
+    return launch_status(attn_launch(a, kv_int8 != 0, (hipStream_t)stream), "attention prefill");
 }
 
 int jllm_hip_fp16_to_int8(int8_t* dst, float* scale_out, const uint16_t* src, int rows, int cols, void* stream) {

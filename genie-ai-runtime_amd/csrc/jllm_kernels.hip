@@ -23,7 +23,8 @@ void zero_fill(void* p, size_t bytes, hipStream_t st) {
 
 void report(int st, const char* fn, void* out, size_t bytes, hipStream_t stream) {
     if (st == JLLM_OK) return;
-    fprintf(stderr, "[jllm] %s failed: %s; output zero-filled\n", fn, jllm_hip_status_string(st));
+    fprintf(stderr, "[jllm] %s failed: %s; %s\n", fn, jllm_hip_status_string(st),
+            out ? "output zero-filled" : "data left unchanged");
     zero_fill(out, bytes, stream);
 }
 
@@ -111,6 +112,65 @@ float* get_splitk_partials(int n_heads, int n_splits, int head_dim) {
 void fp16_to_int8(int8_t* dst, float* scale_out, const half* src, int rows, int cols, hipStream_t stream) {
     report(jllm_hip_fp16_to_int8(dst, scale_out, H(src), rows, cols, stream), "fp16_to_int8", dst,
            (size_t)rows * cols & ~(size_t)1, stream);
+}
+
+bool dequant_embedding_row(half* dst, const void* W, int ggml_type, int token_id, int hidden_dim, hipStream_t stream) {
+    const int st = jllm_hip_dequant_embedding_row(H(dst), W, ggml_type, token_id, hidden_dim, stream);
+    report(st, "dequant_embedding_row", dst, (size_t)(hidden_dim > 0 ? hidden_dim : 0) * 2, stream);
+    return st == JLLM_OK;
+}
+
+void fused_rmsnorm_residual(half* output, const half* x, const half* residual, const void* weight, int rows,
+                            int hidden_dim, float eps, bool weight_fp32, hipStream_t stream) {
+    report(jllm_hip_fused_rmsnorm_residual(H(output), H(x), H(residual), weight, rows, hidden_dim, eps,
+                                           weight_fp32 ? 1 : 0, stream),
+           "fused_rmsnorm_residual", output, (size_t)(rows > 0 ? rows : 0) * (hidden_dim > 0 ? hidden_dim : 0) * 2,
+           stream);
+}
+
+void fused_swiglu(half* output, const half* gate, const half* up, int rows, int intermediate_dim, hipStream_t stream) {
+    report(jllm_hip_fused_swiglu(H(output), H(gate), H(up), rows, intermediate_dim, stream), "fused_swiglu", output,
+           (size_t)(rows > 0 ? rows : 0) * (intermediate_dim > 0 ? intermediate_dim : 0) * 2, stream);
+}
+
+void rope_precompute_table(int max_seq, int head_dim, float theta_base) {
+    (void)jllm_hip_rope_precompute_table(max_seq, head_dim, theta_base);
+}
+void rope_clear_tables() { jllm_hip_rope_clear_tables(); }
+
+// in-place operations: on failure the data is left as it was (no zero fill)
+void rope_inplace(half* q, half* k, int n_heads, int n_kv_heads, int head_dim, int position, float theta_base,
+                  bool neox, hipStream_t stream) {
+    report(jllm_hip_rope_inplace(H(q), H(k), n_heads, n_kv_heads, head_dim, position, theta_base, neox ? 1 : 0,
+                                 stream),
+           "rope_inplace", nullptr, 0, stream);
+}
+
+void rope_inplace_batched(half* q, half* k, int n_heads, int n_kv_heads, int head_dim, int start_pos, int N,
+                          int q_stride, int k_stride, float theta_base, bool neox, hipStream_t stream) {
+    report(jllm_hip_rope_inplace_batched(H(q), H(k), n_heads, n_kv_heads, head_dim, start_pos, N, q_stride, k_stride,
+                                         theta_base, neox ? 1 : 0, stream),
+           "rope_inplace_batched", nullptr, 0, stream);
+}
+
+void rope_inplace_store_kv_fp16(half* q, half* k, const half* v, half* k_cache_dst, half* v_cache_dst, int n_heads,
+                                int n_kv_heads, int head_dim, int position, float theta_base, bool neox,
+                                hipStream_t stream) {
+    report(jllm_hip_qk_norm_rope_store_kv(H(q), H(k), H(v), nullptr, nullptr, 0, 0.0f, k_cache_dst, v_cache_dst,
+                                          nullptr, nullptr, (int64_t)n_kv_heads * head_dim, n_heads, n_kv_heads,
+                                          head_dim, head_dim, position, 1, theta_base, neox ? 1 : 0, 0, stream),
+           "rope_inplace_store_kv_fp16", nullptr, 0, stream);
+}
+
+void flash_attention_prefill_batched(half* output, const half* q, const void* k_cache, const void* v_cache,
+                                     int n_heads, int n_kv_heads, int head_dim, int cache_head_dim, int N,
+                                     int start_pos, float scale, bool kv_int8, const float* k_scales,
+                                     const float* v_scales, int window, hipStream_t stream) {
+    report(jllm_hip_flash_attention_prefill_batched(H(output), H(q), k_cache, v_cache, n_heads, n_kv_heads, head_dim,
+                                                    cache_head_dim, N, start_pos, scale, kv_int8 ? 1 : 0, k_scales,
+                                                    v_scales, window, stream),
+           "flash_attention_prefill_batched", output,
+           (size_t)(N > 0 ? N : 0) * (n_heads > 0 ? n_heads : 0) * (head_dim > 0 ? head_dim : 0) * 2, stream);
 }
 
 }  // namespace jllm

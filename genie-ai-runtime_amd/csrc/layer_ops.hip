@@ -1,0 +1,436 @@
+// layer_ops.hip -- the decoder-layer kernels that sit between the quantized
+// matmuls (gfx950): RMSNorm (+residual), SwiGLU, residual add, RoPE, the
+// fused q/k-norm + RoPE + KV-cache store, embedding-row dequant and greedy
+// argmax.  All are HBM/latency-bound element-wise or row-reduction kernels:
+// 16-byte loads where the layout allows, wave64 shuffle reductions, no LDS
+// beyond a few cross-wave partials.
+//
+// Arithmetic follows the reference kernels operation by operation in fp32
+// (no FMA contraction where the reference's result is a rounded product
+// chain), with fp16 rounding at the same points:
+//   RMSNorm   fused_rmsnorm_residual_kernel  fused_norm.cu:33-101
+//   SwiGLU    swiglu_kernel                  convert.cu:85-112
+//   vec_add   vec_add_kernel                 decode.cu:60-78
+//   RoPE      rope_kernel / rope_batched_kernel rope.cu:322-367, :476-497
+//   KV int8   fp16_to_int8_kernel            convert.cu:26-69
+//   embedding dequant_embedding_q4k/q6k_kernel gemv_q4.cu:793-864
+//   argmax    sample_greedy (host)           sample.cpp:160-170
+#include <float.h>
+#include <limits.h>
+#include <math.h>
+#include "kq_common.h"
+#include "layer_ops.h"
+
+namespace jllm_hip {
+
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm: out = half((x + res) * rrms * w), rrms = 1/sqrt(sum((x+res)^2)/dim
+// + eps).  GS threads per row (64: one wave per row for head-sized rows, 256:
+// one workgroup per hidden-sized row).  Two passes over the row; the second
+// re-reads x from cache.  out may alias x (each element is read before it is
+// written, by the same thread).  VEC = 8 (16-byte accesses) or 2.
+template <bool WF32, bool RES, int GS, int VEC>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* out, const uint16_t* x, const uint16_t* res,
+                                                      const void* w, int rows, int dim, float eps) {
+#pragma clang fp contract(off)
+    __shared__ float red[4];
+    constexpr int RPB = 256 / GS;                        // rows per block
+    const int t = threadIdx.x % GS, rb = threadIdx.x / GS;
+    const int row = blockIdx.x * RPB + rb;
+    const bool live = row < rows;
+    const int64_t off = (int64_t)(live ? row : 0) * dim;
+    auto load = [&](const uint16_t* p, int i, float (&v)[VEC]) {
+        if (VEC == 8) {
+            const u32x4v u = *(const u32x4v*)(p + off + i);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const half2_t h = as_h2(u[e]);
+                v[2 * e] = (float)h[0];
+                v[2 * e + 1] = (float)h[1];
+            }
+        } else {
+            const half2_t h = as_h2(*(const uint32_t*)(p + off + i));
+            v[0] = (float)h[0];
+            v[1] = (float)h[1];
+        }
+    };
+    auto row_vals = [&](int i, float (&v)[VEC]) {
+        load(x, i, v);
+        if (RES) {
+            float r[VEC];
+            load(res, i, r);
+#pragma unroll
+            for (int e = 0; e < VEC; e++) v[e] += r[e];
+        }
+    };
+    float ss = 0.0f;
+    if (live)
+        for (int i = t * VEC; i < dim; i += GS * VEC) {
+            float v[VEC];
+            row_vals(i, v);
+#pragma unroll
+            for (int e = 0; e < VEC; e += 2) ss += v[e] * v[e] + v[e + 1] * v[e + 1];
+        }
+    ss = wave_sum(ss);
+    if (GS == 256) {
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        ss = (red[0] + red[1]) + (red[2] + red[3]);
+    }
+    if (!live) return;
+    const float rrms = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (int i = t * VEC; i < dim; i += GS * VEC) {
+        float v[VEC], wv[VEC];
+        row_vals(i, v);
+        if (WF32) {
+#pragma unroll
+            for (int e = 0; e < VEC; e++) wv[e] = ((const float*)w)[i + e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < VEC; e++) wv[e] = f16_bits_to_f32(((const uint16_t*)w)[i + e]);
+        }
+        uint32_t o[VEC / 2];
+#pragma unroll
+        for (int e = 0; e < VEC; e += 2)
+            o[e / 2] = (uint32_t)f32_to_f16_bits(v[e] * rrms * wv[e]) |
+                       ((uint32_t)f32_to_f16_bits(v[e + 1] * rrms * wv[e + 1]) << 16);
+        if (VEC == 8) *(u32x4v*)(out + off + i) = u32x4v{o[0], o[1], o[2], o[3]};
+        else *(uint32_t*)(out + off + i) = o[0];
+    }
+}
+
+template <bool WF32, bool RES>
+static void rmsnorm_go(uint16_t* out, const uint16_t* x, const uint16_t* res, const void* w, int rows, int dim,
+                       float eps, hipStream_t st) {
+    const bool v8 = dim % 8 == 0 && ((uintptr_t)out | (uintptr_t)x | (uintptr_t)(res ? res : x)) % 16 == 0 &&
+                    (uintptr_t)w % (WF32 ? 32 : 16) == 0;
+    if (dim <= 1024) {
+        const dim3 g((rows + 3) / 4);
+        if (v8) hipLaunchKernelGGL((rmsnorm_kernel<WF32, RES, 64, 8>), g, dim3(256), 0, st, out, x, res, w, rows, dim, eps);
+        else hipLaunchKernelGGL((rmsnorm_kernel<WF32, RES, 64, 2>), g, dim3(256), 0, st, out, x, res, w, rows, dim, eps);
+    } else {
+        const dim3 g(rows);
+        if (v8) hipLaunchKernelGGL((rmsnorm_kernel<WF32, RES, 256, 8>), g, dim3(256), 0, st, out, x, res, w, rows, dim, eps);
+        else hipLaunchKernelGGL((rmsnorm_kernel<WF32, RES, 256, 2>), g, dim3(256), 0, st, out, x, res, w, rows, dim, eps);
+    }
+}
+
+hipError_t rmsnorm_launch(uint16_t* out, const uint16_t* x, const uint16_t* res, const void* w, int rows, int dim,
+                          float eps, bool w_fp32, hipStream_t st) {
+    if (w_fp32) {
+        if (res) rmsnorm_go<true, true>(out, x, res, w, rows, dim, eps, st);
+        else rmsnorm_go<true, false>(out, x, res, w, rows, dim, eps, st);
+    } else {
+        if (res) rmsnorm_go<false, true>(out, x, res, w, rows, dim, eps, st);
+        else rmsnorm_go<false, false>(out, x, res, w, rows, dim, eps, st);
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Element-wise: SwiGLU out = half(g / (1 + e^-g) * u) and the residual add
+// out = half(a + b).  Eight elements per thread (16-byte accesses) over the
+// aligned body, one element per thread for the tail.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+#pragma clang fp contract(off)
+    return g / (1.0f + expf(-g)) * u;
+}
+
+template <int OP, bool V>
+__global__ __launch_bounds__(256) void eltwise_kernel(uint16_t* __restrict__ out, const uint16_t* __restrict__ a,
+                                                      const uint16_t* __restrict__ b, int64_t n) {
+#pragma clang fp contract(off)
+    const int64_t i8 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (V && i8 + 8 <= n) {
+        const u32x4v ua = *(const u32x4v*)(a + i8), ub = *(const u32x4v*)(b + i8);
+        u32x4v o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const half2_t ha = as_h2(ua[e]), hb = as_h2(ub[e]);
+            float r0, r1;
+            if (OP == 0) { r0 = silu_mul((float)ha[0], (float)hb[0]); r1 = silu_mul((float)ha[1], (float)hb[1]); }
+            else { r0 = (float)ha[0] + (float)hb[0]; r1 = (float)ha[1] + (float)hb[1]; }
+            o[e] = (uint32_t)f32_to_f16_bits(r0) | ((uint32_t)f32_to_f16_bits(r1) << 16);
+        }
+        *(u32x4v*)(out + i8) = o;
+    } else {
+        for (int64_t i = i8; i < n && i < i8 + 8; i++) {
+            const float fa = f16_bits_to_f32(a[i]), fb = f16_bits_to_f32(b[i]);
+            out[i] = f32_to_f16_bits(OP == 0 ? silu_mul(fa, fb) : fa + fb);
+        }
+    }
+}
+
+template <int OP>
+static hipError_t eltwise_go(uint16_t* out, const uint16_t* a, const uint16_t* b, int64_t n, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const int64_t thr = (n + 7) / 8;
+    const dim3 g((unsigned)((thr + 255) / 256));
+    if ((((uintptr_t)out | (uintptr_t)a | (uintptr_t)b) & 15) == 0)
+        hipLaunchKernelGGL((eltwise_kernel<OP, true>), g, dim3(256), 0, st, out, a, b, n);
+    else
+        hipLaunchKernelGGL((eltwise_kernel<OP, false>), g, dim3(256), 0, st, out, a, b, n);
+    return hipGetLastError();
+}
+hipError_t swiglu_launch(uint16_t* out, const uint16_t* gate, const uint16_t* up, int64_t n, hipStream_t st) {
+    return eltwise_go<0>(out, gate, up, n, st);
+}
+hipError_t vec_add_launch(uint16_t* out, const uint16_t* a, const uint16_t* b, int64_t n, hipStream_t st) {
+    return eltwise_go<1>(out, a, b, n, st);
+}
+
+// ---------------------------------------------------------------------------
+// RoPE.  freq[i] = 1 / theta^(2i/hd) is computed on the host in fp32 exactly
+// as the reference writes it (1.0f / powf(theta, (2.0f*i)/hd)); the angle
+// is the fp32 product position * freq[i] and cos/sin are evaluated on it,
+// so the rounding of the angle matches the reference.  Pair i is
+// (i, i + hd/2) for neox, (2i, 2i+1) otherwise.
+void rope_frequencies(RopeFreq& fr, int head_dim, float theta) {
+    for (int i = 0; i < ROPE_MAX_HALF; i++)
+        fr.f[i] = i < head_dim / 2 ? 1.0f / powf(theta, (2.0f * (float)i) / (float)head_dim) : 0.0f;
+}
+
+__device__ __forceinline__ void rotate(float v0, float v1, float c, float s, float& r0, float& r1) {
+#pragma clang fp contract(off)
+    r0 = round_to_f16(v0 * c - v1 * s);
+    r1 = round_to_f16(v0 * s + v1 * c);
+}
+
+// one thread per (token, head, pair)
+__global__ __launch_bounds__(256) void rope_kernel(uint16_t* q, uint16_t* k, int n_heads, int n_kv, int hd,
+                                                   int start_pos, int N, int q_stride, int k_stride, RopeFreq fr,
+                                                   int neox) {
+    const int h2 = hd / 2;
+    const int64_t per_tok = (int64_t)(n_heads + n_kv) * h2;
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gid >= per_tok * N) return;
+    const int t = (int)(gid / per_tok);
+    const int r = (int)(gid % per_tok);
+    const int head = r / h2, i = r % h2;
+    uint16_t* p = head < n_heads ? q + (int64_t)t * q_stride + (int64_t)head * hd
+                                 : k + (int64_t)t * k_stride + (int64_t)(head - n_heads) * hd;
+    const float ang = (float)(start_pos + t) * fr.f[i];
+    float s, c;
+    sincosf(ang, &s, &c);
+    const int i0 = neox ? i : 2 * i, i1 = neox ? i + h2 : 2 * i + 1;
+    float r0, r1;
+    rotate(f16_bits_to_f32(p[i0]), f16_bits_to_f32(p[i1]), c, s, r0, r1);
+    p[i0] = f32_to_f16_bits(r0);
+    p[i1] = f32_to_f16_bits(r1);
+}
+
+hipError_t rope_launch(uint16_t* q, uint16_t* k, int n_heads, int n_kv, int head_dim, int start_pos, int N,
+                       int q_stride, int k_stride, const RopeFreq& fr, bool neox, hipStream_t st) {
+    const int64_t total = (int64_t)(n_heads + n_kv) * (head_dim / 2) * N;
+    if (total <= 0) return hipSuccess;
+    hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, q, k, n_heads, n_kv,
+                       head_dim, start_pos, N, q_stride, k_stride, fr, neox ? 1 : 0);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Fused attention front for N tokens: one wave per (token, slot), slots =
+// n_heads q heads, n_kv k heads, n_kv v heads.  Lane i < hd/2 holds the
+// rotary pair i (both elements), so the norm is one wave reduction and the
+// rotation needs no data exchange.  The fp16 roundings of the unfused
+// sequence are kept: normed value -> fp16 (rmsnorm output), rotated ->
+// fp16 (rope output), then the KV quantiser reads those fp16 values.
+// Replaces decode.cu:1441-1478 (q/k norm, rope_inplace, fp16_to_int8 x2)
+// and the per-token loop of decode.cu:1806-1842.
+__global__ __launch_bounds__(256) void qk_post_kernel(QKPostArgs a) {
+#pragma clang fp contract(off)
+    const int hd = a.head_dim, h2 = hd / 2;
+    const int slots = a.n_heads + 2 * a.n_kv;
+    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int l = threadIdx.x & 63;
+    if (gw >= slots * a.N) return;                      // whole wave exits together
+    const int t = gw / slots, slot = gw % slots;
+    const int kind = slot < a.n_heads ? 0 : (slot < a.n_heads + a.n_kv ? 1 : 2);   // q, k, v
+    const int head = kind == 0 ? slot : (kind == 1 ? slot - a.n_heads : slot - a.n_heads - a.n_kv);
+    const uint16_t* src = kind == 0 ? a.q + ((int64_t)t * a.n_heads + head) * hd
+                                    : (kind == 1 ? a.k : a.v) + ((int64_t)t * a.n_kv + head) * hd;
+    const bool act = l < h2;
+    const int i0 = a.neox ? l : 2 * l, i1 = a.neox ? l + h2 : 2 * l + 1;
+    float v0 = act ? f16_bits_to_f32(src[i0]) : 0.0f;
+    float v1 = act ? f16_bits_to_f32(src[i1]) : 0.0f;
+    if (kind < 2 && a.q_norm) {
+        const float ss = wave_sum(v0 * v0 + v1 * v1);
+        const float rrms = 1.0f / sqrtf(ss / (float)hd + a.eps);
+        const void* w = kind == 0 ? a.q_norm : a.k_norm;
+        float w0 = 0.0f, w1 = 0.0f;
+        if (act) {
+            if (a.norm_fp32) { w0 = ((const float*)w)[i0]; w1 = ((const float*)w)[i1]; }
+            else { w0 = f16_bits_to_f32(((const uint16_t*)w)[i0]); w1 = f16_bits_to_f32(((const uint16_t*)w)[i1]); }
+        }
+        v0 = round_to_f16(v0 * rrms * w0);
+        v1 = round_to_f16(v1 * rrms * w1);
+    }
+    const int pos = a.start_pos + t;
+    if (kind < 2) {
+        float s, c;
+        sincosf((float)pos * a.fr.f[act ? l : 0], &s, &c);
+        rotate(v0, v1, c, s, v0, v1);
+    }
+    if (kind < 2 && act) {
+        uint16_t* dq = kind == 0 ? a.q + ((int64_t)t * a.n_heads + head) * hd : a.k + ((int64_t)t * a.n_kv + head) * hd;
+        dq[i0] = f32_to_f16_bits(v0);
+        dq[i1] = f32_to_f16_bits(v1);
+    }
+    if (kind == 0) return;
+    const int64_t row = (int64_t)t * a.kv_stride + (int64_t)head * a.cache_head_dim;
+    void* cache = kind == 1 ? a.k_dst : a.v_dst;
+    if (a.kv_int8) {
+        const float mx = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
+        const float scale = mx / 127.0f;
+        const float inv = scale > 0.0f ? 127.0f / mx : 0.0f;
+        if (act) {
+            int q0 = (int)__builtin_rintf(v0 * inv), q1 = (int)__builtin_rintf(v1 * inv);
+            q0 = q0 > 127 ? 127 : (q0 < -127 ? -127 : q0);
+            q1 = q1 > 127 ? 127 : (q1 < -127 ? -127 : q1);
+            int8_t* d = (int8_t*)cache + row;
+            d[i0] = (int8_t)q0;
+            d[i1] = (int8_t)q1;
+        }
+        float* sc = kind == 1 ? a.k_scales : a.v_scales;
+        if (l == 0 && sc) sc[(int64_t)t * a.n_kv + head] = scale;
+    } else if (act) {
+        uint16_t* d = (uint16_t*)cache + row;
+        d[i0] = f32_to_f16_bits(v0);
+        d[i1] = f32_to_f16_bits(v1);
+    }
+}
+
+hipError_t qk_post_launch(const QKPostArgs& a, hipStream_t st) {
+    const int64_t waves = (int64_t)(a.n_heads + 2 * a.n_kv) * a.N;
+    if (waves <= 0) return hipSuccess;
+    hipLaunchKernelGGL(qk_post_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Embedding rows: dst[t][hidden] = dequant(W row tokens[t]).  Each thread
+// produces 8 consecutive weights of one 256-weight super-block (one 16-byte
+// store); a 256-thread workgroup covers 8 super-blocks.
+__device__ __forceinline__ void q4k_sc_min(const uint8_t* q, int j, int& d, int& m) {
+    if (j < 4) { d = q[j] & 63; m = q[j + 4] & 63; }
+    else { d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4); m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4); }
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(256) void embed_kernel(uint16_t* __restrict__ dst, const uint8_t* __restrict__ W,
+                                                    const int32_t* __restrict__ tokens, int token0, int N, int nb,
+                                                    int vocab) {
+#pragma clang fp contract(off)
+    const int64_t g = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);      // (token, super-block)
+    if (g >= (int64_t)N * nb) return;
+    const int t = (int)(g / nb), b = (int)(g % nb);
+    const int tok = tokens ? tokens[t] : token0;
+    const int i = (threadIdx.x & 31) * 8;                                // first weight of this thread
+    float val[8];
+    if (vocab > 0 && (tok < 0 || tok >= vocab)) {                         // id out of range: zero row
+#pragma unroll
+        for (int e = 0; e < 8; e++) val[e] = 0.0f;
+    } else if (TYPE == 12) {
+        const uint8_t* blk = W + ((int64_t)tok * nb + b) * 144;
+        const float dall = f16_bits_to_f32(blk[0] | (blk[1] << 8));
+        const float dmin = f16_bits_to_f32(blk[2] | (blk[3] << 8));
+        const int il = i >> 6, l64 = i & 63, l32 = l64 & 31;
+        int sc, mn;
+        q4k_sc_min(blk + 4, 2 * il + (l64 >= 32), sc, mn);
+        const uint8_t* qs = blk + 16 + 32 * il + l32;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int qv = l64 < 32 ? (qs[e] & 0xF) : (qs[e] >> 4);
+            val[e] = dall * (float)sc * (float)qv - dmin * (float)mn;
+        }
+    } else {
+        const uint8_t* blk = W + ((int64_t)tok * nb + b) * 210;
+        const float d = f16_bits_to_f32(blk[208] | (blk[209] << 8));
+        const int hb = i >> 7, local = i & 127, lane = local & 31, quarter = local >> 5;
+        const uint8_t* ql = blk + hb * 64;
+        const uint8_t* qh = blk + 128 + hb * 32;
+        const int8_t* scs = (const int8_t*)(blk + 192) + hb * 8;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int ln = lane + e, is = ln >> 4;
+            const int lo = (quarter & 1) ? ql[ln + 32] : ql[ln];
+            const int qv = ((quarter >> 1) ? (lo >> 4) : (lo & 0xF)) | (((qh[ln] >> (2 * quarter)) & 3) << 4);
+            val[e] = d * (float)scs[is + 2 * quarter] * (float)(qv - 32);
+        }
+    }
+    u32x4v o;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        o[e] = (uint32_t)f32_to_f16_bits(val[2 * e]) | ((uint32_t)f32_to_f16_bits(val[2 * e + 1]) << 16);
+    *(u32x4v*)(dst + (int64_t)t * nb * 256 + (int64_t)b * 256 + i) = o;
+}
+
+hipError_t embed_launch(uint16_t* dst, const void* W, int type, const int32_t* tokens, int token0, int N, int hidden,
+                        int vocab, hipStream_t st) {
+    const int nb = hidden / 256;
+    const int64_t groups = (int64_t)N * nb;
+    if (groups <= 0) return hipSuccess;
+    const dim3 g((unsigned)((groups + 7) / 8));
+    if (type == 12) hipLaunchKernelGGL((embed_kernel<12>), g, dim3(256), 0, st, dst, (const uint8_t*)W, tokens, token0, N, nb, vocab);
+    else hipLaunchKernelGGL((embed_kernel<14>), g, dim3(256), 0, st, dst, (const uint8_t*)W, tokens, token0, N, nb, vocab);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Greedy argmax over fp32 logits: the lowest index of the largest finite
+// value (0 when none is finite), i.e. the host loop of sample_greedy run as
+// one 1024-thread workgroup (float4 loads over the aligned body).
+__device__ __forceinline__ void arg_better(float v, int i, float& bv, int& bi) {
+    if (isfinite(v) && (v > bv || (v == bv && i < bi))) { bv = v; bi = i; }
+}
+
+__global__ __launch_bounds__(1024) void argmax_kernel(int32_t* out, const float* __restrict__ x, int n) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int t = threadIdx.x;
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+    const bool v4 = ((uintptr_t)x & 15) == 0;
+    const int n4 = v4 ? n / 4 : 0;
+    for (int j = t; j < n4; j += 1024) {
+        const float4 f = ((const float4*)x)[j];
+        arg_better(f.x, 4 * j, bv, bi);
+        arg_better(f.y, 4 * j + 1, bv, bi);
+        arg_better(f.z, 4 * j + 2, bv, bi);
+        arg_better(f.w, 4 * j + 3, bv, bi);
+    }
+    for (int j = 4 * n4 + t; j < n; j += 1024) arg_better(x[j], j, bv, bi);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if ((t & 63) == 0) { sv[t >> 6] = bv; si[t >> 6] = bi; }
+    __syncthreads();
+    if (t == 0) {
+        for (int w = 1; w < 16; w++)
+            if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) { bv = sv[w]; bi = si[w]; }
+        out[0] = bi == INT_MAX ? 0 : bi;
+    }
+}
+
+hipError_t argmax_launch(int32_t* out, const float* x, int n, hipStream_t st) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, st, out, x, n);
+    return hipGetLastError();
+}
+
+}  // namespace jllm_hip

@@ -39,6 +39,18 @@ SIGNATURES = {
     "jllm_hip_decode_attn_splits": (I, [I]),
     "jllm_hip_get_splitk_partials": (P, [I, I, I]),
     "jllm_hip_fp16_to_int8": (I, [P, P, P, I, I, P]),
+    "jllm_hip_flash_attention_prefill_batched": (I, [P, P, P, P, I, I, I, I, I, I, F, I, P, P, I, P]),
+    "jllm_hip_fused_rmsnorm_residual": (I, [P, P, P, P, I, I, F, I, P]),
+    "jllm_hip_fused_swiglu": (I, [P, P, P, I, I, P]),
+    "jllm_hip_vec_add": (I, [P, P, P, I64, P]),
+    "jllm_hip_rope_inplace": (I, [P, P, I, I, I, I, F, I, P]),
+    "jllm_hip_rope_inplace_batched": (I, [P, P, I, I, I, I, I, I, I, F, I, P]),
+    "jllm_hip_rope_precompute_table": (I, [I, I, F]),
+    "jllm_hip_rope_clear_tables": (None, []),
+    "jllm_hip_qk_norm_rope_store_kv": (I, [P, P, P, P, P, I, F, P, P, P, P, I64, I, I, I, I, I, I, F, I, I, P]),
+    "jllm_hip_dequant_embedding_row": (I, [P, P, I, I, I, P]),
+    "jllm_hip_dequant_embedding_rows": (I, [P, P, I, P, I, I, I, P]),
+    "jllm_hip_argmax_f32": (I, [P, P, I, P]),
 }
 
 

@@ -126,7 +126,7 @@ int jllm_hip_flash_attention_decode(uint16_t* out, const uint16_t* q, const void
                                     float scale, int kv_int8, const float* k_scales, const float* v_scales,
                                     int window, void* stream);
 
-/* Same with an explicit split count (1..64) instead of the policy of
+/* Same with an explicit split count (1..256) instead of the policy of
  * jllm_hip_decode_attn_splits.  Replaces the n_splits argument of
  * flash_attention_decode_dyn, jllm_kernels.h:380 (attention.cu:1007-1034). */
 int jllm_hip_flash_attention_decode_splits(uint16_t* out, const uint16_t* q, const void* k, const void* v,
@@ -136,8 +136,9 @@ int jllm_hip_flash_attention_decode_splits(uint16_t* out, const uint16_t* q, con
 
 /* Split-count policy and partials buffer.  Replace decode_attn_splits and
  * get_splitk_partials, jllm_kernels.h:402-403 (attention.cu:975-1005).  The
- * MI355X policy is ceil(seq/64) splits capped at 32 (so 8 KV heads fill 256
- * CUs), not the reference's 1/4/8.  The buffer (floats: m[H*S] | l[H*S] |
+ * MI355X policy is ceil(seq/32) splits capped at 128 (one wave per KV head
+ * and split, so 8 KV heads put 1024 waves on 256 CUs), not the reference's
+ * 1/4/8.  With one split the output is written directly (no reduce).  The buffer (floats: m[H*S] | l[H*S] |
  * acc[H*S*head_dim]) is allocated on first use and never freed; call
  * jllm_hip_get_splitk_partials before graph capture.  NULL on failure. */
 int    jllm_hip_decode_attn_splits(int seq_len);
@@ -147,6 +148,93 @@ float* jllm_hip_get_splitk_partials(int n_heads, int n_splits, int head_dim);
  * absmax/127, q = rn(v * 127/absmax) clamped to +-127.  Replaces
  * fp16_to_int8, jllm_kernels.h:413 (convert.cu:26-75). */
 int jllm_hip_fp16_to_int8(int8_t* dst, float* scale_out, const uint16_t* src, int rows, int cols, void* stream);
+
+/* Causal attention of N query tokens against the cache (prefill): token t
+ * (absolute position start_pos + t) attends to keys [0, start_pos + t] (the
+ * last `window` of them when window > 0).  q and out are [N][n_heads x
+ * head_dim]; cache layout and limits as jllm_hip_flash_attention_decode.
+ * One wave per (KV head, token), no partials buffer.
+ * Replaces flash_attention_prefill_batched, jllm_kernels.h:354
+ * (attention.cu:382-514, launcher :617-682). */
+int jllm_hip_flash_attention_prefill_batched(uint16_t* out, const uint16_t* q, const void* k, const void* v,
+                                             int n_heads, int n_kv_heads, int head_dim, int cache_head_dim, int N,
+                                             int start_pos, float scale, int kv_int8, const float* k_scales,
+                                             const float* v_scales, int window, void* stream);
+
+/* ---- decoder-layer kernels around the matmuls ---- */
+
+/* out[rows x hidden_dim] = half((x + residual) / sqrt(mean((x+residual)^2)
+ * + eps) * weight).  residual may be NULL; out may equal x.  weight is fp32
+ * (weight_fp32 != 0) or fp16.  hidden_dim even; x, out, residual 4-byte
+ * aligned.  Replaces fused_rmsnorm_residual, jllm_kernels.h:174
+ * (fused_norm.cu:33-115). */
+int jllm_hip_fused_rmsnorm_residual(uint16_t* out, const uint16_t* x, const uint16_t* residual, const void* weight,
+                                    int rows, int hidden_dim, float eps, int weight_fp32, void* stream);
+
+/* out = half(silu(gate) * up), silu(g) = g / (1 + e^-g), over rows x
+ * intermediate_dim.  Replaces fused_swiglu, jllm_kernels.h:191
+ * (convert.cu:85-112). */
+int jllm_hip_fused_swiglu(uint16_t* out, const uint16_t* gate, const uint16_t* up, int rows, int intermediate_dim,
+                          void* stream);
+
+/* out = half(a + b) over n elements (the prefill residual adds).  Replaces
+ * the engine-internal vec_add, src/engine/decode.cu:60-78. */
+int jllm_hip_vec_add(uint16_t* out, const uint16_t* a, const uint16_t* b, int64_t n, void* stream);
+
+/* Rotary position embedding in place: pair i of each head is (i, i + hd/2)
+ * when neox != 0, else (2i, 2i+1); angle = position * 1/theta^(2i/hd)
+ * (fp32).  k may be NULL (rotate q only).  head_dim even, <= 128.
+ * Replace rope_inplace :241 and rope_inplace_batched :274 (rope.cu:322-367,
+ * :427-446, :476-497; strides are per-token row strides in halves).
+ * rope_precompute_table / rope_clear_tables (:238-239, rope.cu:82-137) are
+ * accepted for interface parity and keep nothing: cos/sin are evaluated per
+ * element from host-computed frequencies, with the same fp32 angle. */
+int  jllm_hip_rope_inplace(uint16_t* q, uint16_t* k, int n_heads, int n_kv_heads, int head_dim, int position,
+                           float theta_base, int neox, void* stream);
+int  jllm_hip_rope_inplace_batched(uint16_t* q, uint16_t* k, int n_heads, int n_kv_heads, int head_dim,
+                                   int start_pos, int N, int q_stride, int k_stride, float theta_base, int neox,
+                                   void* stream);
+int  jllm_hip_rope_precompute_table(int max_seq, int head_dim, float theta_base);
+void jllm_hip_rope_clear_tables(void);
+
+/* The attention front of N tokens in one launch: q_norm/k_norm RMSNorm over
+ * each head (skipped when q_norm is NULL), RoPE of q and k (both in place),
+ * then k and v written to the cache rows of positions start_pos + t: int8
+ * with a per-(position, kv head) scale absmax/127 (kv_int8 != 0) or fp16.
+ * q [N][n_heads*hd], k and v [N][n_kv_heads*hd].  k_dst/v_dst address the
+ * cache row of position start_pos: token t goes to t * kv_stride elements
+ * further, head h at h * cache_head_dim; its scales to k_scales/v_scales
+ * [t * n_kv_heads + h] (may be NULL).  The intermediate fp16 roundings of
+ * the unfused sequence are kept.  Replaces the sequence
+ * fused_rmsnorm_residual(q), fused_rmsnorm_residual(k), rope_inplace,
+ * fp16_to_int8(k), fp16_to_int8(v) of the engine (src/engine/decode.cu
+ * :1441-1478 decode, :1806-1842 prefill) and rope_inplace_store_kv_fp16,
+ * jllm_kernels.h:255 (rope.cu:369-410). */
+int jllm_hip_qk_norm_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v, const void* q_norm,
+                                   const void* k_norm, int norm_fp32, float eps, void* k_dst, void* v_dst,
+                                   float* k_scales, float* v_scales, int64_t kv_stride, int n_heads, int n_kv_heads,
+                                   int head_dim, int cache_head_dim, int start_pos, int N, float theta_base, int neox,
+                                   int kv_int8, void* stream);
+
+/* dst[hidden_dim] (fp16, 16-byte aligned) = dequantised row token_id of a
+ * Q4_K / Q6_K embedding table.  Returns a status instead of the reference's
+ * bool.  Replaces dequant_embedding_row, jllm_kernels.h:160
+ * (gemv_q4.cu:793-864, :2803-2828). */
+int jllm_hip_dequant_embedding_row(uint16_t* dst, const void* W, int ggml_type, int token_id, int hidden_dim,
+                                   void* stream);
+
+/* The same for N tokens whose ids are in DEVICE memory (tokens[N]); an id
+ * outside [0, vocab) gives a zero row.  No single reference counterpart: the
+ * engine loops dequant_embedding per prompt token (decode.cu:2796-2801);
+ * reading ids on the device lets a greedy decode loop run without a host
+ * round trip. */
+int jllm_hip_dequant_embedding_rows(uint16_t* dst, const void* W, int ggml_type, const int32_t* tokens, int N,
+                                    int hidden_dim, int vocab, void* stream);
+
+/* out[0] (device int32) = the lowest index of the largest finite logit (0
+ * when none is finite).  The GPU form of the host greedy sampler
+ * sample_greedy, src/engine/sample.cpp:160-170. */
+int jllm_hip_argmax_f32(int32_t* out, const float* logits, int n, void* stream);
 
 #ifdef __cplusplus
 }

@@ -7,7 +7,8 @@
 // Error behaviour: the reference functions return void and, when the GPU
 // path cannot run, compute on the host or zero-fill the output for an
 // unsupported type.  Here there is no host path: any failure is reported on
-// stderr and the output is zero-filled on the stream.
+// stderr and the output is zero-filled on the stream (in-place operations
+// such as RoPE leave their data unchanged).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -56,5 +57,26 @@ float* get_splitk_partials(int n_heads, int n_splits, int head_dim);
 
 // KV quantiser (reference :413)
 void fp16_to_int8(int8_t* dst, float* scale_out, const half* src, int rows, int cols, hipStream_t stream);
+
+// prefill attention (reference :354)
+void flash_attention_prefill_batched(half* output, const half* q, const void* k_cache, const void* v_cache,
+                                     int n_heads, int n_kv_heads, int head_dim, int cache_head_dim, int N,
+                                     int start_pos, float scale, bool kv_int8, const float* k_scales,
+                                     const float* v_scales, int window, hipStream_t stream);
+
+// decoder-layer kernels (reference :160, :174, :191, :238-241, :255, :274)
+bool dequant_embedding_row(half* dst, const void* W, int ggml_type, int token_id, int hidden_dim, hipStream_t stream);
+void fused_rmsnorm_residual(half* output, const half* x, const half* residual, const void* weight, int rows,
+                            int hidden_dim, float eps, bool weight_fp32, hipStream_t stream);
+void fused_swiglu(half* output, const half* gate, const half* up, int rows, int intermediate_dim, hipStream_t stream);
+void rope_precompute_table(int max_seq, int head_dim, float theta_base);
+void rope_clear_tables();
+void rope_inplace(half* q, half* k, int n_heads, int n_kv_heads, int head_dim, int position, float theta_base,
+                  bool neox, hipStream_t stream);
+void rope_inplace_store_kv_fp16(half* q, half* k, const half* v, half* k_cache_dst, half* v_cache_dst, int n_heads,
+                                int n_kv_heads, int head_dim, int position, float theta_base, bool neox,
+                                hipStream_t stream);
+void rope_inplace_batched(half* q, half* k, int n_heads, int n_kv_heads, int head_dim, int start_pos, int N,
+                          int q_stride, int k_stride, float theta_base, bool neox, hipStream_t stream);
 
 }  // namespace jllm

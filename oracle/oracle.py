@@ -43,6 +43,14 @@ def lib():
             "orc_fp16_to_int8": (None, [P, P, P, I, I]),
             "orc_decode_attn_splits": (I, [I]),
             "orc_attn_decode_int8": (None, [P, P, P, P, I, I, I, I, I, F, P, P, I, I]),
+            "orc_rmsnorm": (None, [P, P, P, P, I, I, F, I]),
+            "orc_swiglu": (None, [P, P, P, ctypes.c_int64]),
+            "orc_vec_add": (None, [P, P, P, ctypes.c_int64]),
+            "orc_rope": (None, [P, P, I, I, I, I, I, I, I, F, I]),
+            "orc_qk_post": (None, [P, P, P, P, P, I, F, P, P, P, P, I, I, I, I, I, I, F, I, I]),
+            "orc_embed_row": (None, [P, P, I, I, I]),
+            "orc_argmax": (I, [P, I]),
+            "orc_attn_prefill_int8": (None, [P, P, P, P, I, I, I, I, I, I, F, P, P, I]),
         }
         for n, (r, a) in sig.items():
             f = getattr(_lib, n)
@@ -143,4 +151,75 @@ def attn_decode_int8(q, k, v, n_heads, n_kv, hd, chd, seq, scale, ks, vs, window
     out = np.empty(n_heads * hd, dtype=np.uint16)
     lib().orc_attn_decode_int8(_p(out), _p(q), _p(k), _p(v), n_heads, n_kv, hd, chd, seq, float(scale),
                                _p(ks), _p(vs), window, n_splits)
+    return out
+
+
+# ---- decoder-layer operations (layer_oracle.c) ----
+
+def rmsnorm(x, res, w, rows, dim, eps, w_fp32):
+    x = _c(x, np.uint16)
+    res = _c(res, np.uint16) if res is not None else None
+    w = _c(w, np.float32 if w_fp32 else np.uint16)
+    out = np.empty(rows * dim, dtype=np.uint16)
+    lib().orc_rmsnorm(_p(out), _p(x), _p(res), _p(w), rows, dim, float(eps), 1 if w_fp32 else 0)
+    return out
+
+
+def swiglu(g, u):
+    g, u = _c(g, np.uint16).ravel(), _c(u, np.uint16).ravel()
+    out = np.empty(g.size, dtype=np.uint16)
+    lib().orc_swiglu(_p(out), _p(g), _p(u), g.size)
+    return out
+
+
+def vec_add(a, b):
+    a, b = _c(a, np.uint16).ravel(), _c(b, np.uint16).ravel()
+    out = np.empty(a.size, dtype=np.uint16)
+    lib().orc_vec_add(_p(out), _p(a), _p(b), a.size)
+    return out
+
+
+def rope(q, k, n_heads, n_kv, hd, start_pos, N, theta, neox, q_stride=None, k_stride=None):
+    """Returns rotated copies (q, k); k may be None."""
+    q = np.array(q, dtype=np.uint16, copy=True).ravel()
+    k = np.array(k, dtype=np.uint16, copy=True).ravel() if k is not None else None
+    lib().orc_rope(_p(q), _p(k), n_heads, n_kv if k is not None else 0, hd, start_pos, N,
+                   q_stride or n_heads * hd, k_stride or n_kv * hd, float(theta), 1 if neox else 0)
+    return q, k
+
+
+def qk_post(q, k, v, q_norm, k_norm, norm_fp32, eps, k_cache, v_cache, k_scales, v_scales,
+            n_heads, n_kv, hd, chd, start_pos, N, theta, neox, kv_int8):
+    """q, k rotated in place (copies returned); caches/scales updated in place."""
+    q = np.array(q, dtype=np.uint16, copy=True).ravel()
+    k = np.array(k, dtype=np.uint16, copy=True).ravel()
+    v = _c(v, np.uint16)
+    wt = np.float32 if norm_fp32 else np.uint16
+    qn = _c(q_norm, wt) if q_norm is not None else None
+    kn = _c(k_norm, wt) if k_norm is not None else None
+    lib().orc_qk_post(_p(q), _p(k), _p(v), _p(qn), _p(kn), 1 if norm_fp32 else 0, float(eps),
+                      _p(k_cache), _p(v_cache), _p(k_scales), _p(v_scales),
+                      n_heads, n_kv, hd, chd, start_pos, N, float(theta), 1 if neox else 0, 1 if kv_int8 else 0)
+    return q, k
+
+
+def embed_row(W, ggml_type, token, hidden):
+    W = _c(W, np.uint8)
+    out = np.empty(hidden, dtype=np.uint16)
+    lib().orc_embed_row(_p(out), _p(W), ggml_type, int(token), hidden)
+    return out
+
+
+def argmax(x):
+    x = _c(x, np.float32).ravel()
+    return lib().orc_argmax(_p(x), x.size)
+
+
+def attn_prefill_int8(q, k, v, n_heads, n_kv, hd, chd, N, start_pos, scale, ks, vs, window):
+    q, k, v = _c(q, np.uint16), _c(k, np.int8), _c(v, np.int8)
+    ks = _c(ks, np.float32) if ks is not None else None
+    vs = _c(vs, np.float32) if vs is not None else None
+    out = np.empty(N * n_heads * hd, dtype=np.uint16)
+    lib().orc_attn_prefill_int8(_p(out), _p(q), _p(k), _p(v), n_heads, n_kv, hd, chd, N, start_pos, float(scale),
+                                _p(ks), _p(vs), window)
     return out

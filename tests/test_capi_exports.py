@@ -78,3 +78,18 @@ def test_argument_validation_without_gpu():
     assert l.jllm_hip_gemv_quant(None, None, 13, None, 4, 256, None) != 0
     assert l.jllm_hip_gemm_quant_batched(None, None, 12, None, 4, 4, 300, None) == -1
     assert l.jllm_hip_quantize_mmq_q8_1(None, None, 1, 128, 64, 1, None) == -1
+
+
+def test_layer_op_argument_validation_without_gpu():
+    l = jllm.lib()
+    assert l.jllm_hip_fused_rmsnorm_residual(None, None, None, None, 1, 255, 1e-6, 1, None) == -1   # odd dim
+    assert l.jllm_hip_fused_rmsnorm_residual(None, None, None, None, 0, 256, 1e-6, 1, None) == 0    # no rows
+    assert l.jllm_hip_rope_inplace(None, None, 4, 2, 130, 0, 1e6, 1, None) == -1                   # hd > 128
+    assert l.jllm_hip_rope_precompute_table(4096, 128, 1e6) == 0
+    assert l.jllm_hip_qk_norm_rope_store_kv(None, None, None, None, None, 1, 1e-6, None, None, None, None,
+                                            1024, 32, 8, 128, 64, 0, 1, 1e6, 1, 1, None) == -1    # chd < hd
+    assert l.jllm_hip_dequant_embedding_row(None, None, 13, 0, 2560, None) == -2
+    assert l.jllm_hip_dequant_embedding_rows(None, None, 12, None, 4, 2560, 0, None) == -1          # vocab 0
+    assert l.jllm_hip_argmax_f32(None, None, 10, None) == -1
+    assert l.jllm_hip_flash_attention_prefill_batched(None, None, None, None, 32, 8, 128, 128, 0, 0, 1.0, 1,
+                                                      None, None, 0, None) == 0                     # N = 0

@@ -1,0 +1,194 @@
+"""Pins the decoder-layer oracle (oracle/layer_oracle.c) independently of itself.
+
+Checks come from the reference's own known-answer tests (tests/test_kernels.cu
+of genie-ai-runtime: RMSNorm of x + residual = 2 is 1.0, silu(1) * 2 =
+1.4621, RoPE at position 0 is the identity), closed forms, float64 numpy
+restatements written from the textbook definitions, and identities (pair
+norm, rotation composition).  Runs on the CPU.
+"""
+import numpy as np
+import pytest
+
+import np_ref
+import oracle
+import synth
+
+
+def f16b(a):
+    return np.asarray(a, np.float32).astype(np.float16).view(np.uint16)
+
+
+def f64(bits):
+    return np_ref.f16(bits)
+
+
+# ---- RMSNorm ---------------------------------------------------------------
+
+def test_rmsnorm_known_answer():
+    # test_kernels.cu: x = 1, residual = 1, weight = 1 -> 1.0 (sum is 2)
+    x = f16b(np.ones(256))
+    out = f64(oracle.rmsnorm(x, x, np.ones(256, np.float32), 1, 256, 1e-6, True))
+    assert np.all(np.abs(out - 1.0) < 1e-3)
+
+
+@pytest.mark.parametrize("w_fp32", [True, False])
+def test_rmsnorm_closed_forms(w_fp32):
+    dim, eps = 512, 1e-2
+    g = synth.rng(3)
+    w = (1.0 + 0.5 * g.standard_normal(dim)).astype(np.float32)
+    wbits = w if w_fp32 else f16b(w)
+    wv = w.astype(np.float64) if w_fp32 else f64(wbits)
+    # constant row c with residual r: every element is (c+r)/sqrt((c+r)^2 + eps) * w
+    c, r = 0.375, 0.125
+    out = f64(oracle.rmsnorm(f16b(np.full(dim, c)), f16b(np.full(dim, r)), wbits, 1, dim, eps, w_fp32))
+    want = (c + r) / np.sqrt((c + r) ** 2 + eps) * wv
+    assert np.allclose(out, want, rtol=1e-3, atol=1e-6)
+    # one-hot row a*e_k: a / sqrt(a^2/dim + eps) * w_k at k, 0 elsewhere
+    k, a = 137, 3.0
+    x = np.zeros(dim); x[k] = a
+    out = f64(oracle.rmsnorm(f16b(x), None, wbits, 1, dim, eps, w_fp32))
+    want = np.zeros(dim); want[k] = a / np.sqrt(a * a / dim + eps) * wv[k]
+    assert np.allclose(out, want, rtol=1e-3, atol=1e-6)
+
+
+def test_rmsnorm_random_rows_vs_float64():
+    rows, dim, eps = 7, 2560, 1e-6
+    g = synth.rng(4)
+    x, res = synth.x_f16(g, rows * dim), synth.x_f16(g, rows * dim)
+    w = (1.0 + 0.02 * g.standard_normal(dim)).astype(np.float32)
+    out = f64(oracle.rmsnorm(x, res, w, rows, dim, eps, True)).reshape(rows, dim)
+    v = (f64(x) + f64(res)).reshape(rows, dim)
+    want = v / np.sqrt((v * v).mean(axis=1, keepdims=True) + eps) * w
+    assert np.all(np.abs(out - want) <= 2.0 ** -10 * np.abs(want) + 1e-6)
+
+
+# ---- SwiGLU / residual add ---------------------------------------------------
+
+def test_swiglu_known_answers_and_float64():
+    out = f64(oracle.swiglu(f16b([1.0, 0.0, 20.0, -20.0]), f16b([2.0, 5.0, 0.5, 3.0])))
+    assert abs(out[0] - 1.4621) < 1e-3                        # test_kernels.cu
+    assert out[1] == 0.0 and abs(out[2] - 10.0) < 1e-2 and abs(out[3]) < 1e-6
+    g = synth.rng(5)
+    a, b = synth.x_f16(g, 4096), synth.x_f16(g, 4096)
+    ga, ub = f64(a), f64(b)
+    want = ga / (1.0 + np.exp(-ga)) * ub
+    got = f64(oracle.swiglu(a, b))
+    assert np.all(np.abs(got - want) <= 2.0 ** -10 * np.abs(want) + 1e-7)
+
+
+def test_vec_add_is_rounded_sum():
+    g = synth.rng(6)
+    a, b = synth.x_f16(g, 5000), synth.x_f16(g, 5000)
+    want = (f64(a) + f64(b)).astype(np.float16).view(np.uint16)   # exact sum, one rounding
+    assert np.array_equal(oracle.vec_add(a, b), want)
+
+
+# ---- RoPE --------------------------------------------------------------------
+
+@pytest.mark.parametrize("neox", [True, False])
+def test_rope_position_zero_identity(neox):
+    g = synth.rng(8)
+    q, k = synth.x_f16(g, 4 * 128), synth.x_f16(g, 2 * 128)
+    q2, k2 = oracle.rope(q, k, 4, 2, 128, 0, 1, 1e6, neox)
+    assert np.array_equal(q2, q) and np.array_equal(k2, k)
+
+
+@pytest.mark.parametrize("neox", [True, False])
+def test_rope_one_hot_pairs(neox):
+    hd, theta, pos = 64, 10000.0, 37
+    h2 = hd // 2
+    for i in (0, 1, 5, h2 - 1):
+        x = np.zeros(hd); x[i if neox else 2 * i] = 1.0
+        q2, _ = oracle.rope(f16b(x), None, 1, 0, hd, pos, 1, theta, neox)
+        out = f64(q2)
+        ang = pos * theta ** (-2.0 * i / hd)
+        i0, i1 = (i, i + h2) if neox else (2 * i, 2 * i + 1)
+        want = np.zeros(hd); want[i0], want[i1] = np.cos(ang), np.sin(ang)
+        assert np.allclose(out, want, atol=2e-3), i
+
+
+def test_rope_norm_and_composition():
+    hd, theta = 128, 1e6
+    g = synth.rng(9)
+    q = synth.x_f16(g, 3 * hd)
+    a, _ = oracle.rope(q, None, 3, 0, hd, 200, 1, theta, True)
+    v, w = f64(q).reshape(3, 2, 64), f64(a).reshape(3, 2, 64)
+    assert np.allclose(np.hypot(w[:, 0], w[:, 1]), np.hypot(v[:, 0], v[:, 1]), rtol=2e-3, atol=2e-3)
+    # R(120) R(80) = R(200)
+    b, _ = oracle.rope(q, None, 3, 0, hd, 80, 1, theta, True)
+    c, _ = oracle.rope(b, None, 3, 0, hd, 120, 1, theta, True)
+    assert np.allclose(f64(c), f64(a), atol=1e-2)
+
+
+def test_rope_batched_is_per_token():
+    hd, H, KV, N = 64, 4, 2, 5
+    g = synth.rng(10)
+    q, k = synth.x_f16(g, N * H * hd), synth.x_f16(g, N * KV * hd)
+    qb, kb = oracle.rope(q, k, H, KV, hd, 11, N, 5e5, True)
+    for t in range(N):
+        qt, kt = oracle.rope(q[t * H * hd:(t + 1) * H * hd], k[t * KV * hd:(t + 1) * KV * hd], H, KV, hd,
+                             11 + t, 1, 5e5, True)
+        assert np.array_equal(qb[t * H * hd:(t + 1) * H * hd], qt)
+        assert np.array_equal(kb[t * KV * hd:(t + 1) * KV * hd], kt)
+
+
+# ---- attention front (q/k norm, rope, KV store) --------------------------------
+
+def test_qk_post_composes_the_pinned_pieces():
+    H, KV, hd, N, pos0, eps, theta = 4, 2, 128, 3, 5, 1e-6, 1e6
+    g = synth.rng(11)
+    q, k, v = synth.x_f16(g, N * H * hd), synth.x_f16(g, N * KV * hd), synth.x_f16(g, N * KV * hd)
+    qn = (1 + 0.1 * g.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.1 * g.standard_normal(hd)).astype(np.float32)
+    kc = np.zeros((pos0 + N, KV, hd), np.int8); vc = np.zeros_like(kc)
+    ksc = np.zeros((pos0 + N, KV), np.float32); vsc = np.zeros_like(ksc)
+    q2, k2 = oracle.qk_post(q, k, v, qn, kn, True, eps, kc, vc, ksc, vsc, H, KV, hd, hd, pos0, N, theta, True, True)
+    qr = oracle.rmsnorm(q, None, qn, N * H, hd, eps, True)
+    kr = oracle.rmsnorm(k, None, kn, N * KV, hd, eps, True)
+    qr, kr = oracle.rope(qr, kr, H, KV, hd, pos0, N, theta, True)
+    assert np.array_equal(q2, qr) and np.array_equal(k2, kr)
+    kq, ks = oracle.fp16_to_int8(kr, N * KV, hd)
+    vq, vs = oracle.fp16_to_int8(v, N * KV, hd)
+    assert np.array_equal(kc[pos0:].reshape(N * KV, hd), kq) and np.array_equal(ksc[pos0:].ravel(), ks)
+    assert np.array_equal(vc[pos0:].reshape(N * KV, hd), vq) and np.array_equal(vsc[pos0:].ravel(), vs)
+    assert not kc[:pos0].any()
+
+
+# ---- embedding / argmax ----------------------------------------------------------
+
+@pytest.mark.parametrize("t", [12, 14])
+def test_embed_row_is_rounded_dequant(t):
+    g = synth.rng(12)
+    W = synth.weights(g, t, 20, 512)
+    out = f64(oracle.embed_row(W, t, 13, 512))
+    want = np_ref.dequant(W, t, 20, 512)[13]
+    assert np.array_equal(out, want.astype(np.float16).astype(np.float64))
+
+
+def test_argmax_first_finite_max():
+    g = synth.rng(13)
+    x = g.standard_normal(151936).astype(np.float32)
+    assert oracle.argmax(x) == int(np.argmax(x))
+    x[[5, 900]] = 100.0
+    x[7] = np.inf
+    x[8] = np.nan
+    assert oracle.argmax(x) == 5
+    assert oracle.argmax(np.full(10, np.nan, np.float32)) == 0
+
+
+# ---- prefill attention -----------------------------------------------------------
+
+@pytest.mark.parametrize("start,N,window", [(0, 9, 0), (40, 24, 0), (40, 24, 16)])
+def test_prefill_attention_vs_float64(start, N, window):
+    H, KV, hd = 8, 2, 64
+    g = synth.rng(14)
+    ctx = start + N
+    q = synth.x_f16(g, N * H * hd)
+    k, v = synth.kv_int8(g, ctx, KV, hd), synth.kv_int8(g, ctx, KV, hd)
+    ks, vs = synth.kv_scales(g, ctx, KV), synth.kv_scales(g, ctx, KV)
+    scale = 1.0 / np.sqrt(hd)
+    out = f64(oracle.attn_prefill_int8(q, k, v, H, KV, hd, hd, N, start, scale, ks, vs, window)).reshape(N, H, hd)
+    for t in range(N):
+        want = np_ref.attention_f64(q[t * H * hd:(t + 1) * H * hd], k, v, ks, vs, H, KV, hd, start + t + 1, scale,
+                                    window)
+        assert np.allclose(out[t], want, rtol=2e-3, atol=2e-3 * np.abs(want).max()), t
