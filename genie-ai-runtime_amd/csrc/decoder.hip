@@ -1,0 +1,254 @@
+// decoder.hip -- the Llama/Qwen3 decoder loop that drives the quantized
+// matmuls: batched prefill of a prompt and greedy decode steps, with an
+// INT8 (or FP16) KV cache, all on one HIP stream.
+//
+// Layer order and arithmetic follow the reference engine:
+//   decode step  Engine::decode_step / transformer_layer /
+//                transformer_layer_attn_compute / _attn_block / _ffn_block
+//                (src/engine/decode.cu:2101-2158, :1168-1246, :1437-1520)
+//   prefill      Engine::generate Path B + transformer_prefill
+//                (src/engine/decode.cu:2779-2807, :1760-1884) and the
+//                first-token sampling from the last prefill row (:2950-2990)
+//   sampling     greedy (src/engine/sample.cpp:160-170), on the GPU here
+// with two MI355X-specific changes that do not alter the arithmetic: the
+// q/k RMSNorm + RoPE + KV quantisation of each layer is one fused launch
+// (the intermediate fp16 roundings are kept), and the greedy argmax runs on
+// the device so the sampled token id never leaves HBM -- the next step's
+// embedding gather reads it there, and a whole generation needs no host
+// synchronisation until the caller copies the tokens out.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+#include <new>
+#include "capi_common.h"
+
+using jllm_hip::launch_status;
+
+struct jllm_hip_decoder {
+    jllm_hip_decoder_config cfg;
+    jllm_hip_model_weights mw;
+    jllm_hip_layer_weights* lw = nullptr;
+    // KV cache, per layer [max_seq][n_kv * head_dim] (int8 or fp16) and
+    // per-(position, kv head) fp32 scales
+    uint8_t* kc = nullptr;
+    uint8_t* vc = nullptr;
+    float* ks = nullptr;
+    float* vs = nullptr;
+    size_t layer_kv_bytes = 0, layer_sc_floats = 0;
+    // activations, sized for max_batch rows (prefill) and one row (decode)
+    uint16_t *x, *x2, *normed, *q, *k, *v, *attn, *proj, *gate, *up, *act;
+    float* logits;
+    int32_t* tok;            // device token scratch [max_batch]
+    void* arena = nullptr;   // one allocation for everything above
+    int max_batch = 0;
+};
+
+namespace {
+
+bool valid_type(int t) { return t == 12 || t == 14; }
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+#define TRY(call)                                        \
+    do {                                                 \
+        int _st = (call);                                \
+        if (_st != JLLM_OK) return _st;                  \
+    } while (0)
+
+float attn_scale(const jllm_hip_decoder_config& c) { return 1.0f / sqrtf((float)c.head_dim); }
+
+uint8_t* layer_k(jllm_hip_decoder* d, int l) { return d->kc + (size_t)l * d->layer_kv_bytes; }
+uint8_t* layer_v(jllm_hip_decoder* d, int l) { return d->vc + (size_t)l * d->layer_kv_bytes; }
+float* layer_ks(jllm_hip_decoder* d, int l) { return d->ks + (size_t)l * d->layer_sc_floats; }
+float* layer_vs(jllm_hip_decoder* d, int l) { return d->vs + (size_t)l * d->layer_sc_floats; }
+
+// One decoder layer for one token at position pos; x is updated in place
+// (transformer_layer, decode.cu:1168-1246).
+int decode_layer(jllm_hip_decoder* d, int l, int pos, void* st) {
+    const jllm_hip_decoder_config& c = d->cfg;
+    const jllm_hip_layer_weights& w = d->lw[l];
+    const int H = c.hidden_dim, QD = c.n_heads * c.head_dim, KVD = c.n_kv_heads * c.head_dim, I = c.intermediate_dim;
+    const size_t row = (size_t)KVD * (c.kv_int8 ? 1 : 2);
+    TRY(jllm_hip_fused_rmsnorm_residual(d->normed, d->x, nullptr, w.rms_attn, 1, H, c.rms_eps, c.norm_fp32, st));
+    TRY(jllm_hip_gemv_quant_triple(d->q, w.wq, w.type_wq, QD, d->k, w.wk, w.type_wk, KVD, d->v, w.wv, w.type_wv, KVD,
+                                   d->normed, H, st));
+    TRY(jllm_hip_qk_norm_rope_store_kv(d->q, d->k, d->v, w.q_norm, w.k_norm, c.qk_norm_fp32, c.rms_eps,
+                                       layer_k(d, l) + (size_t)pos * row, layer_v(d, l) + (size_t)pos * row,
+                                       layer_ks(d, l) + (size_t)pos * c.n_kv_heads,
+                                       layer_vs(d, l) + (size_t)pos * c.n_kv_heads, KVD, c.n_heads, c.n_kv_heads,
+                                       c.head_dim, c.head_dim, pos, 1, c.rope_theta, c.rope_neox, c.kv_int8, st));
+    TRY(jllm_hip_flash_attention_decode(d->attn, d->q, layer_k(d, l), layer_v(d, l), c.n_heads, c.n_kv_heads,
+                                        c.head_dim, c.head_dim, pos + 1, attn_scale(c), c.kv_int8,
+                                        c.kv_int8 ? layer_ks(d, l) : nullptr, c.kv_int8 ? layer_vs(d, l) : nullptr, 0,
+                                        st));
+    TRY(jllm_hip_gemv_quant_add(d->x2, w.wo, w.type_wo, d->attn, d->x, H, QD, st));
+    TRY(jllm_hip_fused_rmsnorm_residual(d->normed, d->x2, nullptr, w.rms_ffn, 1, H, c.rms_eps, c.norm_fp32, st));
+    TRY(jllm_hip_gemv_quant_pair(d->gate, w.w_gate, w.type_w_gate, I, d->up, w.w_up, w.type_w_up, I, d->normed, H,
+                                 st));
+    TRY(jllm_hip_fused_swiglu(d->act, d->gate, d->up, 1, I, st));
+    TRY(jllm_hip_gemv_quant_add(d->x, w.w_down, w.type_w_down, d->act, d->x2, H, I, st));
+    return JLLM_OK;
+}
+
+// One layer over N prompt tokens at positions start..start+N-1; xb [N][H]
+// updated in place (transformer_prefill, decode.cu:1760-1884).
+int prefill_layer(jllm_hip_decoder* d, int l, int start, int N, void* st) {
+    const jllm_hip_decoder_config& c = d->cfg;
+    const jllm_hip_layer_weights& w = d->lw[l];
+    const int H = c.hidden_dim, QD = c.n_heads * c.head_dim, KVD = c.n_kv_heads * c.head_dim, I = c.intermediate_dim;
+    const size_t row = (size_t)KVD * (c.kv_int8 ? 1 : 2);
+    TRY(jllm_hip_fused_rmsnorm_residual(d->normed, d->x, nullptr, w.rms_attn, N, H, c.rms_eps, c.norm_fp32, st));
+    TRY(jllm_hip_gemm_quant_batched(d->q, w.wq, w.type_wq, d->normed, QD, N, H, st));
+    TRY(jllm_hip_gemm_quant_batched(d->k, w.wk, w.type_wk, d->normed, KVD, N, H, st));
+    TRY(jllm_hip_gemm_quant_batched(d->v, w.wv, w.type_wv, d->normed, KVD, N, H, st));
+    TRY(jllm_hip_qk_norm_rope_store_kv(d->q, d->k, d->v, w.q_norm, w.k_norm, c.qk_norm_fp32, c.rms_eps,
+                                       layer_k(d, l) + (size_t)start * row, layer_v(d, l) + (size_t)start * row,
+                                       layer_ks(d, l) + (size_t)start * c.n_kv_heads,
+                                       layer_vs(d, l) + (size_t)start * c.n_kv_heads, KVD, c.n_heads, c.n_kv_heads,
+                                       c.head_dim, c.head_dim, start, N, c.rope_theta, c.rope_neox, c.kv_int8, st));
+    TRY(jllm_hip_flash_attention_prefill_batched(d->attn, d->q, layer_k(d, l), layer_v(d, l), c.n_heads,
+                                                 c.n_kv_heads, c.head_dim, c.head_dim, N, start, attn_scale(c),
+                                                 c.kv_int8, c.kv_int8 ? layer_ks(d, l) : nullptr,
+                                                 c.kv_int8 ? layer_vs(d, l) : nullptr, 0, st));
+    TRY(jllm_hip_gemm_quant_batched(d->proj, w.wo, w.type_wo, d->attn, H, N, QD, st));
+    TRY(jllm_hip_vec_add(d->x2, d->x, d->proj, (int64_t)N * H, st));
+    TRY(jllm_hip_fused_rmsnorm_residual(d->normed, d->x2, nullptr, w.rms_ffn, N, H, c.rms_eps, c.norm_fp32, st));
+    TRY(jllm_hip_gemm_quant_batched(d->gate, w.w_gate, w.type_w_gate, d->normed, I, N, H, st));
+    TRY(jllm_hip_gemm_quant_batched(d->up, w.w_up, w.type_w_up, d->normed, I, N, H, st));
+    TRY(jllm_hip_fused_swiglu(d->act, d->gate, d->up, N, I, st));
+    TRY(jllm_hip_gemm_quant_batched(d->proj, w.w_down, w.type_w_down, d->act, H, N, I, st));
+    TRY(jllm_hip_vec_add(d->x, d->x2, d->proj, (int64_t)N * H, st));
+    return JLLM_OK;
+}
+
+// output norm -> lm_head (fp32 logits) -> greedy token into *out
+// (decode.cu:2147-2158 and :2956-2966; sample_greedy on the device)
+int head(jllm_hip_decoder* d, const uint16_t* xrow, int32_t* out, void* st) {
+    const jllm_hip_decoder_config& c = d->cfg;
+    TRY(jllm_hip_fused_rmsnorm_residual(d->normed, xrow, nullptr, d->mw.output_norm, 1, c.hidden_dim, c.rms_eps,
+                                        c.output_norm_fp32, st));
+    TRY(jllm_hip_gemv_quant_f32(d->logits, d->mw.output, d->mw.output_type, d->normed, c.vocab_size, c.hidden_dim,
+                                st));
+    if (out) TRY(jllm_hip_argmax_f32(out, d->logits, c.vocab_size, st));
+    return JLLM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+jllm_hip_decoder* jllm_hip_decoder_create(const jllm_hip_decoder_config* cfg, const jllm_hip_model_weights* mw,
+                                          const jllm_hip_layer_weights* layers, int max_batch) {
+    if (!cfg || !mw || !layers) return nullptr;
+    const jllm_hip_decoder_config& c = *cfg;
+    if (c.n_layers <= 0 || c.hidden_dim <= 0 || c.hidden_dim % 256 != 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 ||
+        c.head_dim <= 0 || (c.n_heads * c.head_dim) % 256 != 0 || c.intermediate_dim % 256 != 0 ||
+        c.intermediate_dim <= 0 || c.vocab_size <= 0 || c.max_seq <= 0 || max_batch <= 0) {
+        fprintf(stderr, "[decoder] invalid configuration\n");
+        return nullptr;
+    }
+    if (!valid_type(mw->embd_type) || !valid_type(mw->output_type) || !mw->tok_embd || !mw->output ||
+        !mw->output_norm) {
+        fprintf(stderr, "[decoder] embedding / output weights missing or not Q4_K/Q6_K\n");
+        return nullptr;
+    }
+    for (int l = 0; l < c.n_layers; l++) {
+        const jllm_hip_layer_weights& w = layers[l];
+        if (!valid_type(w.type_wq) || !valid_type(w.type_wk) || !valid_type(w.type_wv) || !valid_type(w.type_wo) ||
+            !valid_type(w.type_w_gate) || !valid_type(w.type_w_up) || !valid_type(w.type_w_down) || !w.rms_attn ||
+            !w.rms_ffn) {
+            fprintf(stderr, "[decoder] layer %d: weights missing or not Q4_K/Q6_K\n", l);
+            return nullptr;
+        }
+    }
+    jllm_hip_decoder* d = new (std::nothrow) jllm_hip_decoder();
+    if (!d) return nullptr;
+    d->cfg = c;
+    d->mw = *mw;
+    d->lw = new (std::nothrow) jllm_hip_layer_weights[c.n_layers];
+    if (!d->lw) { delete d; return nullptr; }
+    memcpy(d->lw, layers, sizeof(jllm_hip_layer_weights) * (size_t)c.n_layers);
+    d->max_batch = max_batch < c.max_seq ? max_batch : c.max_seq;
+
+    const size_t KVD = (size_t)c.n_kv_heads * c.head_dim, QD = (size_t)c.n_heads * c.head_dim;
+    const size_t B = (size_t)d->max_batch, H = c.hidden_dim, I = c.intermediate_dim;
+    d->layer_kv_bytes = align256((size_t)c.max_seq * KVD * (c.kv_int8 ? 1 : 2));
+    d->layer_sc_floats = align256((size_t)c.max_seq * c.n_kv_heads * 4) / 4;
+    size_t sizes[] = {
+        d->layer_kv_bytes * c.n_layers, d->layer_kv_bytes * c.n_layers,              // kc, vc
+        d->layer_sc_floats * 4 * c.n_layers, d->layer_sc_floats * 4 * c.n_layers,    // ks, vs
+        B * H * 2, B * H * 2, B * H * 2,                                             // x, x2, normed
+        B * QD * 2, B * KVD * 2, B * KVD * 2, B * QD * 2, B * H * 2,                 // q, k, v, attn, proj
+        B * I * 2, B * I * 2, B * I * 2,                                             // gate, up, act
+        (size_t)c.vocab_size * 4, B * 4};                                            // logits, tok
+    const int NB = sizeof(sizes) / sizeof(sizes[0]);
+    size_t total = 0;
+    for (int i = 0; i < NB; i++) total += align256(sizes[i]);
+    if (hipMalloc(&d->arena, total) != hipSuccess) {
+        fprintf(stderr, "[decoder] hipMalloc of %zu bytes failed\n", total);
+        delete[] d->lw;
+        delete d;
+        return nullptr;
+    }
+    // zero once (no stream capture is active at creation)
+    (void)hipMemset(d->arena, 0, total);
+    uint8_t* p = (uint8_t*)d->arena;
+    void* slot[17];
+    for (int i = 0; i < NB; i++) { slot[i] = p; p += align256(sizes[i]); }
+    d->kc = (uint8_t*)slot[0]; d->vc = (uint8_t*)slot[1]; d->ks = (float*)slot[2]; d->vs = (float*)slot[3];
+    d->x = (uint16_t*)slot[4]; d->x2 = (uint16_t*)slot[5]; d->normed = (uint16_t*)slot[6];
+    d->q = (uint16_t*)slot[7]; d->k = (uint16_t*)slot[8]; d->v = (uint16_t*)slot[9];
+    d->attn = (uint16_t*)slot[10]; d->proj = (uint16_t*)slot[11];
+    d->gate = (uint16_t*)slot[12]; d->up = (uint16_t*)slot[13]; d->act = (uint16_t*)slot[14];
+    d->logits = (float*)slot[15]; d->tok = (int32_t*)slot[16];
+    return d;
+}
+
+void jllm_hip_decoder_destroy(jllm_hip_decoder* d) {
+    if (!d) return;
+    if (d->arena) (void)hipFree(d->arena);
+    delete[] d->lw;
+    delete d;
+}
+
+int jllm_hip_decoder_prefill(jllm_hip_decoder* d, const int32_t* tokens, int N, int start_pos, int32_t* next_token,
+                             void* stream) {
+    if (!d || !tokens || N <= 0 || start_pos < 0 || start_pos + N > d->cfg.max_seq) return JLLM_ERR_INVALID;
+    const jllm_hip_decoder_config& c = d->cfg;
+    // chunks of at most max_batch tokens; each chunk attends to all earlier KV
+    for (int c0 = 0; c0 < N; c0 += d->max_batch) {
+        const int n = N - c0 < d->max_batch ? N - c0 : d->max_batch;
+        TRY(jllm_hip_dequant_embedding_rows(d->x, d->mw.tok_embd, d->mw.embd_type, tokens + c0, n, c.hidden_dim,
+                                            c.vocab_size, stream));
+        for (int l = 0; l < c.n_layers; l++) TRY(prefill_layer(d, l, start_pos + c0, n, stream));
+        if (c0 + n == N) TRY(head(d, d->x + (size_t)(n - 1) * c.hidden_dim, next_token, stream));
+    }
+    return JLLM_OK;
+}
+
+int jllm_hip_decoder_step(jllm_hip_decoder* d, const int32_t* token, int pos, int32_t* next_token, void* stream) {
+    if (!d || !token || pos < 0 || pos >= d->cfg.max_seq) return JLLM_ERR_INVALID;
+    const jllm_hip_decoder_config& c = d->cfg;
+    TRY(jllm_hip_dequant_embedding_rows(d->x, d->mw.tok_embd, d->mw.embd_type, token, 1, c.hidden_dim, c.vocab_size,
+                                        stream));
+    for (int l = 0; l < c.n_layers; l++) TRY(decode_layer(d, l, pos, stream));
+    return head(d, d->x, next_token, stream);
+}
+
+int jllm_hip_decoder_generate(jllm_hip_decoder* d, const int32_t* prompt, int n_prompt, int n_gen, int32_t* out,
+                              void* stream) {
+    if (!d || !prompt || !out || n_prompt <= 0 || n_gen <= 0 || n_prompt + n_gen - 1 > d->cfg.max_seq)
+        return JLLM_ERR_INVALID;
+    TRY(jllm_hip_decoder_prefill(d, prompt, n_prompt, 0, out, stream));
+    for (int i = 1; i < n_gen; i++) TRY(jllm_hip_decoder_step(d, out + i - 1, n_prompt + i - 1, out + i, stream));
+    return JLLM_OK;
+}
+
+int jllm_hip_decoder_copy_logits(const jllm_hip_decoder* d, float* dst, void* stream) {
+    if (!d || !dst) return JLLM_ERR_INVALID;
+    return launch_status(hipMemcpyAsync(dst, d->logits, (size_t)d->cfg.vocab_size * 4, hipMemcpyDeviceToDevice,
+                                        (hipStream_t)stream), "decoder");
+}
+
+}  // extern "C"

@@ -236,6 +236,68 @@ int jllm_hip_dequant_embedding_rows(uint16_t* dst, const void* W, int ggml_type,
  * sample_greedy, src/engine/sample.cpp:160-170. */
 int jllm_hip_argmax_f32(int32_t* out, const float* logits, int n, void* stream);
 
+/* ---- decoder loop (the engine-side caller of the kernels above) ---- */
+
+/* Model shape (ModelConfig, include/jllm_engine.h:59; Llama/Qwen3 family: RMSNorm,
+ * GQA attention with optional per-head q/k RMSNorm, RoPE, SwiGLU FFN).
+ * hidden_dim, n_heads*head_dim and intermediate_dim are multiples of 256. */
+typedef struct {
+    int   n_layers, hidden_dim, n_heads, n_kv_heads, head_dim, intermediate_dim, vocab_size;
+    int   max_seq;            /* KV-cache positions                              */
+    float rms_eps, rope_theta;
+    int   rope_neox;          /* 1: pairs (i, i + hd/2) (Qwen3)                  */
+    int   kv_int8;            /* 1: INT8 KV cache with per-(pos, head) scales   */
+    int   norm_fp32;          /* rms_attn / rms_ffn weights fp32 (1) or fp16 (0) */
+    int   qk_norm_fp32;       /* q_norm / k_norm weights fp32 (1) or fp16 (0)    */
+    int   output_norm_fp32;   /* output_norm weight fp32 (1) or fp16 (0)         */
+} jllm_hip_decoder_config;
+
+/* Device pointers of one layer (LayerWeights, include/jllm_engine.h:165); matrix
+ * types are 12 (Q4_K) or 14 (Q6_K); q_norm/k_norm may be NULL. */
+typedef struct {
+    const void *rms_attn, *rms_ffn, *q_norm, *k_norm;
+    const void *wq, *wk, *wv, *wo, *w_gate, *w_up, *w_down;
+    int type_wq, type_wk, type_wv, type_wo, type_w_gate, type_w_up, type_w_down;
+} jllm_hip_layer_weights;
+
+typedef struct {
+    const void* tok_embd;  int embd_type;      /* [vocab][hidden] Q4_K/Q6_K (may alias output) */
+    const void* output_norm;                   /* [hidden]                                      */
+    const void* output;    int output_type;    /* lm_head [vocab][hidden]                       */
+} jllm_hip_model_weights;
+
+typedef struct jllm_hip_decoder jllm_hip_decoder;
+
+/* Allocates the KV cache (n_layers x max_seq) and the activation buffers
+ * for prefill chunks of up to max_batch tokens, in one device allocation
+ * freed by jllm_hip_decoder_destroy.  The weights stay owned by the caller.
+ * NULL on an invalid configuration or allocation failure. */
+jllm_hip_decoder* jllm_hip_decoder_create(const jllm_hip_decoder_config* cfg, const jllm_hip_model_weights* mw,
+                                          const jllm_hip_layer_weights* layers, int max_batch);
+void jllm_hip_decoder_destroy(jllm_hip_decoder* d);
+
+/* Prefill N prompt tokens (DEVICE int32 ids) at positions start_pos..,
+ * layer-major in chunks of max_batch tokens, then the greedy next token into
+ * *next_token (DEVICE).  Engine::generate Path B + transformer_prefill +
+ * first-token sampling (src/engine/decode.cu:2779-2807, :1760-1884,
+ * :2950-2990). */
+int jllm_hip_decoder_prefill(jllm_hip_decoder* d, const int32_t* tokens, int N, int start_pos, int32_t* next_token,
+                             void* stream);
+
+/* One greedy decode step: embed *token (DEVICE) at position pos, all layers,
+ * output norm, lm_head, argmax into *next_token (DEVICE).
+ * Engine::decode_step (src/engine/decode.cu:2101-2236, greedy sampling). */
+int jllm_hip_decoder_step(jllm_hip_decoder* d, const int32_t* token, int pos, int32_t* next_token, void* stream);
+
+/* prefill(prompt) then n_gen - 1 decode steps; out[n_gen] (DEVICE) receives
+ * the generated ids.  Asynchronous: no host synchronisation inside. */
+int jllm_hip_decoder_generate(jllm_hip_decoder* d, const int32_t* prompt, int n_prompt, int n_gen, int32_t* out,
+                              void* stream);
+
+/* Enqueue a copy of the fp32 logits [vocab] of the last prefill/step into
+ * dst (device memory). */
+int jllm_hip_decoder_copy_logits(const jllm_hip_decoder* d, float* dst, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,134 @@
+"""CPU restatement of the reference engine's greedy decoder loop, composed
+from the pinned oracle kernels -- TEST INFRASTRUCTURE ONLY (tests/ use it
+as the checker of the GPU decoder; no product path may import it).
+
+Follows src/engine/decode.cu of genie-ai-runtime:
+  decode step   Engine::decode_step :2101-2158 -> transformer_layer
+                :1168-1246 -> transformer_layer_attn_compute :1437-1496,
+                _attn_block :1498-1511, _ffn_block :1513-1522
+  prefill       Path B :2779-2807 -> transformer_prefill :1760-1884, first
+                token from the last prefill row :2950-2990
+  sampling      sample_greedy, src/engine/sample.cpp:160-170
+and the GEMV dispatch of gemv_q4.cu: gemv_quant / _pair (both Q4_K) /
+_triple -> int8 MMVQ on the q8_1-quantised activation; gemv_quant_add and
+gemv_quant_f32 of Q6_K -> float dequant (gemv_quant_cpu arithmetic);
+gemm_quant_batched -> MMQ for N > 1, gemv_quant for N == 1.
+
+A model is the dict of decoder.synth_np (raw GGUF block bytes as numpy).
+"""
+import numpy as np
+
+import oracle
+
+
+def _f16(a):
+    """fp32 values -> fp16 bit patterns (RNE)."""
+    return np.asarray(a, np.float32).astype(np.float16).view(np.uint16)
+
+
+def _f32(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+def mmvq_f16(W, t, x, M, K):
+    return _f16(oracle.mmvq(W, t, oracle.quantize_q8_1(x, K), M, K))
+
+
+def pair(W0, t0, W1, t1, x, M, K):
+    if t0 == 12 and t1 == 12:
+        return mmvq_f16(W0, t0, x, M, K), mmvq_f16(W1, t1, x, M, K)
+    return _f16(oracle.gemv_quant_cpu(W0, t0, x, M, K)), _f16(oracle.gemv_quant_cpu(W1, t1, x, M, K))
+
+
+def gemv_add(W, t, x, res, M, K):
+    """gemv_quant_add: half(half(W.x) + residual), float dequant."""
+    proj = _f32(_f16(oracle.gemv_quant_cpu(W, t, x, M, K)))
+    return _f16(proj + _f32(res))
+
+
+def gemm(W, t, x, M, N, K):
+    """gemm_quant_batched: [N][M] fp16."""
+    if N == 1:
+        return mmvq_f16(W, t, x, M, K)
+    Npad = (N + 63) // 64 * 64
+    q8 = oracle.quantize_mmq(x, N, K, Npad, t == 12)
+    return _f16(oracle.mmq(W, t, q8, M, N, K, Npad)).ravel()
+
+
+class OracleDecoder:
+    def __init__(self, shape, model, max_seq, kv_int8=True):
+        self.s, self.m = shape, model
+        KV, hd = shape.n_kv_heads, shape.head_dim
+        self.kc = [np.zeros((max_seq, KV, hd), np.int8) for _ in range(shape.n_layers)]
+        self.vc = [np.zeros((max_seq, KV, hd), np.int8) for _ in range(shape.n_layers)]
+        self.ks = [np.zeros((max_seq, KV), np.float32) for _ in range(shape.n_layers)]
+        self.vs = [np.zeros((max_seq, KV), np.float32) for _ in range(shape.n_layers)]
+        self.logits = None
+
+    def _embed(self, tokens):
+        s = self.s
+        return np.concatenate([oracle.embed_row(self.m["tok_embd"], self.m["embd_type"], t, s.hidden_dim)
+                               for t in tokens])
+
+    def _head(self, xrow):
+        s = self.s
+        normed = oracle.rmsnorm(xrow, None, self.m["output_norm"], 1, s.hidden_dim, s.rms_eps, True)
+        self.logits = oracle.gemv_quant_cpu(self.m["output"], self.m["output_type"], normed, s.vocab_size,
+                                            s.hidden_dim)
+        return oracle.argmax(self.logits)
+
+    def _attn_front(self, l, L, q, k, v, start, N):
+        s = self.s
+        return oracle.qk_post(q, k, v, L["q_norm"], L["k_norm"], True, s.rms_eps, self.kc[l], self.vc[l],
+                              self.ks[l], self.vs[l], s.n_heads, s.n_kv_heads, s.head_dim, s.head_dim, start, N,
+                              s.rope_theta, True, True)
+
+    def prefill(self, tokens, start=0):
+        s = self.s
+        H, QD, KVD, I = s.hidden_dim, s.n_heads * s.head_dim, s.n_kv_heads * s.head_dim, s.intermediate_dim
+        N = len(tokens)
+        x = self._embed(tokens)
+        for l, L in enumerate(self.m["layers"]):
+            T = L["types"]
+            normed = oracle.rmsnorm(x, None, L["rms_attn"], N, H, s.rms_eps, True)
+            q = gemm(L["wq"], T["wq"], normed, QD, N, H)
+            k = gemm(L["wk"], T["wk"], normed, KVD, N, H)
+            v = gemm(L["wv"], T["wv"], normed, KVD, N, H)
+            q, k = self._attn_front(l, L, q, k, v, start, N)
+            attn = oracle.attn_prefill_int8(q, self.kc[l], self.vc[l], s.n_heads, s.n_kv_heads, s.head_dim,
+                                            s.head_dim, N, start, 1.0 / np.sqrt(s.head_dim), self.ks[l], self.vs[l],
+                                            0)
+            x2 = oracle.vec_add(x, gemm(L["wo"], T["wo"], attn, H, N, QD))
+            normed = oracle.rmsnorm(x2, None, L["rms_ffn"], N, H, s.rms_eps, True)
+            gate = gemm(L["w_gate"], T["w_gate"], normed, I, N, H)
+            up = gemm(L["w_up"], T["w_up"], normed, I, N, H)
+            act = oracle.swiglu(gate, up)
+            x = oracle.vec_add(x2, gemm(L["w_down"], T["w_down"], act, H, N, I))
+        return self._head(x[(N - 1) * H:])
+
+    def step(self, token, pos):
+        s = self.s
+        H, QD, KVD, I = s.hidden_dim, s.n_heads * s.head_dim, s.n_kv_heads * s.head_dim, s.intermediate_dim
+        x = self._embed([token])
+        for l, L in enumerate(self.m["layers"]):
+            T = L["types"]
+            normed = oracle.rmsnorm(x, None, L["rms_attn"], 1, H, s.rms_eps, True)
+            q = mmvq_f16(L["wq"], T["wq"], normed, QD, H)
+            k = mmvq_f16(L["wk"], T["wk"], normed, KVD, H)
+            v = mmvq_f16(L["wv"], T["wv"], normed, KVD, H)
+            q, k = self._attn_front(l, L, q, k, v, pos, 1)
+            attn = oracle.attn_decode_int8(q, self.kc[l], self.vc[l], s.n_heads, s.n_kv_heads, s.head_dim,
+                                           s.head_dim, pos + 1, 1.0 / np.sqrt(s.head_dim), self.ks[l], self.vs[l], 0,
+                                           oracle.decode_attn_splits(pos + 1))
+            x2 = gemv_add(L["wo"], T["wo"], attn, x, H, QD)
+            normed = oracle.rmsnorm(x2, None, L["rms_ffn"], 1, H, s.rms_eps, True)
+            gate, up = pair(L["w_gate"], T["w_gate"], L["w_up"], T["w_up"], normed, I, H)
+            act = oracle.swiglu(gate, up)
+            x = gemv_add(L["w_down"], T["w_down"], act, x2, H, I)
+        return self._head(x)
+
+    def generate(self, prompt, n_gen):
+        out = [self.prefill(list(prompt))]
+        for i in range(1, n_gen):
+            out.append(self.step(out[-1], len(prompt) + i - 1))
+        return out
