@@ -12,10 +12,12 @@ steps are replayed from a HIP graph.  value = algorithmic bytes / time.
 Also reported in the same JSON line: the roofline of the dominant kernel
 (gate/up pair GEMV, timed on its stream with HIP events), the int8 MMQ
 prefill GEMM, INT8-KV split-K decode attention,
+the end-to-end greedy decoder (configs[4]: TTFT, prefill and decode tok/s),
 and the CPU baseline (the oracle's restatement of the reference's host
 scalar GEMV, configs[0] shape, bounded sample).
 """
 import argparse
+import faulthandler
 import json
 import os
 import sys
@@ -35,7 +37,13 @@ def mat_bytes(t, rows, K):
     return rows * (K // 256) * BB[t]
 
 
+def stage(msg):
+    """Progress marker on stderr (the JSON result is the only stdout line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def main():
+    faulthandler.enable()
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
@@ -55,6 +63,7 @@ def main():
     import synth
 
     dev = torch.device("cuda:0")
+    stage("init cuda:0")
     torch.cuda.set_device(dev)
     g = synth.rng(20260101)
 
@@ -83,6 +92,8 @@ def main():
     vec_bytes_layer = 2 * (HID * 3 + QD + KVD * 2 + QD + HID * 2 + HID * 3 + FFN * 2 + FFN + HID * 2)
     step_bytes = L * (layer_bytes + vec_bytes_layer) + mat_bytes(Q6, VOCAB, HID) + 2 * HID + 4 * VOCAB
 
+    stage("weights resident; eager GEMV step")
+
     def step():
         for Lw in layers:
             jllm.gemv_quant_triple(yq, Lw["q"], Q4, QD, yk, Lw["k"], Q4, KVD, yv, Lw["v"], Q4, KVD, x_h, HID)
@@ -93,6 +104,7 @@ def main():
 
     step()
     torch.cuda.synchronize()
+    stage("graph capture of the GEMV step")
     eager_logits = logits.clone()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
@@ -132,6 +144,7 @@ def main():
                    "wall_s_timed": round(wall, 3)},
     }
 
+    stage("timed; pair-kernel roofline")
     # ---- dominant kernel: the gate/up pair GEMV (36 launches on distinct weights)
     pair_bytes = 2 * mat_bytes(Q4, FFN, HID) + 2 * HID + 4 * FFN
     gp = torch.cuda.CUDAGraph()
@@ -154,8 +167,15 @@ def main():
                        "bytes_per_launch": pair_bytes, "us_per_launch": round(us_launch, 3)}
 
     if not args.skip_extras:
+        stage("MMQ prefill GEMM")
         out["mmq"] = bench_mmq(np, torch, jllm, synth, up, dev, g)
+        stage("decode attention")
         out["attention"] = bench_attention(np, torch, jllm, synth, up, dev, g)
+        del layers, lm_head, graph, gp
+        torch.cuda.empty_cache()
+        stage("end-to-end decoder")
+        out["e2e"] = bench_e2e(np, torch, dev)
+    stage("CPU baseline")
     out["cpu_baseline"] = cpu_baseline(np, synth, args.cpu_seconds)
     print(json.dumps(out), flush=True)
 
@@ -236,6 +256,44 @@ def bench_attention(np, torch, jllm, synth, up, dev, g):
                                         "hbm_frac": round(by / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
         del caches
     return res
+
+
+def bench_e2e(np, torch, dev, n_prompt=512, n_gen=128):
+    """random-init Qwen3-4B-shaped decoder in Q4_K_M layout (36 layers,
+    Q6_K lm_head and every other ffn_down, fp32 norms ~ 1+N(0,0.02), RoPE base 1e6,
+    INT8 KV), a random 512-token prompt, then greedy decode to 128 tokens.  TTFT =
+    prefill of the prompt + first-token sampling; decode tok/s over the remaining
+    127 steps.  Everything runs through the decoder's C ABI on one stream."""
+    import decoder
+    shape = decoder.QWEN3_4B
+    model = decoder.synth_device(shape, 4242, dev)
+    torch.cuda.synchronize()
+    d = decoder.Decoder(shape, model, n_prompt + n_gen, max_batch=n_prompt)
+    prompt = torch.randint(0, shape.vocab_size, (n_prompt,), dtype=torch.int32, device=dev,
+                           generator=torch.Generator(device=dev).manual_seed(1))
+    toks = torch.zeros(n_gen, dtype=torch.int32, device=dev)
+    d.generate(prompt, 8, toks)                                   # warm-up (code objects, allocations)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    ev[0].record()
+    d.prefill(prompt, 0, toks[0:1])
+    ev[1].record()
+    for i in range(1, n_gen):
+        d.step(toks[i - 1:i], n_prompt + i - 1, toks[i:i + 1])
+    ev[2].record()
+    torch.cuda.synchronize()
+    ttft = ev[0].elapsed_time(ev[1])
+    dec_ms = ev[1].elapsed_time(ev[2])
+    gen = toks.cpu().numpy()
+    d.close()
+    del model
+    torch.cuda.empty_cache()
+    return {"workload": "configs[4]: Qwen3-4B-shaped Q4_K_M decoder, 36 layers, INT8 KV, prompt 512, "
+                        "128 greedy tokens", "ttft_ms": round(ttft, 2),
+            "prefill_tok_s": round(n_prompt / (ttft * 1e-3), 1),
+            "decode_tok_s": round((n_gen - 1) / (dec_ms * 1e-3), 1),
+            "decode_ms_per_token": round(dec_ms / (n_gen - 1), 3),
+            "distinct_tokens": int(len(set(gen.tolist()))), "first_tokens": gen[:8].tolist()}
 
 
 def cpu_baseline(np, synth, seconds):

@@ -38,15 +38,6 @@ class ModelW(ctypes.Structure):
     _fields_ = [("tok_embd", P), ("embd_type", I), ("output_norm", P), ("output", P), ("output_type", I)]
 
 
-jllm.SIGNATURES.update({
-    "jllm_hip_decoder_create": (P, [ctypes.POINTER(Config), ctypes.POINTER(ModelW), ctypes.POINTER(LayerW), I]),
-    "jllm_hip_decoder_destroy": (None, [P]),
-    "jllm_hip_decoder_prefill": (I, [P, P, I, I, P, P]),
-    "jllm_hip_decoder_step": (I, [P, P, I, P, P]),
-    "jllm_hip_decoder_generate": (I, [P, P, I, I, P, P]),
-    "jllm_hip_decoder_copy_logits": (I, [P, P, P]),
-})
-
 MATS = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
 
 
@@ -184,7 +175,8 @@ class Decoder:
         self._layers = arr
         self.mw = ModelW(model["tok_embd"].data_ptr(), model["embd_type"], model["output_norm"].data_ptr(),
                          model["output"].data_ptr(), model["output_type"])
-        self.h = jllm.lib().jllm_hip_decoder_create(ctypes.byref(self.cfg), ctypes.byref(self.mw), arr, max_batch)
+        self.h = jllm.lib().jllm_hip_decoder_create(ctypes.addressof(self.cfg), ctypes.addressof(self.mw),
+                                                    ctypes.addressof(arr), max_batch)
         if not self.h:
             raise jllm.JllmError("jllm_hip_decoder_create failed")
 

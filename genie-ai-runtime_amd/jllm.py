@@ -51,6 +51,13 @@ SIGNATURES = {
     "jllm_hip_dequant_embedding_row": (I, [P, P, I, I, I, P]),
     "jllm_hip_dequant_embedding_rows": (I, [P, P, I, P, I, I, I, P]),
     "jllm_hip_argmax_f32": (I, [P, P, I, P]),
+    # decoder loop; the struct arguments are passed by address
+    "jllm_hip_decoder_create": (P, [P, P, P, I]),
+    "jllm_hip_decoder_destroy": (None, [P]),
+    "jllm_hip_decoder_prefill": (I, [P, P, I, I, P, P]),
+    "jllm_hip_decoder_step": (I, [P, P, I, P, P]),
+    "jllm_hip_decoder_generate": (I, [P, P, I, I, P, P]),
+    "jllm_hip_decoder_copy_logits": (I, [P, P, P]),
 }
 
 

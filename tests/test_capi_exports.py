@@ -93,3 +93,15 @@ def test_layer_op_argument_validation_without_gpu():
     assert l.jllm_hip_argmax_f32(None, None, 10, None) == -1
     assert l.jllm_hip_flash_attention_prefill_batched(None, None, None, None, 32, 8, 128, 128, 0, 0, 1.0, 1,
                                                       None, None, 0, None) == 0                     # N = 0
+
+
+def test_pointer_returning_entry_points_keep_64_bit_results():
+    """Every declaration of jllm_hip.h that returns a pointer is bound with a
+    pointer restype in jllm.SIGNATURES itself (the ctypes default, int,
+    would truncate the handle to 32 bits), whatever was imported first."""
+    hdr = open(os.path.join(ROOT, "include", "jllm_hip.h")).read()
+    ptr_fns = re.findall(r"^[\w ]*\*\s*(jllm_hip_\w+)\s*\(", hdr, re.M)
+    assert "jllm_hip_decoder_create" in ptr_fns and "jllm_hip_get_splitk_partials" in ptr_fns
+    for n in ptr_fns:
+        assert jllm.SIGNATURES[n][0] in (ctypes.c_void_p, ctypes.c_char_p), n
+        assert getattr(jllm.lib(), n).restype in (ctypes.c_void_p, ctypes.c_char_p), n
