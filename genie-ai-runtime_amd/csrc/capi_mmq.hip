@@ -7,7 +7,7 @@
 using namespace jllm_hip;
 
 namespace {
-DeviceScratch g_q8;     // q8 activations [K/128][Npad] x 144 B, grown on demand, never freed
+DeviceScratch g_q8;     // quantised activations (fp16 codes + scale words), grown on demand, never freed
 
 int npad_of(int N) { return ((N + MMQ_TILE_N - 1) / MMQ_TILE_N) * MMQ_TILE_N; }
 
@@ -36,14 +36,17 @@ int run_mmq(const char* tag, void* y, const void* W, int type, const uint16_t* x
     }
     if (!aligned16(Wd)) return JLLM_ERR_INVALID;
     const int Npad = npad_of(N);
-    void* q8 = g_q8.get((size_t)(K / 128) * Npad * 144);
+    const size_t cb = mmq_codes_bytes(K, Npad);
+    uint8_t* q8 = (uint8_t*)g_q8.get(cb + mmq_scales_bytes(K, Npad));
     if (!q8) {
         fprintf(stderr, "[%s] q8 scratch allocation failed\n", tag);
         return JLLM_ERR_NOMEM;
     }
+    uint16_t* codes = (uint16_t*)q8;
+    uint32_t* scl = (uint32_t*)(q8 + cb);
     hipStream_t st = (hipStream_t)stream;
-    hipError_t e = quantize_mmq_launch(x, q8, N, K, Npad, type == 12, st);
-    if (e == hipSuccess) e = mmq_launch(y, (const uint8_t*)Wd, type, q8, M, N, K, Npad, out_kind, st);
+    hipError_t e = quantize_mmq_f16_launch(x, codes, scl, N, K, Npad, type == 12, st);
+    if (e == hipSuccess) e = mmq_launch(y, (const uint8_t*)Wd, type, codes, scl, M, N, K, Npad, out_kind, st);
     return launch_status(e, tag);
 }
 }  // namespace
@@ -66,19 +69,16 @@ int jllm_hip_gemm_quant_batched_f32(float* y, const void* W, int type, const uin
 }
 
 int jllm_hip_quantize_mmq_q8_1(const uint16_t* x, void* q8, int N, int K, int Npad, int ds4, void* stream) {
-    if (!x || !q8 || N < 0 || K <= 0 || K % 128 != 0 || Npad < N || Npad % MMQ_TILE_N != 0) return JLLM_ERR_INVALID;
+    if (!x || !q8 || N < 0 || K <= 0 || K % 128 != 0 || Npad < N || Npad % MMQ_REF_NPAD != 0) return JLLM_ERR_INVALID;
     if (Npad == 0) return JLLM_OK;
     return launch_status(quantize_mmq_launch(x, q8, N, K, Npad, ds4 != 0, (hipStream_t)stream), "GEMM");
 }
 
-int jllm_hip_mmq_subdots(int32_t* out, const void* W, int type, const void* q8, int M, int N, int K, int Npad,
+int jllm_hip_mmq_subdots(int32_t* out, const void* W, int type, const uint16_t* x, int M, int N, int K,
                          void* stream) {
-    if (type != 12 && type != 14) return JLLM_ERR_UNSUPPORTED;
-    if (!out || !q8 || M <= 0 || N <= 0 || K <= 0 || K % 256 != 0 || Npad < N || Npad % MMQ_TILE_N != 0)
-        return JLLM_ERR_INVALID;
-    const void* Wd = resolve_weight(W);
-    if (!Wd) return JLLM_ERR_POINTER;
-    return launch_status(mmq_launch(out, (const uint8_t*)Wd, type, q8, M, N, K, Npad, 2, (hipStream_t)stream), "GEMM");
+    int st = check_gemm("GEMM", out, type, x, M, N, K); if (st) return st;
+    if (M == 0 || N == 0) return JLLM_OK;
+    return run_mmq("GEMM", out, W, type, x, M, N, K, 2, stream);
 }
 
 }  // extern "C"

@@ -1,4 +1,4 @@
-// mmq.h -- internal interface of the gfx950 int8 MFMA prefill GEMM (MMQ).
+// mmq.h -- internal interface of the gfx950 prefill GEMM (MMQ).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -6,15 +6,24 @@
 
 namespace jllm_hip {
 
-constexpr int MMQ_TILE_N = 64;    // tokens per workgroup tile (and Npad granularity)
+constexpr int MMQ_TILE_N = 64;    // tokens per workgroup tile (Npad granularity of the kernel layout)
+constexpr int MMQ_REF_NPAD = 64;  // Npad granularity of the reference-layout quantiser entry point
 
-// activation quantiser: x [N x K] fp16 -> [K/128][Npad] blocks of 144 B
-// (ds4 = 1: half2 (d, sum x) per 32; ds4 = 0: float d per 32)
+// activation quantiser in the reference block layout: x [N x K] fp16 ->
+// [K/128][Npad] blocks of 144 B (ds4 = 1: half2 (d, sum x) per 32; ds4 = 0:
+// float d per 32)
 hipError_t quantize_mmq_launch(const uint16_t* x, void* q8, int N, int K, int Npad, bool ds4, hipStream_t st);
+
+// the same values in the kernels' layout: codes fp16 [K/256][Npad][256],
+// scale words [K/32][Npad] (DS4: half d | half sum << 16; D4: float d)
+hipError_t quantize_mmq_f16_launch(const uint16_t* x, uint16_t* codes, uint32_t* scl, int N, int K, int Npad,
+                                   bool ds4, hipStream_t st);
+inline size_t mmq_codes_bytes(int K, int Npad) { return (size_t)K * Npad * 2; }
+inline size_t mmq_scales_bytes(int K, int Npad) { return (size_t)(K / 32) * Npad * 4; }
 
 // out_kind: 0 = fp16 y[N x M], 1 = fp32 y[N x M], 2 = raw int32 sub-block
 // dots [N][M][K/G] (G = 32 for Q4_K, 16 for Q6_K)
-hipError_t mmq_launch(void* y, const uint8_t* W, int type, const void* q8, int M, int N, int K, int Npad,
-                      int out_kind, hipStream_t st);
+hipError_t mmq_launch(void* y, const uint8_t* W, int type, const uint16_t* codes, const uint32_t* scl, int M, int N,
+                      int K, int Npad, int out_kind, hipStream_t st);
 
 }  // namespace jllm_hip

@@ -1,23 +1,36 @@
-// mmq.hip -- int8 MFMA prefill GEMM for Q4_K / Q6_K weights on gfx950.
+// mmq.hip -- prefill GEMM (MMQ) for Q4_K / Q6_K weights on gfx950.
 //
 // y[t][r] = sum_k x[t][k] * W[r][k] for N tokens, M weight rows, with the
-// activation quantised to q8_1 in 32-value blocks and every 32-weight (Q4_K)
-// or 16-weight (Q6_K) group dotted EXACTLY in int32 by the matrix cores,
-// then scaled in fp32 -- the arithmetic of the reference's default prefill
-// path (mmq_q4k_llama.cu:92-453, mmq_q6k_llama.cu:71-483, SM 8.x branch):
+// activation quantised to q8_1 in 32-value blocks (the reference's DS4 / D4
+// quantisers, bit-exact) and every 32-weight (Q4_K) / 16-weight (Q6_K)
+// group dotted EXACTLY, then scaled in fp32 -- the arithmetic of the
+// reference's default prefill path (mmq_q4k_llama.cu:92-453,
+// mmq_q6k_llama.cu:71-483):
 //   Q4_K: sum += half(d*sc_j) * d8_j * C_j ;  sum += half(-dmin*m_j) * sumx_j
 //   Q6_K: per 128-half, tmp += float(C_g0*sc_g0 + C_g1*sc_g1) * d8 (per 32),
 //         sum += tmp * d.
 //
-// Matrix-core mapping: one v_mfma_i32_32x32x32_i8 per (32 rows, 32 tokens,
-// Q4_K sub-block) -- K = 32 is exactly one sub-block, so each accumulator
-// holds one reference int32 dot; Q6_K uses v_mfma_i32_32x32x16_i8 per 16-group.
-// A workgroup computes a 128-row x 64-token tile: per super-block it stages
-// the 128 weight blocks and the 64 tokens' q8 codes in LDS (row strides
-// padded so the per-lane 16-byte reads are bank-conflict free), each wave
-// owns 32 rows x 64 tokens.  Tiles are ordered row-major and handed out so
-// that each XCD (blockIdx % 8) works on a contiguous range of row tiles,
-// keeping a weight tile in one L2.
+// Matrix-core mapping.  The reference scales every 32-wide int32 dot in
+// fp32, and on gfx950 one fp32 VALU op costs as much as ~64 int8 MACs on the
+// matrix cores, so an int8-MFMA kernel is bound by that epilogue.  Here the
+// dots run on v_mfma_f32_32x32x16_f16 instead: weight codes (0..15, or
+// (q-32)*sc with |.| <= 1024) and activation codes (-127..127) are exact in
+// fp16, their products are exact in fp32 and every partial sum stays below
+// 2^24, so the fp32 accumulator of a 32-wide dot IS the int32 dot (or, for
+// Q6_K, exactly C_g0*sc_g0 + C_g1*sc_g1).  What is left for the VALU is one
+// fma per dot: the Q4_K scale products half(d*sc_j)*d8_j (exact: two fp16
+// values) come from a second MFMA as an outer product, the min term
+// sum_j half(-dmin*m_j)*sumx_j is a K = 8 MFMA per super-block, and Q6_K's
+// per-token d8 is a lane constant.  The activation quantiser writes its
+// codes directly as fp16 (same values as the reference's int8 codes), so
+// only the weights are converted in the kernel (nibble / byte -> fp16 with
+// v_perm_b32 and one packed-fp16 subtract).
+//
+// A workgroup computes a 128-row x 64-token tile (4 waves, each 32 rows x
+// 64 tokens = two 32x32 MFMA tiles), staging half a super-block (128 K) of
+// weight bytes and activation codes in LDS per step, double-buffered: the
+// next step's global loads are in flight while the current one computes.  Tiles are handed out
+// so that each XCD (blockIdx % 8) works on a contiguous range of row tiles.
 #include "kq_common.h"
 #include "mmq.h"
 
@@ -27,13 +40,16 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4m __attribute__((ext_vector_type(4)));
 typedef float f32x4m __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2m __attribute__((ext_vector_type(2)));
+typedef _Float16 h8m __attribute__((ext_vector_type(8)));
+typedef _Float16 h4m __attribute__((ext_vector_type(4)));
+typedef float f32x16m __attribute__((ext_vector_type(16)));
 
 constexpr int MMQ_THREADS = 256;
-constexpr int TM = 128;                 // rows per tile
-constexpr int TN = MMQ_TILE_N;          // tokens per tile
-constexpr int A4_STRIDE = 144;          // LDS bytes per staged Q4_K row block
-constexpr int A6_STRIDE = 272;          // LDS bytes per decoded Q6_K row (256 codes + pad)
-constexpr int B_STRIDE = 272;           // LDS bytes per token (256 codes + pad)
+constexpr int TM = 128;                 // rows per workgroup tile (4 waves x 32)
+constexpr int TN = MMQ_TILE_N;          // tokens per workgroup tile (64)
+constexpr int A4_STRIDE = 72;           // LDS bytes per row: 64 Q4_K code bytes of a half super-block + pad
+constexpr int B_STRIDE = 272;           // LDS bytes per token: 128 fp16 activation codes + pad
 
 // ---------------------------------------------------------------------------
 // activation quantiser (quantize_mmq_q8_1_ds4 / _d4, mmq_q4k_llama.cu:383-404,
@@ -74,6 +90,42 @@ hipError_t quantize_mmq_launch(const uint16_t* x, void* q8, int N, int K, int Np
     return hipGetLastError();
 }
 
+// The same quantisation (same codes, d and sum, same butterfly order) in the
+// layout the MMQ kernels read: codes as fp16 values, [K/256][Npad][256], and
+// one 32-bit scale word per 32 values, [K/32][Npad] (DS4: half d | half sum
+// << 16; D4: float d).  One thread per value, 32 lanes per block.
+__global__ __launch_bounds__(256) void quantize_mmq_f16_kernel(const uint16_t* __restrict__ x,
+                                                               uint16_t* __restrict__ codes,
+                                                               uint32_t* __restrict__ scl, int N, int K, int Npad,
+                                                               int ds4) {
+    const int blk = blockIdx.x * 8 + (threadIdx.x >> 5);       // (kb32, col)
+    const int nblk = (K / 32) * Npad;
+    if (blk >= nblk) return;                                   // whole 32-lane groups exit together
+    const int kb32 = blk / Npad, col = blk % Npad, lane = threadIdx.x & 31;
+    const float v = col < N ? f16_bits_to_f32(x[(int64_t)col * K + kb32 * 32 + lane]) : 0.0f;
+    float amax = fabsf(v), sum = v;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+        sum += __shfl_xor(sum, o, 64);
+    }
+    const float d = amax / 127.0f;
+    const float dinv = d > 0.0f ? 1.0f / d : 0.0f;
+    const int q = (int)__builtin_rintf(v * dinv);
+    codes[((int64_t)(kb32 >> 3) * Npad + col) * 256 + (kb32 & 7) * 32 + lane] = f32_to_f16_bits((float)q);
+    if (lane == 0)
+        scl[(int64_t)kb32 * Npad + col] =
+            ds4 ? ((uint32_t)f32_to_f16_bits(d) | ((uint32_t)f32_to_f16_bits(sum) << 16)) : __builtin_bit_cast(uint32_t, d);
+}
+
+hipError_t quantize_mmq_f16_launch(const uint16_t* x, uint16_t* codes, uint32_t* scl, int N, int K, int Npad,
+                                   bool ds4, hipStream_t st) {
+    const int nblk = (K / 32) * Npad;
+    hipLaunchKernelGGL(quantize_mmq_f16_kernel, dim3((nblk + 7) / 8), dim3(256), 0, st, x, codes, scl, N, K, Npad,
+                       ds4 ? 1 : 0);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // tile scheduling
 
@@ -83,305 +135,456 @@ __device__ __forceinline__ int xcd_tile(int bid, int tiles) {
     return (bid % 8) * (full / 8) + bid / 8;
 }
 
+
 // ---------------------------------------------------------------------------
-// B staging (shared by both weight types): the tile's 64 tokens x 256 codes
-// of one super-block (two 128-value q8 blocks per token) and their per-32
-// scales.  DS4: d8 and sum; D4: d8 only.
-template <bool DS4>
-__device__ __forceinline__ void stage_b(const uint8_t* __restrict__ q8, int Npad, int col0, int b,
-                                        uint8_t* sB, float* sD8, float* sSX) {
-    const int t = threadIdx.x;
-#pragma unroll
-    for (int it = 0; it < (TN * 16) / MMQ_THREADS; it++) {
-        const int c = it * MMQ_THREADS + t;          // chunk: token c/16, 16-byte piece c%16
-        const int tok = c >> 4, piece = c & 15, half = piece >> 3;
-        const uint8_t* src = q8 + ((int64_t)(2 * b + half) * Npad + col0 + tok) * 144 + 16 + (piece & 7) * 16;
-        *(u32x4m*)(sB + tok * B_STRIDE + piece * 16) = *(const u32x4m*)src;
-    }
-    if (t < TN * 2) {                                // 64 tokens x 2 q8 blocks: scales
-        const int tok = t >> 1, half = t & 1;
-        const u32x4m w = *(const u32x4m*)(q8 + ((int64_t)(2 * b + half) * Npad + col0 + tok) * 144);
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-            const int j = half * 4 + s;
-            if (DS4) {
-                sD8[j * TN + tok] = f16_bits_to_f32(ww[s] & 0xFFFFu);
-                sSX[j * TN + tok] = f16_bits_to_f32(ww[s] >> 16);
-            } else {
-                sD8[j * TN + tok] = __builtin_bit_cast(float, ww[s]);
-            }
-        }
-    }
+// weight code -> fp16 conversions.  v_perm_b32 interleaves each code byte
+// with 0x64, giving the fp16 value 1024 + byte; one packed fp16 subtract
+// removes the bias exactly.
+
+__device__ __forceinline__ h8m bytes_to_h8(u32x2m w, float bias) {
+    const uint32_t hi = 0x64646464u;
+    u32x4m p;
+    p.x = __builtin_amdgcn_perm(hi, w.x, 0x04010400u);
+    p.y = __builtin_amdgcn_perm(hi, w.x, 0x04030402u);
+    p.z = __builtin_amdgcn_perm(hi, w.y, 0x04010400u);
+    p.w = __builtin_amdgcn_perm(hi, w.y, 0x04030402u);
+    const _Float16 b = (_Float16)bias;
+    return __builtin_bit_cast(h8m, p) - h8m{b, b, b, b, b, b, b, b};
 }
+
+// 8 Q4_K nibbles (low or high halves of 8 code bytes) -> 8 fp16 values 0..15
+__device__ __forceinline__ h8m nib_lo_h8(u32x2m w) { return bytes_to_h8(w & 0x0F0F0F0Fu, 1024.0f); }
+__device__ __forceinline__ h8m nib_hi_h8(u32x2m w) { return bytes_to_h8((w >> 4u) & 0x0F0F0F0Fu, 1024.0f); }
+// 8 signed bytes -> 8 fp16 values (-128..127): bias the bytes by 128 first
+__device__ __forceinline__ h8m i8_to_h8(u32x2m w) { return bytes_to_h8(w ^ 0x80808080u, 1152.0f); }
+
+__device__ __forceinline__ f32x16m mfma16(h8m a, h8m b, f32x16m c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Pipeline shared by both kernels: the K loop runs over half super-blocks
+// ("stages" of 128 weights).  Stage k+1's global loads are issued into
+// registers before stage k is computed from LDS buffer k&1, then written to
+// LDS buffer (k+1)&1; one barrier per stage.  Per-super-block scales live in
+// a second two-slot ring indexed by the super-block's parity.
 
 // ---------------------------------------------------------------------------
 // Q4_K
 
-template <int OUT>
+template <int OUT>   // 0: fp16 y [N][M], 1: fp32 y [N][M], 2: int32 dots [N][M][K/32]
 __global__ __launch_bounds__(MMQ_THREADS, 2)
-void mmq_q4k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const uint8_t* __restrict__ q8,
-                    int M, int N, int K, int Npad) {
-    __shared__ __attribute__((aligned(16))) uint8_t sA[TM * A4_STRIDE];
-    __shared__ __attribute__((aligned(16))) float sDA[8 * TM];     // half(d*sc) per [j][row]
-    __shared__ __attribute__((aligned(16))) float sMA[8 * TM];     // half(-dmin*m) per [j][row]
-    __shared__ __attribute__((aligned(16))) uint8_t sB[TN * B_STRIDE];
-    __shared__ __attribute__((aligned(16))) float sD8[8 * TN];
-    __shared__ __attribute__((aligned(16))) float sSX[8 * TN];
+void mmq_q4k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const uint16_t* __restrict__ codes,
+                    const uint32_t* __restrict__ scl, int M, int N, int K, int Npad) {
+    __shared__ __attribute__((aligned(16))) uint8_t sA[2][TM * A4_STRIDE];
+    __shared__ __attribute__((aligned(16))) uint8_t sB[2][TN * B_STRIDE];
+    __shared__ __attribute__((aligned(16))) _Float16 sDA[2][8 * TM];     // half(d*sc) per [j][row]
+    __shared__ __attribute__((aligned(16))) _Float16 sMA[2][8 * TM];     // half(-dmin*m) per [j][row]
+    __shared__ __attribute__((aligned(16))) uint32_t sS8[2][8 * TN];     // half d8 | half sum x << 16, per [j][token]
 
-    const int nb = K / QK_K;
+    const int nb = K / QK_K, nst = 2 * nb;
     const int n_rt = (M + TM - 1) / TM, n_tt = Npad / TN;
     const int tile = xcd_tile(blockIdx.x, n_rt * n_tt);
     const int row0 = (tile / n_tt) * TM, col0 = (tile % n_tt) * TN;
     const int t = threadIdx.x, w = t >> 6, l = t & 63, li = l & 31, g = l >> 5;
+    const int arow = 32 * w + li;                    // A-operand row of this lane (wave w owns rows 32w..32w+31)
+    const uint32_t gmask = g ? 0u : 0xFFFFu;         // keeps the low fp16 of a word in lanes g = 0 only
 
-    float acc[2][16];
+    // buffer descriptors: per-thread byte offsets are fixed, the stage moves
+    // the scalar offset (no 64-bit address arithmetic in the loop)
+    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0,
+                                                                         (int)((int64_t)M * nb * Q4K_BYTES), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rC = __builtin_amdgcn_make_buffer_rsrc((void*)codes, (short)0,
+                                                                         (int)((int64_t)K * Npad * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc((void*)scl, (short)0,
+                                                                         (int)((int64_t)(K / 32) * Npad * 4), 0x00020000);
+    int voA[2], voB[4], voS[2];
 #pragma unroll
-    for (int nt = 0; nt < 2; nt++)
+    for (int i = 0; i < 2; i++) {                    // 128 rows x 64 code bytes; rows past M re-read the last row
+        const int idx = i * MMQ_THREADS + t, row = idx >> 2, piece = idx & 3;
+        voA[i] = min(row0 + row, M - 1) * nb * Q4K_BYTES + 16 + 16 * piece;
+    }
 #pragma unroll
-        for (int v = 0; v < 16; v++) acc[nt][v] = 0.0f;
+    for (int i = 0; i < 4; i++) {                    // 64 tokens x 128 fp16 codes
+        const int idx = i * MMQ_THREADS + t, tok = idx >> 4, piece = idx & 15;
+        voB[i] = (col0 + tok) * 512 + 16 * piece;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int e = i * MMQ_THREADS + t, j = e / TN, tok = e % TN;
+        voS[i] = (j * Npad + col0 + tok) * 4;
+    }
+    const int voH = min(row0 + (t & (TM - 1)), M - 1) * nb * Q4K_BYTES;
 
-    for (int b = 0; b < nb; b++) {
-        // stage the 128 weight blocks (rows past M re-read the last row)
-        for (int c = t; c < TM * 9; c += MMQ_THREADS) {
-            const int row = c / 9, piece = c % 9;
-            const int R = min(row0 + row, M - 1);
-            *(u32x4m*)(sA + row * A4_STRIDE + piece * 16) =
-                *(const u32x4m*)(W + ((int64_t)R * nb + b) * Q4K_BYTES + piece * 16);
+    struct Stage { u32x4m a[2], b[4]; };
+    Stage R0, R1;                                    // staging registers of even / odd stages
+    u32x4m rh = u32x4m{};
+    uint32_t rs[2] = {0u, 0u};
+    auto fetch = [&](Stage& R, int k) {
+        const int b = k >> 1, s = k & 1;
+#pragma unroll
+        for (int i = 0; i < 2; i++) R.a[i] = __builtin_amdgcn_raw_buffer_load_b128(rW, voA[i], b * Q4K_BYTES + 64 * s, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) R.b[i] = __builtin_amdgcn_raw_buffer_load_b128(rC, voB[i], b * Npad * 512 + 256 * s, 0);
+        if (s == 0) {
+            rh = __builtin_amdgcn_raw_buffer_load_b128(rW, voH, b * Q4K_BYTES, 0);
+#pragma unroll
+            for (int i = 0; i < 2; i++) rs[i] = __builtin_amdgcn_raw_buffer_load_b32(rS, voS[i], b * 8 * Npad * 4, 0);
         }
-        if (t < TM) {    // per-row sub-block scales, rounded to half as the reference does
-            const int R = min(row0 + t, M - 1);
-            const u32x4m h = *(const u32x4m*)(W + ((int64_t)R * nb + b) * Q4K_BYTES);
-            const float d = f16_bits_to_f32(h.x & 0xFFFFu), dmin = f16_bits_to_f32(h.x >> 16);
+    };
+    auto commit = [&](const Stage& R, int k) {
+        const int s = k & 1, slot = (k >> 1) & 1;
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                uint32_t sc, m;
-                q4k_scale_min(h.y, h.z, h.w, j, sc, m);
-                sDA[j * TM + t] = round_to_f16(d * (float)sc);
-                sMA[j * TM + t] = round_to_f16(-dmin * (float)m);
+        for (int i = 0; i < 2; i++) {
+            const int idx = i * MMQ_THREADS + t, row = idx >> 2, piece = idx & 3;
+            uint8_t* d = &sA[s][row * A4_STRIDE + 16 * piece];
+            *(u32x2m*)d = u32x2m{R.a[i].x, R.a[i].y};
+            *(u32x2m*)(d + 8) = u32x2m{R.a[i].z, R.a[i].w};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int idx = i * MMQ_THREADS + t, tok = idx >> 4, piece = idx & 15;
+            *(u32x4m*)&sB[s][tok * B_STRIDE + 16 * piece] = R.b[i];
+        }
+        if (s == 0) {
+            if (t < TM) {   // per-row sub-block scales, rounded to half as the reference does
+                const float d = f16_bits_to_f32(rh.x & 0xFFFFu), dmin = f16_bits_to_f32(rh.x >> 16);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    uint32_t sc, m;
+                    q4k_scale_min(rh.y, rh.z, rh.w, j, sc, m);
+                    sDA[slot][j * TM + t] = (_Float16)(d * (float)sc);
+                    sMA[slot][j * TM + t] = (_Float16)(-dmin * (float)m);
+                }
             }
+#pragma unroll
+            for (int i = 0; i < 2; i++) sS8[slot][i * MMQ_THREADS + t] = rs[i];
         }
-        stage_b<true>(q8, Npad, col0, b, sB, sD8, sSX);
-        __syncthreads();
+    };
 
+    f32x16m acc[2];
+    acc[0] = f32x16m{};
+    acc[1] = f32x16m{};
+
+    auto compute = [&](int k) {
+        const int b = k >> 1, s = k & 1, slot = b & 1;
+        const uint8_t* A = sA[s];
+        const uint8_t* B = sB[s];
+        // four sub-blocks per stage; for each, both token tiles' MFMAs are
+        // issued together (two independent accumulation chains), and the B
+        // operands of the next sub-block are read from LDS before this one's
+        // fmas run
+        h8m Bn[2][2];
+        auto load_b = [&](int jl) {
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++) {
+                const int btok = 32 * tt + li;
+                Bn[tt][0] = *(const h8m*)(B + btok * B_STRIDE + 64 * jl + 16 * g);
+                Bn[tt][1] = *(const h8m*)(B + btok * B_STRIDE + 64 * jl + 32 + 16 * g);
+            }
+        };
+        load_b(0);
 #pragma unroll 1
-        for (int jj = 0; jj < 4; jj++) {
-            // A: 16 packed bytes = the lane's 16 K positions of sub-blocks 2jj (low
-            // nibbles) and 2jj+1 (high nibbles) for row 32w + li
-            const u32x4m a = *(const u32x4m*)(sA + (32 * w + li) * A4_STRIDE + 16 + 32 * jj + 16 * g);
-            const u32x4m M4 = {0x0F0F0F0Fu, 0x0F0F0F0Fu, 0x0F0F0F0Fu, 0x0F0F0F0Fu};
-            const i32x4 alo = __builtin_bit_cast(i32x4, a & M4);
-            const i32x4 ahi = __builtin_bit_cast(i32x4, (a >> 4) & M4);
+        for (int pl = 0; pl < 2; pl++) {
+            // lane (row arow, g): code bytes 32pl + 8g .. +8 and 32pl + 16 + 8g .. +8 -- the
+            // K positions this lane feeds to the two K=16 MFMAs of sub-blocks 2p (low
+            // nibbles) and 2p+1 (high nibbles), p = 2s + pl
+            const u32x2m a0 = *(const u32x2m*)(A + arow * A4_STRIDE + 32 * pl + 8 * g);
+            const u32x2m a1 = *(const u32x2m*)(A + arow * A4_STRIDE + 32 * pl + 16 + 8 * g);
 #pragma unroll
-            for (int p = 0; p < 2; p++) {
-                const int j = 2 * jj + p;
-                i32x16 C[2];
+            for (int jj = 0; jj < 2; jj++) {
+                const int jl = 2 * pl + jj;              // sub-block within the stage
+                const int j = 4 * s + jl;                // sub-block within the super-block
+                const h8m A0 = jj ? nib_hi_h8(a0) : nib_lo_h8(a0);
+                const h8m A1 = jj ? nib_hi_h8(a1) : nib_lo_h8(a1);
+                h8m Bc[2][2];
 #pragma unroll
-                for (int nt = 0; nt < 2; nt++) {
-                    const i32x4 bv = *(const i32x4*)(sB + (32 * nt + li) * B_STRIDE + 32 * j + 16 * g);
-                    const i32x16 zero = {};
-                    C[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(p ? ahi : alo, bv, zero, 0, 0, 0);
-                }
-                // rows of this lane's accumulators: 32w + 8m + 4g + (0..3)
-                f32x4m da[4], ma[4];
+                for (int tt = 0; tt < 2; tt++) { Bc[tt][0] = Bn[tt][0]; Bc[tt][1] = Bn[tt][1]; }
+                f32x16m C[2];
 #pragma unroll
-                for (int m4 = 0; m4 < 4; m4++) {
-                    da[m4] = *(const f32x4m*)(sDA + j * TM + 32 * w + 8 * m4 + 4 * g);
-                    ma[m4] = *(const f32x4m*)(sMA + j * TM + 32 * w + 8 * m4 + 4 * g);
-                }
+                for (int tt = 0; tt < 2; tt++) C[tt] = mfma16(A0, Bc[tt][0], f32x16m{});
 #pragma unroll
-                for (int nt = 0; nt < 2; nt++) {
-                    const float db = sD8[j * TN + 32 * nt + li], sx = sSX[j * TN + 32 * nt + li];
+                for (int tt = 0; tt < 2; tt++) C[tt] = mfma16(A1, Bc[tt][1], C[tt]);   // exact int32 dots of sub-block j
+                if (jl < 3) load_b(jl + 1);
+                if (OUT == 2) {
 #pragma unroll
-                    for (int v = 0; v < 16; v++) {
-                        if (OUT == 2) continue;
-                        const float dav = da[v >> 2][v & 3], mav = ma[v >> 2][v & 3];
-                        acc[nt][v] += dav * db * (float)C[nt][v];
-                        acc[nt][v] += mav * sx;
-                    }
-                    if (OUT == 2) {   // raw dots [N][M][K/32]
+                    for (int tt = 0; tt < 2; tt++)
 #pragma unroll
                         for (int v = 0; v < 16; v++) {
                             const int r = row0 + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3);
-                            const int tok = col0 + 32 * nt + li;
+                            const int tok = col0 + 32 * tt + li;
                             if (r < M && tok < N)
-                                ((int*)y)[((int64_t)tok * M + r) * (K / 32) + b * 8 + j] = C[nt][v];
+                                ((int*)y)[((int64_t)tok * M + r) * (K / 32) + b * 8 + j] = (int)C[tt][v];
                         }
+                } else {
+                    // scale outer products: K slot 0 only (lanes g = 1 hold zeros); every
+                    // lane loads, the g = 1 lanes then drop the value (no branch)
+                    const uint32_t da_bits = (uint32_t)__builtin_bit_cast(uint16_t, sDA[slot][j * TM + arow]) & gmask;
+                    const h8m As = __builtin_bit_cast(h8m, u32x4m{da_bits, 0u, 0u, 0u});
+                    f32x16m S[2];
+#pragma unroll
+                    for (int tt = 0; tt < 2; tt++) {
+                        const uint32_t d8_bits = sS8[slot][j * TN + 32 * tt + li] & gmask;
+                        S[tt] = mfma16(As, __builtin_bit_cast(h8m, u32x4m{d8_bits, 0u, 0u, 0u}), f32x16m{});
                     }
+#pragma unroll
+                    for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+                        for (int v = 0; v < 16; v++) acc[tt][v] = __builtin_fmaf(C[tt][v], S[tt][v], acc[tt][v]);
                 }
             }
         }
+        if (OUT != 2 && s == 1) {
+            // min term of the whole super-block: K = 8 sub-blocks on one MFMA per tile
+            h4m Am;
+#pragma unroll
+            for (int e = 0; e < 4; e++) Am[e] = sMA[slot][(4 * g + e) * TM + arow];
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++) {
+                const int btok = 32 * tt + li;
+                h4m Bm;
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    Bm[e] = __builtin_bit_cast(_Float16, (uint16_t)(sS8[slot][(4 * g + e) * TN + btok] >> 16));
+                acc[tt] = __builtin_amdgcn_mfma_f32_32x32x8f16(Am, Bm, acc[tt], 0, 0, 0);
+            }
+        }
+    };
+
+    // stages come in pairs (s = 0, 1); each stage's loads are issued two stages
+    // before it is written to LDS
+    fetch(R0, 0);
+    fetch(R1, 1);
+    commit(R0, 0);
+    __syncthreads();
+#pragma unroll 1
+    for (int k = 0; k < nst; k += 2) {
+        if (k + 2 < nst) fetch(R0, k + 2);
+        compute(k);
+        commit(R1, k + 1);
+        __syncthreads();
+        if (k + 3 < nst) fetch(R1, k + 3);
+        compute(k + 1);
+        if (k + 2 < nst) commit(R0, k + 2);
         __syncthreads();
     }
     if (OUT == 2) return;
 #pragma unroll
-    for (int nt = 0; nt < 2; nt++) {
-        const int tok = col0 + 32 * nt + li;
+    for (int tt = 0; tt < 2; tt++) {
+        const int tok = col0 + 32 * tt + li;
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             const int r = row0 + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3);
             if (r < M && tok < N) {
-                if (OUT == 1) ((float*)y)[(int64_t)tok * M + r] = acc[nt][v];
-                else          ((uint16_t*)y)[(int64_t)tok * M + r] = f32_to_f16_bits(acc[nt][v]);
+                if (OUT == 1) ((float*)y)[(int64_t)tok * M + r] = acc[tt][v];
+                else          ((uint16_t*)y)[(int64_t)tok * M + r] = f32_to_f16_bits(acc[tt][v]);
             }
         }
     }
 }
 
 // ---------------------------------------------------------------------------
-// Q6_K
+// Q6_K: the raw ql/qh bytes of a half super-block are staged per row
+// (64 + 32 bytes, read from the 2-byte-aligned blocks with dword loads and
+// funnel shifts) and decoded by the lane that feeds them to the MFMA.
 
-typedef float f32x4q6 __attribute__((ext_vector_type(4)));
+constexpr int R6_STRIDE = 104;          // LDS bytes per row: ql (64) + qh (32) of a half super-block + pad
 
-template <int OUT>
+template <int OUT>   // 0: fp16 y, 1: fp32 y, 2: int32 group dots [N][M][K/16]
 __global__ __launch_bounds__(MMQ_THREADS, 2)
-void mmq_q6k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const uint8_t* __restrict__ q8,
-                    int M, int N, int K, int Npad) {
-    __shared__ __attribute__((aligned(16))) uint8_t sA[TM * A6_STRIDE];   // decoded codes q-32 (int8)
-    __shared__ __attribute__((aligned(16))) int sSC[16 * TM];             // int8 scales per [group][row]
-    __shared__ __attribute__((aligned(16))) float sDA[TM];                // d per row
-    __shared__ __attribute__((aligned(16))) uint8_t sB[TN * B_STRIDE];
-    __shared__ __attribute__((aligned(16))) float sD8[8 * TN];
+void mmq_q6k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const uint16_t* __restrict__ codes,
+                    const uint32_t* __restrict__ scl, int M, int N, int K, int Npad) {
+    __shared__ __attribute__((aligned(16))) uint8_t sR[2][TM * R6_STRIDE];
+    __shared__ __attribute__((aligned(16))) uint8_t sB[2][TN * B_STRIDE];
+    __shared__ __attribute__((aligned(16))) _Float16 sSC[2][16 * TM];    // int8 scales as fp16, per [group][row]
+    __shared__ __attribute__((aligned(16))) float sDA[2][TM];            // d per row
+    __shared__ __attribute__((aligned(16))) float sD8[2][8 * TN];        // d8 per [j][token]
 
-    const int nb = K / QK_K;
+    const int nb = K / QK_K, nst = 2 * nb;
     const int n_rt = (M + TM - 1) / TM, n_tt = Npad / TN;
     const int tile = xcd_tile(blockIdx.x, n_rt * n_tt);
     const int row0 = (tile / n_tt) * TM, col0 = (tile % n_tt) * TN;
     const int t = threadIdx.x, w = t >> 6, l = t & 63, li = l & 31, g = l >> 5;
+    const int arow = 32 * w + li;
 
-    float acc[2][16];
+    // staging registers: 6 pieces of 8 raw bytes (3 aligned dwords each), the
+    // activation codes, and at the first half of a super-block the row's scale
+    // bytes and d (5 dwords) and two d8 words
+    uint32_t rr[6][3], rsc[5] = {0u, 0u, 0u, 0u, 0u}, rd = 0u;
+    u32x4m rb[4];
+    uint32_t rs[2];
+    auto piece_src = [&](int k, int i, int& row) -> const uint8_t* {
+        const int b = k >> 1, s = k & 1;
+        const int idx = i * MMQ_THREADS + t;
+        row = idx / 12;
+        const int pc = idx % 12;
+        const uint8_t* blk = W + ((int64_t)min(row0 + row, M - 1) * nb + b) * Q6K_BYTES;
+        return pc < 8 ? blk + 64 * s + 8 * pc : blk + 128 + 32 * s + 8 * (pc - 8);
+    };
+    auto fetch = [&](int k) {
+        const int b = k >> 1, s = k & 1;
 #pragma unroll
-    for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-        for (int v = 0; v < 16; v++) acc[nt][v] = 0.0f;
-
-    for (int b = 0; b < nb; b++) {
-        // decode: unit = (row, 16-element group n16) -> 16 codes; elements
-        // e = 16*n16 + i share the half h, quarter qq and 16 consecutive l.
-        for (int u = t; u < TM * 16; u += MMQ_THREADS) {
-            const int row = u >> 4, n16 = u & 15;
-            const int R = min(row0 + row, M - 1);
-            const uint8_t* blk = W + ((int64_t)R * nb + b) * Q6K_BYTES;
-            const int e0 = 16 * n16, h = e0 >> 7, ph = e0 & 127, qq = ph >> 5, l0 = ph & 31;
-            const uint8_t* pl = blk + 64 * h + l0 + 32 * (qq & 1);
-            const uint8_t* ph2 = blk + 128 + 32 * h + l0;
-            const uint32_t sh = (uint32_t)((uintptr_t)blk & 2u) * 8u;
-            const uint8_t* bl = pl - ((uintptr_t)pl & 3u);
-            const uint8_t* bh = ph2 - ((uintptr_t)ph2 & 3u);
-            uint32_t ql[4], qh[4];
-            {
-                const uint32_t* s0 = (const uint32_t*)bl;
-                const uint32_t* s1 = (const uint32_t*)bh;
-                uint32_t a[5], c[5];
-#pragma unroll
-                for (int k = 0; k < 5; k++) { a[k] = s0[k]; c[k] = s1[k]; }
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    ql[k] = __builtin_amdgcn_alignbit(a[k + 1], a[k], sh);
-                    qh[k] = __builtin_amdgcn_alignbit(c[k + 1], c[k], sh);
-                }
-            }
-            u32x4m codes;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t lo = ((qq >= 2 ? (ql[k] >> 4) : ql[k]) & 0x0F0F0F0Fu);
-                const uint32_t hb = (qh[k] >> (2 * qq)) & 0x03030303u;
-                const uint32_t v = lo | (hb << 4);
-                codes[k] = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;   // bytewise v - 32
-            }
-            *(u32x4m*)(sA + row * A6_STRIDE + 16 * n16) = codes;
+        for (int i = 0; i < 6; i++) {
+            int row;
+            const uint8_t* src = piece_src(k, i, row);
+            const uint32_t* wp = (const uint32_t*)((uintptr_t)src & ~(uintptr_t)3);
+            rr[i][0] = wp[0]; rr[i][1] = wp[1]; rr[i][2] = wp[2];
         }
-        if (t < TM) {
-            const int R = min(row0 + t, M - 1);
-            const uint8_t* blk = W + ((int64_t)R * nb + b) * Q6K_BYTES;
 #pragma unroll
-            for (int gi = 0; gi < 16; gi++) sSC[gi * TM + t] = (int)(int8_t)blk[192 + gi];
-            sDA[t] = f16_bits_to_f32(*(const uint16_t*)(blk + 208));
+        for (int i = 0; i < 4; i++) {
+            const int idx = i * MMQ_THREADS + t, tok = idx >> 4, piece = idx & 15;
+            rb[i] = *(const u32x4m*)(codes + ((int64_t)b * Npad + col0 + tok) * 256 + 128 * s + 8 * piece);
         }
-        stage_b<false>(q8, Npad, col0, b, sB, sD8, nullptr);
-        __syncthreads();
+        if (s == 0) {
+            if (t < TM) {
+                // scales: bytes 192..207 from the aligned dwords covering them (the fifth
+                // only when the block is not dword aligned, so nothing past byte 209 is
+                // read); d: bytes 208..209
+                const uint8_t* p = W + ((int64_t)min(row0 + t, M - 1) * nb + b) * Q6K_BYTES + 192;
+                const uint32_t* wp = (const uint32_t*)((uintptr_t)p & ~(uintptr_t)3);
+#pragma unroll
+                for (int i = 0; i < 4; i++) rsc[i] = wp[i];
+                rsc[4] = ((uintptr_t)p & 3u) ? wp[4] : 0u;
+                rd = *(const uint16_t*)(p + 16);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int e = i * MMQ_THREADS + t, j = e / TN, tok = e % TN;
+                rs[i] = scl[(int64_t)(b * 8 + j) * Npad + col0 + tok];
+            }
+        }
+    };
+    auto commit = [&](int k) {
+        const int b = k >> 1, s = k & 1, slot = b & 1;
+#pragma unroll
+        for (int i = 0; i < 6; i++) {
+            int row;
+            const uint8_t* src = piece_src(k, i, row);
+            const uint32_t sh = (uint32_t)((uintptr_t)src & 3u) * 8u;
+            const int pc = (i * MMQ_THREADS + t) % 12;
+            *(u32x2m*)&sR[s][row * R6_STRIDE + 8 * pc] =
+                u32x2m{__builtin_amdgcn_alignbit(rr[i][1], rr[i][0], sh), __builtin_amdgcn_alignbit(rr[i][2], rr[i][1], sh)};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int idx = i * MMQ_THREADS + t, tok = idx >> 4, piece = idx & 15;
+            *(u32x4m*)&sB[s][tok * B_STRIDE + 16 * piece] = rb[i];
+        }
+        if (s == 0) {
+            if (t < TM) {
+                const uint8_t* p = W + ((int64_t)min(row0 + t, M - 1) * nb + b) * Q6K_BYTES + 192;
+                const uint32_t sh = (uint32_t)((uintptr_t)p & 3u) * 8u;
+                uint32_t v[4];                         // scale bytes 192..207 of the block, realigned
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = __builtin_amdgcn_alignbit(rsc[i + 1], rsc[i], sh);
+#pragma unroll
+                for (int gi = 0; gi < 16; gi++)
+                    sSC[slot][gi * TM + t] = (_Float16)(float)(int8_t)(v[gi >> 2] >> (8 * (gi & 3)));
+                sDA[slot][t] = f16_bits_to_f32(rd);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++) sD8[slot][i * MMQ_THREADS + t] = __builtin_bit_cast(float, rs[i]);
+        }
+    };
 
-        f32x4q6 dA[4];
-#pragma unroll
-        for (int m4 = 0; m4 < 4; m4++) dA[m4] = *(const f32x4q6*)(sDA + 32 * w + 8 * m4 + 4 * g);
+    f32x16m acc[2];
+    acc[0] = f32x16m{};
+    acc[1] = f32x16m{};
+
+    fetch(0);
+    commit(0);
+    __syncthreads();
 #pragma unroll 1
-        for (int hh = 0; hh < 2; hh++) {
-            float tmp[2][16];
-#pragma unroll
-            for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-                for (int v = 0; v < 16; v++) tmp[nt][v] = 0.0f;
+    for (int k = 0; k < nst; k++) {
+        const int b = k >> 1, s = k & 1, slot = b & 1;
+        if (k + 1 < nst) fetch(k + 1);
+        const uint8_t* Rw = &sR[s][arow * R6_STRIDE];
+        const uint8_t* B = sB[s];
+        f32x16m tmp[2];
+        tmp[0] = f32x16m{};
+        tmp[1] = f32x16m{};
 #pragma unroll 1
-            for (int s = 0; s < 4; s++) {
-                const int j = 4 * hh + s;                          // 32-wide block within the super-block
-                const int64_t a0 = *(const int64_t*)(sA + (32 * w + li) * A6_STRIDE + 32 * j + 8 * g);
-                const int64_t a1 = *(const int64_t*)(sA + (32 * w + li) * A6_STRIDE + 32 * j + 16 + 8 * g);
-                i32x4 sc0[4], sc1[4];
+        for (int qq = 0; qq < 4; qq++) {                 // the four 32-wide quarters of this half
+            const int j = 4 * s + qq;                    // 32-wide block within the super-block
+            // lane (row arow, g): elements l = 8g..8g+7 (group 2j) and 16+8g.. (group 2j+1)
+            const u32x2m ql0 = *(const u32x2m*)(Rw + 32 * (qq & 1) + 8 * g);
+            const u32x2m ql1 = *(const u32x2m*)(Rw + 32 * (qq & 1) + 16 + 8 * g);
+            const u32x2m qh0 = *(const u32x2m*)(Rw + 64 + 8 * g);
+            const u32x2m qh1 = *(const u32x2m*)(Rw + 64 + 16 + 8 * g);
+            const uint32_t nsh = qq >= 2 ? 4u : 0u, hsh = 2u * qq;
+            const u32x2m v0 = ((ql0 >> nsh) & 0x0F0F0F0Fu) | (((qh0 >> hsh) & 0x03030303u) << 4u);
+            const u32x2m v1 = ((ql1 >> nsh) & 0x0F0F0F0Fu) | (((qh1 >> hsh) & 0x03030303u) << 4u);
+            h8m A0 = bytes_to_h8(v0, 1056.0f), A1 = bytes_to_h8(v1, 1056.0f);   // q - 32
+            if (OUT != 2) {
+                const _Float16 s0 = sSC[slot][(2 * j) * TM + arow], s1 = sSC[slot][(2 * j + 1) * TM + arow];
+                A0 = A0 * h8m{s0, s0, s0, s0, s0, s0, s0, s0};   // exact: |(q-32)*sc| <= 1024
+                A1 = A1 * h8m{s1, s1, s1, s1, s1, s1, s1, s1};
+            }
 #pragma unroll
-                for (int m4 = 0; m4 < 4; m4++) {
-                    sc0[m4] = *(const i32x4*)(sSC + (2 * j) * TM + 32 * w + 8 * m4 + 4 * g);
-                    sc1[m4] = *(const i32x4*)(sSC + (2 * j + 1) * TM + 32 * w + 8 * m4 + 4 * g);
-                }
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++) {
-                    const int64_t b0 = *(const int64_t*)(sB + (32 * nt + li) * B_STRIDE + 32 * j + 8 * g);
-                    const int64_t b1 = *(const int64_t*)(sB + (32 * nt + li) * B_STRIDE + 32 * j + 16 + 8 * g);
-                    const i32x16 zero = {};
-                    const i32x16 C0 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a0, b0, zero, 0, 0, 0);
-                    const i32x16 C1 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a1, b1, zero, 0, 0, 0);
-                    const float db = sD8[j * TN + 32 * nt + li];
+            for (int tt = 0; tt < 2; tt++) {
+                const int btok = 32 * tt + li;
+                const h8m B0 = *(const h8m*)(B + btok * B_STRIDE + 64 * qq + 16 * g);
+                const h8m B1 = *(const h8m*)(B + btok * B_STRIDE + 64 * qq + 32 + 16 * g);
+                if (OUT == 2) {
+                    const f32x16m C0 = mfma16(A0, B0, f32x16m{});
+                    const f32x16m C1 = mfma16(A1, B1, f32x16m{});
 #pragma unroll
                     for (int v = 0; v < 16; v++) {
-                        if (OUT == 2) {
-                            const int r = row0 + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3);
-                            const int tok = col0 + 32 * nt + li;
-                            if (r < M && tok < N) {
-                                int* o = (int*)y + ((int64_t)tok * M + r) * (K / 16) + b * 16 + 2 * j;
-                                o[0] = C0[v]; o[1] = C1[v];
-                            }
-                        } else {
-                            const int iv = C0[v] * sc0[v >> 2][v & 3] + C1[v] * sc1[v >> 2][v & 3];
-                            tmp[nt][v] += (float)iv * db;
+                        const int r = row0 + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3);
+                        const int tok = col0 + btok;
+                        if (r < M && tok < N) {
+                            int* o = (int*)y + ((int64_t)tok * M + r) * (K / 16) + b * 16 + 2 * j;
+                            o[0] = (int)C0[v];
+                            o[1] = (int)C1[v];
                         }
                     }
+                } else {
+                    f32x16m C = mfma16(A0, B0, f32x16m{});
+                    C = mfma16(A1, B1, C);                    // = C_g0*sc_g0 + C_g1*sc_g1, exact
+                    const float d8 = sD8[slot][j * TN + btok];
+#pragma unroll
+                    for (int v = 0; v < 16; v++) tmp[tt][v] = __builtin_fmaf(C[v], d8, tmp[tt][v]);
                 }
             }
-            if (OUT != 2) {
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-                    for (int v = 0; v < 16; v++) acc[nt][v] += tmp[nt][v] * dA[v >> 2][v & 3];
-            }
         }
+        if (OUT != 2) {
+            f32x4m dA[4];
+#pragma unroll
+            for (int m4 = 0; m4 < 4; m4++) dA[m4] = *(const f32x4m*)(&sDA[slot][32 * w + 8 * m4 + 4 * g]);
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[tt][v] = __builtin_fmaf(tmp[tt][v], dA[v >> 2][v & 3], acc[tt][v]);
+        }
+        if (k + 1 < nst) commit(k + 1);
         __syncthreads();
     }
     if (OUT == 2) return;
 #pragma unroll
-    for (int nt = 0; nt < 2; nt++) {
-        const int tok = col0 + 32 * nt + li;
+    for (int tt = 0; tt < 2; tt++) {
+        const int tok = col0 + 32 * tt + li;
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             const int r = row0 + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3);
             if (r < M && tok < N) {
-                if (OUT == 1) ((float*)y)[(int64_t)tok * M + r] = acc[nt][v];
-                else          ((uint16_t*)y)[(int64_t)tok * M + r] = f32_to_f16_bits(acc[nt][v]);
+                if (OUT == 1) ((float*)y)[(int64_t)tok * M + r] = acc[tt][v];
+                else          ((uint16_t*)y)[(int64_t)tok * M + r] = f32_to_f16_bits(acc[tt][v]);
             }
         }
     }
 }
 
-hipError_t mmq_launch(void* y, const uint8_t* W, int type, const void* q8, int M, int N, int K, int Npad,
-                      int out_kind, hipStream_t st) {
+hipError_t mmq_launch(void* y, const uint8_t* W, int type, const uint16_t* codes, const uint32_t* scl, int M, int N,
+                      int K, int Npad, int out_kind, hipStream_t st) {
     const int tiles = ((M + TM - 1) / TM) * (Npad / TN);
-    const uint8_t* q = (const uint8_t*)q8;
     if (type == TYPE_Q4_K) {
-        if (out_kind == 0) hipLaunchKernelGGL(mmq_q4k_kernel<0>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, q, M, N, K, Npad);
-        else if (out_kind == 1) hipLaunchKernelGGL(mmq_q4k_kernel<1>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, q, M, N, K, Npad);
-        else hipLaunchKernelGGL(mmq_q4k_kernel<2>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, q, M, N, K, Npad);
+        if (out_kind == 0) hipLaunchKernelGGL(mmq_q4k_kernel<0>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad);
+        else if (out_kind == 1) hipLaunchKernelGGL(mmq_q4k_kernel<1>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad);
+        else hipLaunchKernelGGL(mmq_q4k_kernel<2>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad);
     } else {
-        if (out_kind == 0) hipLaunchKernelGGL(mmq_q6k_kernel<0>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, q, M, N, K, Npad);
-        else if (out_kind == 1) hipLaunchKernelGGL(mmq_q6k_kernel<1>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, q, M, N, K, Npad);
-        else hipLaunchKernelGGL(mmq_q6k_kernel<2>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, q, M, N, K, Npad);
+        if (out_kind == 0) hipLaunchKernelGGL(mmq_q6k_kernel<0>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad);
+        else if (out_kind == 1) hipLaunchKernelGGL(mmq_q6k_kernel<1>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad);
+        else hipLaunchKernelGGL(mmq_q6k_kernel<2>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad);
     }
     return hipGetLastError();
 }

@@ -3,6 +3,8 @@
   pair  : the decode gate/up pair GEMV (Q4_K 2 x 9728 x 2560) over 36 distinct
           layers' weights, 3 passes -- the dominant kernel of bench.py
   lmhead: the Q6_K lm_head GEMV (151936 x 2560, fp32 out), 4 distinct copies
+  e2e   : the Qwen3-4B-shaped Q4_K_M decoder (36 layers, INT8 KV): prefill
+          of a 512-token prompt, then 32 greedy decode steps
   copy  : a plain device-to-device copy of 256 MiB (calibrates FETCH_SIZE /
           WRITE_SIZE against a known byte count)
 """
@@ -41,6 +43,17 @@ def main(mode):
         for _ in range(3):
             for wi in ws:
                 jllm.gemv_quant_f32(y, wi, 14, x, 151936, 2560)
+    elif mode == "e2e":
+        import decoder
+        shape = decoder.QWEN3_4B
+        model = decoder.synth_device(shape, 4242, dev)
+        d = decoder.Decoder(shape, model, 640, max_batch=512)
+        prompt = torch.randint(0, shape.vocab_size, (512,), dtype=torch.int32, device=dev,
+                               generator=torch.Generator(device=dev).manual_seed(1))
+        toks = torch.zeros(33, dtype=torch.int32, device=dev)
+        d.generate(prompt, 33, toks)
+        torch.cuda.synchronize()
+        d.close()
     elif mode == "copy":
         a = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
         b = torch.empty_like(a)

@@ -81,9 +81,10 @@ int jllm_hip_gemv_quant_dequant_f32(float* y, const void* W, int ggml_type, cons
 int jllm_hip_quantize_q8_1(const uint16_t* x, void* y, int K, void* stream);
 
 /* Batched GEMM y[N x M] (fp16, token-major) = x[N x K] . W^T.  N == 1 routes
- * to jllm_hip_gemv_quant; otherwise the activation is quantised to q8_1 and
- * multiplied with int8 matrix cores (Q4_K: DS4 layout, exact int32 dot per
- * 32-weight sub-block; Q6_K: D4 layout, per 16-weight group).  Uses a
+ * to jllm_hip_gemv_quant; otherwise the activation is quantised to q8_1 (the
+ * reference's DS4 values for Q4_K, D4 for Q6_K) and multiplied on the matrix
+ * cores with every 32-weight sub-block (Q4_K) / 16-weight group (Q6_K) dot
+ * formed exactly, then scaled as the reference does.  Uses a
  * library-owned q8 scratch buffer (grown on demand, never freed); calls on
  * one device must be serialised (one stream), as in the reference.
  * Replaces gemm_quant_batched, jllm_kernels.h:135 (gemv_q4.cu:2478-2517),
@@ -104,12 +105,13 @@ int jllm_hip_gemm_quant_batched_f32(float* y, const void* W, int ggml_type, cons
  * Npad is a multiple of 64 and >= N; columns >= N are written as zeros. */
 int jllm_hip_quantize_mmq_q8_1(const uint16_t* x, void* q8, int N, int K, int Npad, int ds4, void* stream);
 
-/* Test hook: the raw int32 dots the MMQ kernels compute, out [N][M][K/G]
- * (G = 32 for Q4_K sub-blocks, 16 for Q6_K groups), from a q8 buffer made by
- * jllm_hip_quantize_mmq_q8_1.  No reference counterpart (the reference keeps
- * these in registers); exists so the int32 dots can be checked bit-exactly. */
-int jllm_hip_mmq_subdots(int32_t* out, const void* W, int ggml_type, const void* q8,
-                         int M, int N, int K, int Npad, void* stream);
+/* Test hook: the exact sub-block dots the production MMQ kernels form,
+ * out [N][M][K/G] int32 (G = 32 for Q4_K sub-blocks, 16 for Q6_K groups),
+ * for activations x [N x K] quantised by the production quantiser.  No
+ * reference counterpart (the reference keeps these in registers); exists so
+ * the dots can be checked bit-exactly against the reference's int32 dots. */
+int jllm_hip_mmq_subdots(int32_t* out, const void* W, int ggml_type, const uint16_t* x,
+                         int M, int N, int K, void* stream);
 
 /* Single-query (decode) attention over an INT8 (kv_int8 != 0) or FP16 KV
  * cache, split-K: the keys are cut into slices processed in parallel, each

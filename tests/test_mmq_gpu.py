@@ -1,5 +1,6 @@
 """GPU parity of the prefill path: MMQ activation quantiser (bit-exact), the
-int32 sub-block dots of the int8 MFMA kernels (bit-exact) and the fp32 /
+exact sub-block dots the MMQ kernels form on the matrix cores (bit-exact
+against the reference's int32 dots) and the fp32 /
 fp16 GEMM outputs (rel_inf <= 1e-3 against the CPU oracle; BASELINE
 config 3 shapes are checked on a sampled row subset at full token count)."""
 import numpy as np
@@ -38,19 +39,18 @@ def test_quantize_mmq_bit_exact(dev, ds4, N, K):
 
 
 @pytest.mark.parametrize("t", [12, 14])
-@pytest.mark.parametrize("M,N,K", [(128, 64, 256), (200, 70, 512), (33, 5, 2560)])
+@pytest.mark.parametrize("M,N,K", [(128, 64, 256), (200, 70, 512), (33, 5, 2560), (64, 129, 768)])
 def test_mmq_int32_dots_bit_exact(dev, t, M, N, K):
     print_case("mmq_subdots", t, M, N, K)
     g = synth.rng(M + N + K + t)
     W = synth.weights(g, t, M, K)
     x = synth.x_f16(g, (N, K))
     Npad = _npad(N)
-    q8 = _quantize_dev(x, N, K, Npad, t == 12, dev)
     G = 32 if t == 12 else 16
     out = torch.zeros(N * M * (K // G), dtype=torch.int32, device=dev)
-    jllm.call("jllm_hip_mmq_subdots", out, to_dev(W), t, q8, M, N, K, Npad)
+    jllm.call("jllm_hip_mmq_subdots", out, to_dev(W), t, to_dev(x), M, N, K)
     got = from_dev(out).reshape(N, M, K // G)
-    want = oracle.mmq_subdots(W, t, from_dev(q8), M, N, K, Npad)
+    want = oracle.mmq_subdots(W, t, oracle.quantize_mmq(x, N, K, Npad, t == 12), M, N, K, Npad)
     assert np.array_equal(got, want)
 
 
