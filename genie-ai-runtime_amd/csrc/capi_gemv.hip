@@ -100,6 +100,20 @@ int make_seg(const char* tag, GemvSeg& s, void* y, const void* W, int type, int 
     return JLLM_OK;
 }
 
+// RMSNorm prologue: the whole activation is staged in the first pass
+int set_rms(const char* tag, GemvArgs& a, const void* nw, int fp32, float eps) {
+    if (a.K > 4096) {
+        fprintf(stderr, "[%s] fused RMSNorm needs K <= 4096 (K=%d)\n", tag, a.K);
+        return JLLM_ERR_INVALID;
+    }
+    if (!nw || !aligned16(nw)) {
+        fprintf(stderr, "[%s] RMSNorm weight pointer must be non-null and 16-byte aligned\n", tag);
+        return JLLM_ERR_INVALID;
+    }
+    a.pre.kind = PRE_RMS; a.pre.nw = nw; a.pre.nw_fp32 = fp32 != 0; a.pre.eps = eps;
+    return JLLM_OK;
+}
+
 int run(const char* tag, GemvArgs& a, bool mmvq, int out, void* stream) {
     return launch_status(gemv_launch(a, mmvq, out, (hipStream_t)stream), tag);
 }
@@ -158,6 +172,41 @@ int jllm_hip_gemv_quant_triple(uint16_t* y0, const void* W0, int t0, int M0,
     if ((st = make_seg("GEMV", a.seg[1], y1, W1, t1, M1, nullptr))) return st;
     if ((st = make_seg("GEMV", a.seg[2], y2, W2, t2, M2, nullptr))) return st;
     return run("GEMV", a, true, OUT_HALF, stream);
+}
+
+int jllm_hip_gemv_quant_triple_rmsnorm(uint16_t* y0, const void* W0, int t0, int M0,
+                                       uint16_t* y1, const void* W1, int t1, int M1,
+                                       uint16_t* y2, const void* W2, int t2, int M2,
+                                       const uint16_t* x, const void* norm_weight, int weight_fp32, float eps,
+                                       int K, void* stream) {
+    int st = check_common("GEMV", K, x); if (st) return st;
+    GemvArgs a{}; a.nseg = 3; a.K = K; a.x = x;
+    if ((st = set_rms("GEMV", a, norm_weight, weight_fp32, eps))) return st;
+    if ((st = make_seg("GEMV", a.seg[0], y0, W0, t0, M0, nullptr))) return st;
+    if ((st = make_seg("GEMV", a.seg[1], y1, W1, t1, M1, nullptr))) return st;
+    if ((st = make_seg("GEMV", a.seg[2], y2, W2, t2, M2, nullptr))) return st;
+    return run("GEMV", a, true, OUT_HALF, stream);
+}
+
+int jllm_hip_gemv_quant_pair_rmsnorm(uint16_t* y0, const void* W0, int t0, int M0,
+                                     uint16_t* y1, const void* W1, int t1, int M1,
+                                     const uint16_t* x, const void* norm_weight, int weight_fp32, float eps,
+                                     int K, void* stream) {
+    int st = check_common("GEMV", K, x); if (st) return st;
+    GemvArgs a{}; a.nseg = 2; a.K = K; a.x = x;
+    if ((st = set_rms("GEMV", a, norm_weight, weight_fp32, eps))) return st;
+    if ((st = make_seg("GEMV", a.seg[0], y0, W0, t0, M0, nullptr))) return st;
+    if ((st = make_seg("GEMV", a.seg[1], y1, W1, t1, M1, nullptr))) return st;
+    return run("GEMV", a, t0 == 12 && t1 == 12, OUT_HALF, stream);
+}
+
+int jllm_hip_gemv_quant_f32_rmsnorm(float* y, const void* W, int type, const uint16_t* x, const void* norm_weight,
+                                    int weight_fp32, float eps, int M, int K, void* stream) {
+    int st = check_common("GEMV", K, x); if (st) return st;
+    GemvArgs a{}; a.nseg = 1; a.K = K; a.x = x;
+    if ((st = set_rms("GEMV", a, norm_weight, weight_fp32, eps))) return st;
+    if ((st = make_seg("GEMV", a.seg[0], y, W, type, M, nullptr))) return st;
+    return run("GEMV", a, type == 12, OUT_F32, stream);
 }
 
 int jllm_hip_quantize_q8_1(const uint16_t* x, void* y, int K, void* stream) {

@@ -10,12 +10,14 @@
 //                (src/engine/decode.cu:2779-2807, :1760-1884) and the
 //                first-token sampling from the last prefill row (:2950-2990)
 //   sampling     greedy (src/engine/sample.cpp:160-170), on the GPU here
-// with two MI355X-specific changes that do not alter the arithmetic: the
-// q/k RMSNorm + RoPE + KV quantisation of each layer is one fused launch
-// (the intermediate fp16 roundings are kept), and the greedy argmax runs on
-// the device so the sampled token id never leaves HBM -- the next step's
-// embedding gather reads it there, and a whole generation needs no host
-// synchronisation until the caller copies the tokens out.
+// with MI355X-specific fusions that keep the arithmetic (the fp16 roundings
+// of the unfused sequence are kept; only the order of the RMSNorm sums of
+// squares differs): in a decode step the attention / FFN / output RMSNorms
+// run inside the staging of the GEMV that consumes them, the q/k RMSNorm + RoPE + KV quantisation of each layer is
+// one launch, and the greedy argmax runs on the device so the sampled token
+// id never leaves HBM -- the next step's embedding gather reads it there, and
+// a whole generation needs no host synchronisation until the caller copies
+// the tokens out.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdio.h>
@@ -70,9 +72,9 @@ int decode_layer(jllm_hip_decoder* d, int l, int pos, void* st) {
     const jllm_hip_layer_weights& w = d->lw[l];
     const int H = c.hidden_dim, QD = c.n_heads * c.head_dim, KVD = c.n_kv_heads * c.head_dim, I = c.intermediate_dim;
     const size_t row = (size_t)KVD * (c.kv_int8 ? 1 : 2);
-    TRY(jllm_hip_fused_rmsnorm_residual(d->normed, d->x, nullptr, w.rms_attn, 1, H, c.rms_eps, c.norm_fp32, st));
-    TRY(jllm_hip_gemv_quant_triple(d->q, w.wq, w.type_wq, QD, d->k, w.wk, w.type_wk, KVD, d->v, w.wv, w.type_wv, KVD,
-                                   d->normed, H, st));
+    // attention RMSNorm fused into the QKV GEMV's activation staging
+    TRY(jllm_hip_gemv_quant_triple_rmsnorm(d->q, w.wq, w.type_wq, QD, d->k, w.wk, w.type_wk, KVD, d->v, w.wv,
+                                           w.type_wv, KVD, d->x, w.rms_attn, c.norm_fp32, c.rms_eps, H, st));
     TRY(jllm_hip_qk_norm_rope_store_kv(d->q, d->k, d->v, w.q_norm, w.k_norm, c.qk_norm_fp32, c.rms_eps,
                                        layer_k(d, l) + (size_t)pos * row, layer_v(d, l) + (size_t)pos * row,
                                        layer_ks(d, l) + (size_t)pos * c.n_kv_heads,
@@ -83,9 +85,9 @@ int decode_layer(jllm_hip_decoder* d, int l, int pos, void* st) {
                                         c.kv_int8 ? layer_ks(d, l) : nullptr, c.kv_int8 ? layer_vs(d, l) : nullptr, 0,
                                         st));
     TRY(jllm_hip_gemv_quant_add(d->x2, w.wo, w.type_wo, d->attn, d->x, H, QD, st));
-    TRY(jllm_hip_fused_rmsnorm_residual(d->normed, d->x2, nullptr, w.rms_ffn, 1, H, c.rms_eps, c.norm_fp32, st));
-    TRY(jllm_hip_gemv_quant_pair(d->gate, w.w_gate, w.type_w_gate, I, d->up, w.w_up, w.type_w_up, I, d->normed, H,
-                                 st));
+    // FFN RMSNorm fused into the gate/up GEMV
+    TRY(jllm_hip_gemv_quant_pair_rmsnorm(d->gate, w.w_gate, w.type_w_gate, I, d->up, w.w_up, w.type_w_up, I, d->x2,
+                                         w.rms_ffn, c.norm_fp32, c.rms_eps, H, st));
     TRY(jllm_hip_fused_swiglu(d->act, d->gate, d->up, 1, I, st));
     TRY(jllm_hip_gemv_quant_add(d->x, w.w_down, w.type_w_down, d->act, d->x2, H, I, st));
     return JLLM_OK;
@@ -123,13 +125,12 @@ int prefill_layer(jllm_hip_decoder* d, int l, int start, int N, void* st) {
 }
 
 // output norm -> lm_head (fp32 logits) -> greedy token into *out
-// (decode.cu:2147-2158 and :2956-2966; sample_greedy on the device)
+// (decode.cu:2147-2158 and :2956-2966; sample_greedy on the device); the
+// norm is fused into the lm_head GEMV's activation staging
 int head(jllm_hip_decoder* d, const uint16_t* xrow, int32_t* out, void* st) {
     const jllm_hip_decoder_config& c = d->cfg;
-    TRY(jllm_hip_fused_rmsnorm_residual(d->normed, xrow, nullptr, d->mw.output_norm, 1, c.hidden_dim, c.rms_eps,
-                                        c.output_norm_fp32, st));
-    TRY(jllm_hip_gemv_quant_f32(d->logits, d->mw.output, d->mw.output_type, d->normed, c.vocab_size, c.hidden_dim,
-                                st));
+    TRY(jllm_hip_gemv_quant_f32_rmsnorm(d->logits, d->mw.output, d->mw.output_type, xrow, d->mw.output_norm,
+                                        c.output_norm_fp32, c.rms_eps, c.vocab_size, c.hidden_dim, st));
     if (out) TRY(jllm_hip_argmax_f32(out, d->logits, c.vocab_size, st));
     return JLLM_OK;
 }

@@ -8,6 +8,17 @@ namespace jllm_hip {
 
 enum OutKind { OUT_HALF = 0, OUT_F32 = 1, OUT_ADD = 2 };
 
+// Activation prologue applied while the activation is staged: none or
+// RMSNorm of x (x <- half(x / sqrt(mean(x^2) + eps) * w)), with the values
+// of the separate RMSNorm kernel (up to the order of the sum of squares).
+enum PreKind { PRE_NONE = 0, PRE_RMS = 1 };
+struct GemvPre {
+    int kind;
+    const void* nw;         // RMSNorm weight [K], fp32 or fp16
+    int nw_fp32;
+    float eps;
+};
+
 // One output segment of a fused GEMV launch: rows [0, M) of W (type 12 or
 // 14), result to y (fp16 or fp32), optional fp16 residual for OUT_ADD.
 struct GemvSeg {
@@ -23,6 +34,7 @@ struct GemvArgs {
     int nseg;
     int K;
     const uint16_t* x;     // fp16 activation [K]
+    GemvPre pre;
 };
 
 // Arguments of the streaming kernel (filled by gemv_launch).  Segments
@@ -39,6 +51,7 @@ struct StreamArgs {
     int rows_q[2], rows_r[2];       // rows per wave (quotient, remainder) per type
     int slots_per_wave;     // LDS block slots per wave (max rows per wave * nb)
     int wg_rows;            // residual rows staged per workgroup (waves * max rows per wave)
+    GemvPre pre;
 };
 
 size_t gemv_lds_bytes(bool mmvq, int K);

@@ -569,10 +569,47 @@ __device__ __forceinline__ int make_pieces(const StreamArgs& a, int g0, int g1, 
     return nr;
 }
 
+// ---- activation prologues (applied to an 8-value chunk held in registers)
+
+__device__ __forceinline__ float sumsq8(const u32x4& a) {
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float v0 = f16_bits_to_f32(w[i] & 0xFFFFu), v1 = f16_bits_to_f32(w[i] >> 16);
+        s += v0 * v0 + v1 * v1;
+    }
+    return s;
+}
+
+// half(v * rrms * w) for the 8 values of a chunk; weights: two 16-byte
+// words of fp32 (w_fp32) or one of fp16 (in w0)
+__device__ __forceinline__ u32x4 rms8(const u32x4& a, float rrms, int w_fp32, const u32x4& w0, const u32x4& w1) {
+#pragma clang fp contract(off)
+    float wv[8];
+    if (w_fp32) {
+        const uint32_t ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) wv[i] = __builtin_bit_cast(float, ww[i]);
+    } else {
+        const uint32_t hw[4] = {w0.x, w0.y, w0.z, w0.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) { wv[2 * i] = f16_bits_to_f32(hw[i] & 0xFFFFu); wv[2 * i + 1] = f16_bits_to_f32(hw[i] >> 16); }
+    }
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float v0 = f16_bits_to_f32(w[i] & 0xFFFFu), v1 = f16_bits_to_f32(w[i] >> 16);
+        o[i] = (uint32_t)f32_to_f16_bits(v0 * rrms * wv[2 * i]) | ((uint32_t)f32_to_f16_bits(v1 * rrms * wv[2 * i + 1]) << 16);
+    }
+    return u32x4_make(o[0], o[1], o[2], o[3]);
+}
+
 // One wave's rows: rounds stream through two register stages and the wave's
 // own LDS buffer; the slots of its rows are added up and stored at the end.
 // Both weight types run the same two workgroup barriers (activation staging).
-template <bool MMVQ, int OUT, int TYPE, int L, int NX>
+template <bool MMVQ, int OUT, int TYPE, int L, int NX, int PRE>
 __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int g0, int g1, int lane, int wv,
                                           uint16_t* res_lds, int wg_g0) {
     const int nb = a.nb, K = a.K;
@@ -584,10 +621,21 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         // then the weight loads: the CU's memory pipeline returns them first
         const int nch = K / 8;
         u32x4 xv[NX];
+        u32x4 nwv[PRE == PRE_RMS ? 2 * NX : 1];     // RMSNorm weights of the lane's chunks, loaded with x
 #pragma unroll
         for (int i = 0; i < NX; i++) {
             const int c = (int)threadIdx.x + ST_T * i;
             xv[i] = *(const u32x4*)(a.x + 8 * (c < nch ? c : 0));
+            if (PRE == PRE_RMS) {
+                const int cc = c < nch ? c : 0;
+                if (a.pre.nw_fp32) {
+                    nwv[2 * i] = *((const u32x4*)a.pre.nw + 2 * cc);
+                    nwv[2 * i + 1] = *((const u32x4*)a.pre.nw + 2 * cc + 1);
+                } else {
+                    nwv[2 * i] = *((const u32x4*)a.pre.nw + cc);
+                    nwv[2 * i + 1] = u32x4_make(0u, 0u, 0u, 0u);
+                }
+            }
         }
         uint16_t rv = 0;
         const int nres = OUT == OUT_ADD ? min(a.wg_rows, a.row_off[3] - wg_g0) : 0;   // nres <= ST_T
@@ -597,6 +645,31 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         issue_round<L>(round_desc<TYPE, L>(a, pc, 0), R0, lane);
         issue_round<L>(round_desc<TYPE, L>(a, pc, 1), R1, lane);
         __builtin_amdgcn_sched_barrier(0);
+        if (PRE == PRE_RMS) {
+            // sum of squares of the whole activation (K <= NX * ST_T * 8 here):
+            // lanes, then waves through LDS (the first words of wave 0's round
+            // buffer, not written before the staging barrier below)
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NX; i++) {
+                const int c = (int)threadIdx.x + ST_T * i;
+                if (c < nch) ss += sumsq8(xv[i]);
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            float* red = (float*)(lds + a.xlds_bytes);
+            if (lane == 0) red[wv] = ss;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+            const float rrms = 1.0f / sqrtf(tot / (float)K + a.pre.eps);
+#pragma unroll
+            for (int i = 0; i < NX; i++) {
+                const int c = (int)threadIdx.x + ST_T * i;
+                if (c < nch) xv[i] = rms8(xv[i], rrms, a.pre.nw_fp32, nwv[2 * i], nwv[2 * i + 1]);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < NX; i++) {
             const int c = (int)threadIdx.x + ST_T * i;
@@ -673,7 +746,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
 template <class T>
 __device__ __forceinline__ void pin_sgpr(const T& v) { asm volatile("" :: "s"(v)); }
 
-template <bool MMVQ, int OUT, int L, int NX>
+template <bool MMVQ, int OUT, int L, int NX, int PRE>
 __global__ __launch_bounds__(ST_T) __attribute__((amdgpu_waves_per_eu(4)))
 void gemv_stream_kernel(StreamArgs a_in) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -701,25 +774,25 @@ void gemv_stream_kernel(StreamArgs a_in) {
     }
     uint16_t* res_lds = (uint16_t*)(lds + a.xlds_bytes + ST_W * (64 * 16 * L) + ST_W * 4 * a.slots_per_wave);
     // (both bodies hold the same two workgroup barriers)
-    if (q4) wave_body<MMVQ, OUT, TYPE_Q4_K, L, NX>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
-    else    wave_body<MMVQ, OUT, TYPE_Q6_K, L, NX>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
+    if (q4) wave_body<MMVQ, OUT, TYPE_Q4_K, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
+    else    wave_body<MMVQ, OUT, TYPE_Q6_K, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
 }
 
-template <bool MMVQ, int OUT, int L, int NX>
+template <bool MMVQ, int OUT, int L, int NX, int PRE>
 static hipError_t launch_s(const StreamArgs& a, int grid, size_t lds, hipStream_t st) {
-    static const hipError_t attr = hipFuncSetAttribute((const void*)gemv_stream_kernel<MMVQ, OUT, L, NX>,
+    static const hipError_t attr = hipFuncSetAttribute((const void*)gemv_stream_kernel<MMVQ, OUT, L, NX, PRE>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((gemv_stream_kernel<MMVQ, OUT, L, NX>), dim3(grid), dim3(ST_T), lds, st, a);
+    hipLaunchKernelGGL((gemv_stream_kernel<MMVQ, OUT, L, NX, PRE>), dim3(grid), dim3(ST_T), lds, st, a);
     return hipGetLastError();
 }
 
-template <bool MMVQ, int OUT, int L>
+template <bool MMVQ, int OUT, int L, int PRE = PRE_NONE>
 static hipError_t launch_nx(const StreamArgs& a, int grid, size_t lds, hipStream_t st) {
     const int nch = a.K / 8;
-    if (nch <= ST_T) return launch_s<MMVQ, OUT, L, 1>(a, grid, lds, st);
-    if (nch <= 2 * ST_T) return launch_s<MMVQ, OUT, L, 2>(a, grid, lds, st);
-    return launch_s<MMVQ, OUT, L, 5>(a, grid, lds, st);
+    if (nch <= ST_T) return launch_s<MMVQ, OUT, L, 1, PRE>(a, grid, lds, st);
+    if (PRE == PRE_RMS || nch <= 2 * ST_T) return launch_s<MMVQ, OUT, L, 2, PRE>(a, grid, lds, st);
+    return launch_s<MMVQ, OUT, L, 5, PRE>(a, grid, lds, st);
 }
 
 static constexpr size_t LDS_CU = 160 * 1024;
@@ -788,6 +861,15 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     a.wg_rows = (int)(ST_W * max_rows);
     const size_t lds = lds_of();
     const int g = (int)grid;
+    a.pre = in.pre;
+    if (in.pre.kind == PRE_RMS) {      // the sum of squares needs the whole x in the first staging pass
+        if (a.K > 2 * ST_T * 8) return hipErrorInvalidValue;
+        if (mmvq && out_kind == OUT_HALF) return launch_nx<true, OUT_HALF, ST_L, PRE_RMS>(a, g, lds, st);
+        if (mmvq && out_kind == OUT_F32)  return launch_nx<true, OUT_F32, ST_L, PRE_RMS>(a, g, lds, st);
+        if (!mmvq && out_kind == OUT_F32) return launch_nx<false, OUT_F32, ST_L, PRE_RMS>(a, g, lds, st);
+        if (!mmvq && out_kind == OUT_HALF) return launch_nx<false, OUT_HALF, ST_L, PRE_RMS>(a, g, lds, st);
+        return hipErrorInvalidValue;
+    }
     if (mmvq) {
         if (out_kind == OUT_HALF) return launch_nx<true, OUT_HALF, ST_L>(a, g, lds, st);
         if (out_kind == OUT_F32)  return launch_nx<true, OUT_F32, ST_L>(a, g, lds, st);

@@ -30,6 +30,9 @@ SIGNATURES = {
     "jllm_hip_gemv_quant_f32": (I, [P, P, I, P, I, I, P]),
     "jllm_hip_gemv_quant_dequant_f32": (I, [P, P, I, P, I, I, P]),
     "jllm_hip_quantize_q8_1": (I, [P, P, I, P]),
+    "jllm_hip_gemv_quant_triple_rmsnorm": (I, [P, P, I, I, P, P, I, I, P, P, I, I, P, P, I, F, I, P]),
+    "jllm_hip_gemv_quant_pair_rmsnorm": (I, [P, P, I, I, P, P, I, I, P, P, I, F, I, P]),
+    "jllm_hip_gemv_quant_f32_rmsnorm": (I, [P, P, I, P, P, I, F, I, I, P]),
     "jllm_hip_gemm_quant_batched": (I, [P, P, I, P, I, I, I, P]),
     "jllm_hip_gemm_quant_batched_f32": (I, [P, P, I, P, I, I, I, P]),
     "jllm_hip_quantize_mmq_q8_1": (I, [P, P, I, I, I, I, P]),

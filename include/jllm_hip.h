@@ -76,6 +76,28 @@ int jllm_hip_gemv_quant_f32(float* y, const void* W, int ggml_type, const uint16
 int jllm_hip_gemv_quant_dequant_f32(float* y, const void* W, int ggml_type, const uint16_t* x,
                                     int M, int K, void* stream);
 
+/* RMSNorm fused into the GEMV's activation staging (no reference
+ * counterpart: each replaces two launches of the engine's decode step).
+ * x <- half(x / sqrt(mean(x^2) + eps) * norm_weight) -- the values of
+ * jllm_hip_fused_rmsnorm_residual without residual, up to the order of the
+ * sum of squares -- then the GEMV runs as its unfused entry point:
+ *   _triple_rmsnorm / _pair_rmsnorm: gemv_quant_triple / _pair
+ *     (decode.cu:1208-1224 and :1234-1238);
+ *   _f32_rmsnorm: the output norm + lm_head (decode.cu:2147-2158).
+ * norm_weight: fp32 (weight_fp32 != 0) or fp16, 16-byte aligned; K <= 4096
+ * (hidden sizes; every workgroup sums the squares of the whole vector). */
+int jllm_hip_gemv_quant_triple_rmsnorm(uint16_t* y0, const void* W0, int ggml_type0, int M0,
+                                       uint16_t* y1, const void* W1, int ggml_type1, int M1,
+                                       uint16_t* y2, const void* W2, int ggml_type2, int M2,
+                                       const uint16_t* x, const void* norm_weight, int weight_fp32, float eps,
+                                       int K, void* stream);
+int jllm_hip_gemv_quant_pair_rmsnorm(uint16_t* y0, const void* W0, int ggml_type0, int M0,
+                                     uint16_t* y1, const void* W1, int ggml_type1, int M1,
+                                     const uint16_t* x, const void* norm_weight, int weight_fp32, float eps,
+                                     int K, void* stream);
+int jllm_hip_gemv_quant_f32_rmsnorm(float* y, const void* W, int ggml_type, const uint16_t* x,
+                                    const void* norm_weight, int weight_fp32, float eps, int M, int K, void* stream);
+
 /* q8_1 quantiser in the reference block layout {u16 d, u16 s, i8 qs[32]}
  * (36 B per 32 values).  Replaces quantize_q8_1, gemv_q4.cu:468. */
 int jllm_hip_quantize_q8_1(const uint16_t* x, void* y, int K, void* stream);

@@ -140,3 +140,62 @@ def test_gemv_errors(dev):
     host = torch.zeros(4 * 2 * 144, dtype=torch.uint8)           # plain host memory: no fallback
     with pytest.raises(jllm.JllmError, match="visible"):
         jllm.gemv_quant(y, host, 12, x, 4, 512)
+
+
+# ---- fused activation prologues ---------------------------------------------------
+
+def _rms_case(seed, K):
+    g = synth.rng(seed)
+    x = synth.x_f16(g, K)
+    w = (1.0 + 0.02 * g.standard_normal(K)).astype(np.float32)
+    return g, x, w
+
+
+def test_triple_and_pair_rmsnorm(dev):
+    K, eps = 2560, 1e-6
+    g, x, w = _rms_case(700, K)
+    xn = oracle.rmsnorm(x, None, w, 1, K, eps, True)
+    xq = oracle.quantize_q8_1(xn, K)
+    Wq, Wk, Wv = synth.q4k(g, 4096, K), synth.q4k(g, 1024, K), synth.q6k(g, 1024, K)
+    ys = [empty_f16(4096), empty_f16(1024), empty_f16(1024)]
+    print_case("triple_rmsnorm")
+    jllm.call("jllm_hip_gemv_quant_triple_rmsnorm", ys[0], to_dev(Wq), 12, 4096, ys[1], to_dev(Wk), 12, 1024,
+              ys[2], to_dev(Wv), 14, 1024, to_dev(x), to_dev(w), 1, eps, K)
+    for y, W, t, M in zip(ys, (Wq, Wk, Wv), (12, 12, 14), (4096, 1024, 1024)):
+        ok, err = _close_f16(from_dev(y, np.uint16), oracle.mmvq(W, t, xq, M, K))
+        assert ok, (t, M, err)
+    print_case("pair_rmsnorm fp16 weight")
+    w16 = w.astype(np.float16).view(np.uint16)
+    xn16 = oracle.rmsnorm(x, None, w16, 1, K, eps, False)
+    xq16 = oracle.quantize_q8_1(xn16, K)
+    Wg, Wu = synth.q4k(g, 9728, K), synth.q4k(g, 9728, K)
+    y0, y1 = empty_f16(9728), empty_f16(9728)
+    jllm.call("jllm_hip_gemv_quant_pair_rmsnorm", y0, to_dev(Wg), 12, 9728, y1, to_dev(Wu), 12, 9728, to_dev(x),
+              to_dev(w16), 0, eps, K)
+    for y, W in ((y0, Wg), (y1, Wu)):
+        ok, err = _close_f16(from_dev(y, np.uint16), oracle.mmvq(W, 12, xq16, 9728, K))
+        assert ok, err
+
+
+@pytest.mark.parametrize("t", [12, 14])
+def test_f32_rmsnorm_lm_head(dev, t):
+    K, M, eps = 2560, 151936 if t == 14 else 4000, 1e-6
+    print_case("f32_rmsnorm", t, M)
+    g, x, w = _rms_case(710 + t, K)
+    W = synth.weights(g, t, M, K)
+    xn = oracle.rmsnorm(x, None, w, 1, K, eps, True)
+    y = empty_f32(M)
+    jllm.call("jllm_hip_gemv_quant_f32_rmsnorm", y, to_dev(W), t, to_dev(x), to_dev(w), 1, eps, M, K)
+    want = oracle.mmvq(W, t, oracle.quantize_q8_1(xn, K), M, K) if t == 12 else oracle.gemv_quant_cpu(W, t, xn, M, K)
+    assert rel_inf(from_dev(y), want) <= TOL
+
+
+def test_fused_prologue_argument_checks(dev):
+    l = jllm.lib()
+    x = to_dev(synth.x_f16(synth.rng(1), 4352))
+    y = empty_f32(16)
+    W = to_dev(synth.q4k(synth.rng(2), 16, 4352))
+    w = to_dev(np.ones(4352, np.float32))
+    # K above the single-pass staging limit of the fused RMSNorm
+    assert l.jllm_hip_gemv_quant_f32_rmsnorm(jllm._ptr(y), jllm._ptr(W), 12, jllm._ptr(x), jllm._ptr(w), 1,
+                                             1e-6, 16, 4352, None) == -1
