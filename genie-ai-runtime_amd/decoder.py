@@ -207,3 +207,106 @@ class Decoder:
             self.close()
         except Exception:
             pass
+
+
+# ---- GGUF ------------------------------------------------------------------------
+
+def write_gguf(path, shape, model_np, arch="qwen3", max_seq=40960):
+    """Store a synth_np model as a GGUF v3 file with llama.cpp's tensor names
+    (the names the reference loader maps, model.cpp:675-810)."""
+    lib = jllm.lib()
+    w = lib.jllm_hip_gguf_writer_create()
+    if not w:
+        raise jllm.JllmError("gguf writer")
+    try:
+        def u32(k, v):
+            jllm.check(lib.jllm_hip_gguf_writer_set_u32(w, k.encode(), int(v)), k)
+
+        def f32(k, v):
+            jllm.check(lib.jllm_hip_gguf_writer_set_f32(w, k.encode(), float(v)), k)
+        jllm.check(lib.jllm_hip_gguf_writer_set_str(w, b"general.architecture", arch.encode()), "arch")
+        jllm.check(lib.jllm_hip_gguf_writer_set_str(w, b"general.name", b"random Q4_K_M decoder"), "name")
+        u32(f"{arch}.block_count", shape.n_layers)
+        u32(f"{arch}.context_length", max_seq)
+        u32(f"{arch}.embedding_length", shape.hidden_dim)
+        u32(f"{arch}.feed_forward_length", shape.intermediate_dim)
+        u32(f"{arch}.attention.head_count", shape.n_heads)
+        u32(f"{arch}.attention.head_count_kv", shape.n_kv_heads)
+        u32(f"{arch}.attention.key_length", shape.head_dim)
+        u32(f"{arch}.attention.value_length", shape.head_dim)
+        f32(f"{arch}.rope.freq_base", shape.rope_theta)
+        f32(f"{arch}.attention.layer_norm_rms_epsilon", shape.rms_eps)
+        keep = []
+
+        def tensor(name, t, dims, arr):
+            a = np.ascontiguousarray(arr)
+            keep.append(a)
+            d = (ctypes.c_int64 * len(dims))(*dims)
+            jllm.check(lib.jllm_hip_gguf_writer_add_tensor(w, name.encode(), t, len(dims), d,
+                                                           a.ctypes.data_as(ctypes.c_void_p), a.nbytes), name)
+        H, V = shape.hidden_dim, shape.vocab_size
+        tensor("token_embd.weight", model_np["embd_type"], [H, V], model_np["tok_embd"])
+        tensor("output_norm.weight", 0, [H], model_np["output_norm"])
+        if model_np["output"] is not model_np["tok_embd"]:
+            tensor("output.weight", model_np["output_type"], [H, V], model_np["output"])
+        names = {"wq": "attn_q", "wk": "attn_k", "wv": "attn_v", "wo": "attn_output", "w_gate": "ffn_gate",
+                 "w_up": "ffn_up", "w_down": "ffn_down"}
+        for l, L in enumerate(model_np["layers"]):
+            for m in MATS:
+                M, K = shape.mat_shape(m)
+                tensor(f"blk.{l}.{names[m]}.weight", L["types"][m], [K, M], L[m])
+            tensor(f"blk.{l}.attn_norm.weight", 0, [H], L["rms_attn"])
+            tensor(f"blk.{l}.ffn_norm.weight", 0, [H], L["rms_ffn"])
+            tensor(f"blk.{l}.attn_q_norm.weight", 0, [shape.head_dim], L["q_norm"])
+            tensor(f"blk.{l}.attn_k_norm.weight", 0, [shape.head_dim], L["k_norm"])
+        jllm.check(lib.jllm_hip_gguf_writer_write(w, str(path).encode()), "gguf write")
+    finally:
+        lib.jllm_hip_gguf_writer_free(w)
+
+
+def gguf_config(path):
+    """(Config, raw handle) of a GGUF file; the caller closes the handle."""
+    lib = jllm.lib()
+    g = lib.jllm_hip_gguf_open(str(path).encode())
+    if not g:
+        raise jllm.JllmError(f"cannot read GGUF {path}")
+    cfg = Config()
+    st = lib.jllm_hip_gguf_config(g, ctypes.addressof(cfg))
+    if st:
+        lib.jllm_hip_gguf_close(g)
+        jllm.check(st, "gguf config")
+    return cfg, g
+
+
+class GGUFDecoder:
+    """A decoder over a GGUF file: tensors uploaded by the library's loader."""
+
+    def __init__(self, path, max_seq=None, max_batch=512):
+        lib = jllm.lib()
+        self.cfg, self.g = gguf_config(path)
+        if max_seq:
+            self.cfg.max_seq = max_seq
+        self.model = lib.jllm_hip_gguf_model_load(self.g, ctypes.addressof(self.cfg))
+        if not self.model:
+            lib.jllm_hip_gguf_close(self.g)
+            raise jllm.JllmError("gguf model load")
+        self.h = lib.jllm_hip_decoder_create(ctypes.addressof(self.cfg), lib.jllm_hip_gguf_model_weights(self.model),
+                                             lib.jllm_hip_gguf_layer_weights(self.model), max_batch)
+        if not self.h:
+            self.close()
+            raise jllm.JllmError("jllm_hip_decoder_create failed")
+
+    def generate(self, prompt, n_gen, out):
+        jllm.call("jllm_hip_decoder_generate", self.h, prompt, prompt.numel(), n_gen, out)
+
+    def close(self):
+        lib = jllm.lib()
+        if getattr(self, "h", None):
+            lib.jllm_hip_decoder_destroy(self.h)
+            self.h = None
+        if getattr(self, "model", None):
+            lib.jllm_hip_gguf_model_free(self.model)
+            self.model = None
+        if getattr(self, "g", None):
+            lib.jllm_hip_gguf_close(self.g)
+            self.g = None

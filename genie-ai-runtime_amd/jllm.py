@@ -54,6 +54,27 @@ SIGNATURES = {
     "jllm_hip_dequant_embedding_row": (I, [P, P, I, I, I, P]),
     "jllm_hip_dequant_embedding_rows": (I, [P, P, I, P, I, I, I, P]),
     "jllm_hip_argmax_f32": (I, [P, P, I, P]),
+    # GGUF reader / loader / writer
+    "jllm_hip_gguf_open": (P, [ctypes.c_char_p]),
+    "jllm_hip_gguf_close": (None, [P]),
+    "jllm_hip_gguf_n_tensors": (I64, [P]),
+    "jllm_hip_gguf_find_tensor": (I64, [P, ctypes.c_char_p]),
+    "jllm_hip_gguf_tensor": (I, [P, I64, P, P, P, P, P, P]),
+    "jllm_hip_gguf_get_u64": (I, [P, ctypes.c_char_p, P]),
+    "jllm_hip_gguf_get_f64": (I, [P, ctypes.c_char_p, P]),
+    "jllm_hip_gguf_get_str": (ctypes.c_char_p, [P, ctypes.c_char_p]),
+    "jllm_hip_gguf_config": (I, [P, P]),
+    "jllm_hip_gguf_model_load": (P, [P, P]),
+    "jllm_hip_gguf_model_weights": (P, [P]),
+    "jllm_hip_gguf_layer_weights": (P, [P]),
+    "jllm_hip_gguf_model_free": (None, [P]),
+    "jllm_hip_gguf_writer_create": (P, []),
+    "jllm_hip_gguf_writer_free": (None, [P]),
+    "jllm_hip_gguf_writer_set_u32": (I, [P, ctypes.c_char_p, ctypes.c_uint32]),
+    "jllm_hip_gguf_writer_set_f32": (I, [P, ctypes.c_char_p, F]),
+    "jllm_hip_gguf_writer_set_str": (I, [P, ctypes.c_char_p, ctypes.c_char_p]),
+    "jllm_hip_gguf_writer_add_tensor": (I, [P, ctypes.c_char_p, I, I, P, P, I64]),
+    "jllm_hip_gguf_writer_write": (I, [P, ctypes.c_char_p]),
     # decoder loop; the struct arguments are passed by address
     "jllm_hip_decoder_create": (P, [P, P, P, I]),
     "jllm_hip_decoder_destroy": (None, [P]),

@@ -322,6 +322,60 @@ int jllm_hip_decoder_generate(jllm_hip_decoder* d, const int32_t* prompt, int n_
  * dst (device memory). */
 int jllm_hip_decoder_copy_logits(const jllm_hip_decoder* d, float* dst, void* stream);
 
+/* ---- GGUF models ---- */
+
+/* Reader: maps a GGUF v2/v3 file read-only and parses its metadata and
+ * tensor table (every field bounds-checked; NULL and a message on stderr
+ * for a malformed file).  Replaces the reference loader's GGUF parsing,
+ * src/engine/model.cpp:150-345 (config) and :445-657 (tensor infos, mmap).
+ * Tensor data pointers are host pointers into the mapping, valid until
+ * jllm_hip_gguf_close. */
+typedef struct jllm_hip_gguf jllm_hip_gguf;
+jllm_hip_gguf* jllm_hip_gguf_open(const char* path);
+void           jllm_hip_gguf_close(jllm_hip_gguf* g);
+int64_t        jllm_hip_gguf_n_tensors(const jllm_hip_gguf* g);
+int64_t        jllm_hip_gguf_find_tensor(const jllm_hip_gguf* g, const char* name);
+int            jllm_hip_gguf_tensor(const jllm_hip_gguf* g, int64_t i, const char** name, int* ggml_type,
+                                    int* n_dims, int64_t* dims /* [4], dims[0] fastest */,
+                                    const void** data, int64_t* bytes);
+int            jllm_hip_gguf_get_u64(const jllm_hip_gguf* g, const char* key, uint64_t* out);
+int            jllm_hip_gguf_get_f64(const jllm_hip_gguf* g, const char* key, double* out);
+const char*    jllm_hip_gguf_get_str(const jllm_hip_gguf* g, const char* key);
+
+/* The decoder shape from the metadata (`<arch>.block_count`,
+ * `.embedding_length`, `.attention.head_count(_kv)`, `.attention.key_length`,
+ * `.feed_forward_length`, `.rope.freq_base`,
+ * `.attention.layer_norm_rms_epsilon`, vocab from token_embd.weight when
+ * `.vocab_size` is absent, neox RoPE for the Qwen/Gemma/Phi families; norm
+ * weight types from the blk.0 / output_norm tensors), as load_gguf_config
+ * does (model.cpp:150-345).  max_seq = `.context_length`; kv_int8 = 1. */
+int jllm_hip_gguf_config(const jllm_hip_gguf* g, jllm_hip_decoder_config* cfg);
+
+/* Uploads the decoder's tensors (token_embd, output_norm, output -- tied to
+ * token_embd when absent --, and per layer attn_q/k/v/output, ffn_gate/up/
+ * down, attn_norm, ffn_norm, attn_q_norm/k_norm) into one device allocation
+ * and fills the weight structs for jllm_hip_decoder_create, by the names of
+ * load_and_map_weights (model.cpp:657-810). */
+typedef struct jllm_hip_gguf_model jllm_hip_gguf_model;
+jllm_hip_gguf_model*          jllm_hip_gguf_model_load(const jllm_hip_gguf* g, const jllm_hip_decoder_config* cfg);
+const jllm_hip_model_weights* jllm_hip_gguf_model_weights(const jllm_hip_gguf_model* m);
+const jllm_hip_layer_weights* jllm_hip_gguf_layer_weights(const jllm_hip_gguf_model* m);
+void                          jllm_hip_gguf_model_free(jllm_hip_gguf_model* m);
+
+/* Writer (GGUF v3, alignment 32): scalar u32 / f32 / string metadata and
+ * tensors (copied at add time).  No reference counterpart in the runtime
+ * (the reference reads files made by llama.cpp tools); used to store models
+ * such as the benchmark's random Q4_K_M decoder. */
+typedef struct jllm_hip_gguf_writer jllm_hip_gguf_writer;
+jllm_hip_gguf_writer* jllm_hip_gguf_writer_create(void);
+void jllm_hip_gguf_writer_free(jllm_hip_gguf_writer* w);
+int  jllm_hip_gguf_writer_set_u32(jllm_hip_gguf_writer* w, const char* key, uint32_t value);
+int  jllm_hip_gguf_writer_set_f32(jllm_hip_gguf_writer* w, const char* key, float value);
+int  jllm_hip_gguf_writer_set_str(jllm_hip_gguf_writer* w, const char* key, const char* value);
+int  jllm_hip_gguf_writer_add_tensor(jllm_hip_gguf_writer* w, const char* name, int ggml_type, int n_dims,
+                                     const int64_t* dims, const void* data, int64_t bytes);
+int  jllm_hip_gguf_writer_write(const jllm_hip_gguf_writer* w, const char* path);
+
 #ifdef __cplusplus
 }
 #endif
