@@ -82,7 +82,7 @@ int check_common(const char* tag, int K, const uint16_t* x) {
 }
 
 int make_seg(const char* tag, GemvSeg& s, void* y, const void* W, int type, int M, const uint16_t* res) {
-    if (type != 12 && type != 14) {
+    if (type != 12 && type != 13 && type != 14) {
         fprintf(stderr, "[%s] FATAL: unsupported GPU GGML type %d (M=%d)\n", tag, type, M);
         return JLLM_ERR_UNSUPPORTED;
     }
@@ -114,6 +114,17 @@ int set_rms(const char* tag, GemvArgs& a, const void* nw, int fp32, float eps) {
     return JLLM_OK;
 }
 
+// MMVQ (q8_1 activation) or float dequant, by the reference dispatchers'
+// routes: single rows by type (gemv_q4.cu:1263-1290: Q4_K and Q6_K MMVQ,
+// Q5_K float), pairs only for Q4_K+Q4_K (:1391), triples for the four
+// instantiated combinations of Q4_K/Q6_K (:1475-1490); anything else float.
+bool mmvq_single(int t) { return t != 13; }
+bool mmvq_pair(int t0, int t1) { return t0 == 12 && t1 == 12; }
+bool mmvq_triple(int t0, int t1, int t2) {
+    return (t0 == 12 && t1 == 12 && (t2 == 12 || t2 == 14)) || (t0 == 14 && t1 == 14 && t2 == 14) ||
+           (t0 == 14 && t1 == 12 && t2 == 12);
+}
+
 int run(const char* tag, GemvArgs& a, bool mmvq, int out, void* stream) {
     return launch_status(gemv_launch(a, mmvq, out, (hipStream_t)stream), tag);
 }
@@ -126,7 +137,7 @@ int jllm_hip_gemv_quant(uint16_t* y, const void* W, int type, const uint16_t* x,
     int st = check_common("GEMV", K, x); if (st) return st;
     GemvArgs a{}; a.nseg = 1; a.K = K; a.x = x;
     if ((st = make_seg("GEMV", a.seg[0], y, W, type, M, nullptr))) return st;
-    return run("GEMV", a, true, OUT_HALF, stream);
+    return run("GEMV", a, mmvq_single(type), OUT_HALF, stream);
 }
 
 int jllm_hip_gemv_quant_f32(float* y, const void* W, int type, const uint16_t* x, int M, int K, void* stream) {
@@ -159,7 +170,7 @@ int jllm_hip_gemv_quant_pair(uint16_t* y0, const void* W0, int t0, int M0,
     GemvArgs a{}; a.nseg = 2; a.K = K; a.x = x;
     if ((st = make_seg("GEMV", a.seg[0], y0, W0, t0, M0, nullptr))) return st;
     if ((st = make_seg("GEMV", a.seg[1], y1, W1, t1, M1, nullptr))) return st;
-    return run("GEMV", a, t0 == 12 && t1 == 12, OUT_HALF, stream);
+    return run("GEMV", a, mmvq_pair(t0, t1), OUT_HALF, stream);
 }
 
 int jllm_hip_gemv_quant_triple(uint16_t* y0, const void* W0, int t0, int M0,
@@ -171,7 +182,7 @@ int jllm_hip_gemv_quant_triple(uint16_t* y0, const void* W0, int t0, int M0,
     if ((st = make_seg("GEMV", a.seg[0], y0, W0, t0, M0, nullptr))) return st;
     if ((st = make_seg("GEMV", a.seg[1], y1, W1, t1, M1, nullptr))) return st;
     if ((st = make_seg("GEMV", a.seg[2], y2, W2, t2, M2, nullptr))) return st;
-    return run("GEMV", a, true, OUT_HALF, stream);
+    return run("GEMV", a, mmvq_triple(t0, t1, t2), OUT_HALF, stream);
 }
 
 int jllm_hip_gemv_quant_triple_rmsnorm(uint16_t* y0, const void* W0, int t0, int M0,
@@ -185,7 +196,7 @@ int jllm_hip_gemv_quant_triple_rmsnorm(uint16_t* y0, const void* W0, int t0, int
     if ((st = make_seg("GEMV", a.seg[0], y0, W0, t0, M0, nullptr))) return st;
     if ((st = make_seg("GEMV", a.seg[1], y1, W1, t1, M1, nullptr))) return st;
     if ((st = make_seg("GEMV", a.seg[2], y2, W2, t2, M2, nullptr))) return st;
-    return run("GEMV", a, true, OUT_HALF, stream);
+    return run("GEMV", a, mmvq_triple(t0, t1, t2), OUT_HALF, stream);
 }
 
 int jllm_hip_gemv_quant_pair_rmsnorm(uint16_t* y0, const void* W0, int t0, int M0,
@@ -197,7 +208,7 @@ int jllm_hip_gemv_quant_pair_rmsnorm(uint16_t* y0, const void* W0, int t0, int M
     if ((st = set_rms("GEMV", a, norm_weight, weight_fp32, eps))) return st;
     if ((st = make_seg("GEMV", a.seg[0], y0, W0, t0, M0, nullptr))) return st;
     if ((st = make_seg("GEMV", a.seg[1], y1, W1, t1, M1, nullptr))) return st;
-    return run("GEMV", a, t0 == 12 && t1 == 12, OUT_HALF, stream);
+    return run("GEMV", a, mmvq_pair(t0, t1), OUT_HALF, stream);
 }
 
 int jllm_hip_gemv_quant_f32_rmsnorm(float* y, const void* W, int type, const uint16_t* x, const void* norm_weight,

@@ -96,7 +96,7 @@ int jllm_hip_qk_norm_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v, 
 
 int jllm_hip_dequant_embedding_rows(uint16_t* dst, const void* W, int ggml_type, const int32_t* tokens, int N,
                                     int hidden_dim, int vocab, void* stream) {
-    if (ggml_type != 12 && ggml_type != 14) return JLLM_ERR_UNSUPPORTED;
+    if (ggml_type < 12 || ggml_type > 14) return JLLM_ERR_UNSUPPORTED;
     if (N < 0 || vocab <= 0 || hidden_dim <= 0 || hidden_dim % 256 != 0) return JLLM_ERR_INVALID;
     if (N == 0) return JLLM_OK;
     if (!dst || !tokens || ((uintptr_t)dst & 15u)) return JLLM_ERR_INVALID;

@@ -1,6 +1,7 @@
 // capi_mmq.hip -- C ABI for the batched (prefill) GEMM: activation
 // quantiser, int8 MFMA MMQ, and the routing of gemm_quant_batched
-// (gemv_q4.cu:2478-2517).
+// (gemv_q4.cu:2478-2517): Q4_K / Q6_K through the MMQ, Q5_K through its
+// fp16 GEMM (the reference runs Q5_K in float, gemv_q4.cu:2436-2440).
 #include "capi_common.h"
 #include "mmq.h"
 
@@ -11,8 +12,8 @@ DeviceScratch g_q8;     // quantised activations (fp16 codes + scale words), gro
 
 int npad_of(int N) { return ((N + MMQ_TILE_N - 1) / MMQ_TILE_N) * MMQ_TILE_N; }
 
-int check_gemm(const char* tag, const void* y, int type, const uint16_t* x, int M, int N, int K) {
-    if (type != 12 && type != 14) {
+int check_gemm(const char* tag, const void* y, int type, const uint16_t* x, int M, int N, int K, bool q5 = false) {
+    if (type != 12 && type != 14 && !(q5 && type == 13)) {
         fprintf(stderr, "[%s] FATAL: unsupported GPU GGML type %d\n", tag, type);
         return JLLM_ERR_UNSUPPORTED;
     }
@@ -36,6 +37,7 @@ int run_mmq(const char* tag, void* y, const void* W, int type, const uint16_t* x
     }
     if (!aligned16(Wd)) return JLLM_ERR_INVALID;
     const int Npad = npad_of(N);
+    if (type == 13) return launch_status(gemm_q5k_launch(y, (const uint8_t*)Wd, x, M, N, K, out_kind, (hipStream_t)stream), tag);
     const size_t cb = mmq_codes_bytes(K, Npad);
     uint8_t* q8 = (uint8_t*)g_q8.get(cb + mmq_scales_bytes(K, Npad));
     if (!q8) {
@@ -55,7 +57,7 @@ extern "C" {
 
 int jllm_hip_gemm_quant_batched(uint16_t* y, const void* W, int type, const uint16_t* x,
                                 int M, int N, int K, void* stream) {
-    int st = check_gemm("GEMM", y, type, x, M, N, K); if (st) return st;
+    int st = check_gemm("GEMM", y, type, x, M, N, K, true); if (st) return st;
     if (M == 0 || N == 0) return JLLM_OK;
     if (N == 1) return jllm_hip_gemv_quant(y, W, type, x, M, K, stream);
     return run_mmq("GEMM", y, W, type, x, M, N, K, 0, stream);
@@ -63,7 +65,7 @@ int jllm_hip_gemm_quant_batched(uint16_t* y, const void* W, int type, const uint
 
 int jllm_hip_gemm_quant_batched_f32(float* y, const void* W, int type, const uint16_t* x,
                                     int M, int N, int K, void* stream) {
-    int st = check_gemm("GEMM", y, type, x, M, N, K); if (st) return st;
+    int st = check_gemm("GEMM", y, type, x, M, N, K, true); if (st) return st;
     if (M == 0 || N == 0) return JLLM_OK;
     return run_mmq("GEMM", y, W, type, x, M, N, K, 1, stream);
 }

@@ -48,7 +48,7 @@ struct jllm_hip_decoder {
 
 namespace {
 
-bool valid_type(int t) { return t == 12 || t == 14; }
+bool valid_type(int t) { return t >= 12 && t <= 14; }   // Q4_K, Q5_K, Q6_K
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
@@ -151,7 +151,7 @@ jllm_hip_decoder* jllm_hip_decoder_create(const jllm_hip_decoder_config* cfg, co
     }
     if (!valid_type(mw->embd_type) || !valid_type(mw->output_type) || !mw->tok_embd || !mw->output ||
         !mw->output_norm) {
-        fprintf(stderr, "[decoder] embedding / output weights missing or not Q4_K/Q6_K\n");
+        fprintf(stderr, "[decoder] embedding / output weights missing or not Q4_K/Q5_K/Q6_K\n");
         return nullptr;
     }
     for (int l = 0; l < c.n_layers; l++) {
@@ -159,7 +159,7 @@ jllm_hip_decoder* jllm_hip_decoder_create(const jllm_hip_decoder_config* cfg, co
         if (!valid_type(w.type_wq) || !valid_type(w.type_wk) || !valid_type(w.type_wv) || !valid_type(w.type_wo) ||
             !valid_type(w.type_w_gate) || !valid_type(w.type_w_up) || !valid_type(w.type_w_down) || !w.rms_attn ||
             !w.rms_ffn) {
-            fprintf(stderr, "[decoder] layer %d: weights missing or not Q4_K/Q6_K\n", l);
+            fprintf(stderr, "[decoder] layer %d: weights missing or not Q4_K/Q5_K/Q6_K\n", l);
             return nullptr;
         }
     }

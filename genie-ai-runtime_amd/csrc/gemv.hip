@@ -1,4 +1,4 @@
-// gemv.hip -- Q4_K / Q6_K decode GEMV for gfx950 (wave64).
+// gemv.hip -- Q4_K / Q5_K / Q6_K decode GEMV for gfx950 (wave64).
 //
 // Two arithmetic modes, matching the reference dispatcher's defaults
 // (gemv_q4.cu:1245-1616):
@@ -7,7 +7,8 @@
 //     weight codes, one exact int32 per 32-weight Q4_K sub-block or per
 //     16-weight Q6_K group, then scaled in fp32 (gemv_q4.cu:474-618).
 //   * float dequant: weights dequantised in registers and dotted with the
-//     fp16 activation in fp32 (gemv_q4.cu:266-398).
+//     fp16 activation in fp32 (gemv_q4.cu:266-398).  The only mode of Q5_K,
+//     as in the reference (gemv_q4.cu:318-363).
 //
 // Layout of the work (streaming kernel below): the rows of a launch are
 // split between waves; each wave streams its rows' bytes (contiguous in
@@ -93,11 +94,14 @@ __device__ __forceinline__ int xpad(int k) { return k + ((k >> 7) << 3); }
 //   Q4_K: qs bytes [32q, 32q+32): low nibbles = sub-block 2q, high = 2q+1.
 //   Q6_K: half h = q/2 of the block, positions l0..l0+15 (l0 = 16*(q&1)) of
 //         each 32-wide quarter g = 0..3: elements h*128 + 32g + l0 + [0,16).
-// One register layout for both types (Q4_K uses a = header, b/c = qs).
+//   Q5_K: as Q4_K (qs bytes [32q, 32q+32)), plus all 32 qh bytes, of which
+//         the lane uses bits 2q (low nibbles) and 2q+1 (high nibbles).
+// One register layout for all types (Q4_K / Q5_K use a = header, b/c = qs,
+// Q5_K h0/h1 = qh).
 // Q6_K blocks are only 2-byte aligned: their pieces are read dword-aligned
 // from up to 2 bytes early (sh = 16 when so) and realigned with a funnel
 // shift.
-struct Raw { u32x4 a, b, c; uint32_t a4, b4, c4; u32x2 sc; uint32_t sc2, d, sh; };
+struct Raw { u32x4 a, b, c; uint32_t a4, b4, c4; u32x2 sc; uint32_t sc2, d, sh; u32x4 h0, h1; };
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
 
@@ -269,6 +273,40 @@ __device__ __forceinline__ float f16_block<TYPE_Q4_K>(const Raw& r, int b, int q
     return dall * a - dmin * mm;
 }
 
+// float dequant Q5_K: as Q4_K with 5-bit codes (nibble | qh bit << 4) built
+// as bytes, then dotted with x as subnormal halves.
+template <>
+__device__ __forceinline__ float f16_block<TYPE_Q5_K>(const Raw& r, int b, int q, const Q4Consts& c, const uint8_t* lds, int K) {
+    const uint16_t* s_x = (const uint16_t*)lds;
+    const float* s_x32 = (const float*)(lds + 2 * K + K / 8);
+    const int k0 = xpad(b * 256 + 64 * q);
+    const uint32_t w[8] = {r.b.x, r.b.y, r.b.z, r.b.w, r.c.x, r.c.y, r.c.z, r.c.w};
+    const uint32_t hq[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+    const uint32_t s0 = 2u * (uint32_t)q;
+    float sl = 0.0f, sh = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+        const u32x4 xa = *(const u32x4*)(s_x + k0 + 4 * i);        // x[k0+4i .. +8)
+        const u32x4 xb = *(const u32x4*)(s_x + k0 + 32 + 4 * i);   // high-nibble partners
+        const uint32_t lo0 = (w[i] & 0x0F0F0F0Fu) | (((hq[i] >> s0) & 0x01010101u) << 4);
+        const uint32_t lo1 = (w[i + 1] & 0x0F0F0F0Fu) | (((hq[i + 1] >> s0) & 0x01010101u) << 4);
+        const uint32_t hi0 = ((w[i] >> 4) & 0x0F0F0F0Fu) | (((hq[i] >> (s0 + 1)) & 0x01010101u) << 4);
+        const uint32_t hi1 = ((w[i + 1] >> 4) & 0x0F0F0F0Fu) | (((hq[i + 1] >> (s0 + 1)) & 0x01010101u) << 4);
+        sl = fdot2(pair01(lo0), xa.x, sl); sl = fdot2(pair23(lo0), xa.y, sl);
+        sl = fdot2(pair01(lo1), xa.z, sl); sl = fdot2(pair23(lo1), xa.w, sl);
+        sh = fdot2(pair01(hi0), xb.x, sh); sh = fdot2(pair23(hi0), xb.y, sh);
+        sh = fdot2(pair01(hi1), xb.z, sh); sh = fdot2(pair23(hi1), xb.w, sh);
+    }
+    uint32_t sc0, m0, sc1, m1;
+    q4_scales(c, r.a, 0, sc0, m0);
+    q4_scales(c, r.a, 1, sc1, m1);
+    const f32x2 xs = *(const f32x2*)(s_x32 + b * 8 + 2 * q);
+    const float dall = f16_bits_to_f32(r.a.x & 0xFFFFu), dmin = f16_bits_to_f32(r.a.x >> 16);
+    const float a = ((float)sc0 * sl + (float)sc1 * sh) * 16777216.0f;
+    const float mm = (float)m0 * xs.x + (float)m1 * xs.y;
+    return dall * a - dmin * mm;
+}
+
 // float dequant Q6_K: per 16-weight group sum((code-32)*x) = sum(code*x) - 32*sum(x)
 // with sum(code*x) from fp16 dot products of the codes as subnormal halves.
 template <>
@@ -311,7 +349,9 @@ __device__ __forceinline__ void store_row(const GemvSeg& s, int r, float acc, co
 
 template <bool MMVQ, int TYPE>
 __device__ __forceinline__ float block_dot(const Raw& r, int b, int q, const Q4Consts& c, const uint8_t* lds, int K) {
-    return MMVQ ? mmvq_block<TYPE>(r, b, q, c, lds, K) : f16_block<TYPE>(r, b, q, c, lds, K);
+    static_assert(!(MMVQ && TYPE == TYPE_Q5_K), "Q5_K has no MMVQ mode");
+    if constexpr (MMVQ) return mmvq_block<TYPE>(r, b, q, c, lds, K);
+    else return f16_block<TYPE>(r, b, q, c, lds, K);
 }
 
 // ---- streaming kernel ----------------------------------------------------
@@ -446,11 +486,16 @@ struct RoundDesc {
     int slot0;             // slot of the first block
 };
 
+template <int TYPE>
+constexpr int block_bytes() { return TYPE == TYPE_Q4_K ? Q4K_BYTES : (TYPE == TYPE_Q5_K ? Q5K_BYTES : Q6K_BYTES); }
+
 template <int TYPE, int L>
 struct WGeom {
-    static constexpr int BB = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    static constexpr int BB = block_bytes<TYPE>();
     static constexpr int BYTES = 64 * 16 * L;                                  // one wave's round
-    static constexpr int NBLK = TYPE == TYPE_Q4_K ? BYTES / BB : (BYTES - 14) / BB;
+    // Q4_K / Q5_K blocks are 16-byte multiples (rounds start aligned); a Q6_K
+    // round may start up to 14 bytes into its first 16-byte chunk
+    static constexpr int NBLK = TYPE == TYPE_Q6_K ? (BYTES - 14) / BB : BYTES / BB;
 };
 
 template <int TYPE, int L>
@@ -499,6 +544,13 @@ __device__ __forceinline__ void load_raw_lds(const uint8_t* buf, int off, int q,
         r.a = *(const u32x4*)blk;
         r.b = *(const u32x4*)(blk + 16 + 32 * q);
         r.c = *(const u32x4*)(blk + 32 + 32 * q);
+    } else if (TYPE == TYPE_Q5_K) {
+        const uint8_t* blk = buf + off;          // 16-byte aligned
+        r.a = *(const u32x4*)blk;
+        r.h0 = *(const u32x4*)(blk + 16);
+        r.h1 = *(const u32x4*)(blk + 32);
+        r.b = *(const u32x4*)(blk + 48 + 32 * q);
+        r.c = *(const u32x4*)(blk + 64 + 32 * q);
     } else {
         const int h = q >> 1, l0 = 16 * (q & 1);
         r.sh = (uint32_t)(off & 2) * 8u;
@@ -526,7 +578,7 @@ __device__ __forceinline__ float quad_sum(float v) {
 template <bool MMVQ, int TYPE>
 __device__ __forceinline__ void compute_round(const RoundDesc& d, const uint8_t* buf, const uint8_t* xlds,
                                               float* slots, int K, int nb, int lane) {
-    constexpr int BB = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    constexpr int BB = block_bytes<TYPE>();
     const int quad = lane >> 2, q = lane & 3;
     const Q4Consts c = q4_consts(q);
     int col = d.col0 + quad;
@@ -746,7 +798,8 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
 template <class T>
 __device__ __forceinline__ void pin_sgpr(const T& v) { asm volatile("" :: "s"(v)); }
 
-template <bool MMVQ, int OUT, int L, int NX, int PRE>
+// TA: the type of the first row class (Q4_K or Q5_K); the second is Q6_K.
+template <bool MMVQ, int OUT, int L, int NX, int PRE, int TA>
 __global__ __launch_bounds__(ST_T) __attribute__((amdgpu_waves_per_eu(4)))
 void gemv_stream_kernel(StreamArgs a_in) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -774,25 +827,41 @@ void gemv_stream_kernel(StreamArgs a_in) {
     }
     uint16_t* res_lds = (uint16_t*)(lds + a.xlds_bytes + ST_W * (64 * 16 * L) + ST_W * 4 * a.slots_per_wave);
     // (both bodies hold the same two workgroup barriers)
-    if (q4) wave_body<MMVQ, OUT, TYPE_Q4_K, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
+    if (q4) wave_body<MMVQ, OUT, TA, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
     else    wave_body<MMVQ, OUT, TYPE_Q6_K, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
 }
 
-template <bool MMVQ, int OUT, int L, int NX, int PRE>
+template <bool MMVQ, int OUT, int L, int NX, int PRE, int TA>
 static hipError_t launch_s(const StreamArgs& a, int grid, size_t lds, hipStream_t st) {
-    static const hipError_t attr = hipFuncSetAttribute((const void*)gemv_stream_kernel<MMVQ, OUT, L, NX, PRE>,
+    static const hipError_t attr = hipFuncSetAttribute((const void*)gemv_stream_kernel<MMVQ, OUT, L, NX, PRE, TA>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((gemv_stream_kernel<MMVQ, OUT, L, NX, PRE>), dim3(grid), dim3(ST_T), lds, st, a);
+    hipLaunchKernelGGL((gemv_stream_kernel<MMVQ, OUT, L, NX, PRE, TA>), dim3(grid), dim3(ST_T), lds, st, a);
     return hipGetLastError();
 }
 
-template <bool MMVQ, int OUT, int L, int PRE = PRE_NONE>
-static hipError_t launch_nx(const StreamArgs& a, int grid, size_t lds, hipStream_t st) {
+template <bool MMVQ, int OUT, int L, int PRE, int TA>
+static hipError_t launch_nx_t(const StreamArgs& a, int grid, size_t lds, hipStream_t st) {
     const int nch = a.K / 8;
-    if (nch <= ST_T) return launch_s<MMVQ, OUT, L, 1, PRE>(a, grid, lds, st);
-    if (PRE == PRE_RMS || nch <= 2 * ST_T) return launch_s<MMVQ, OUT, L, 2, PRE>(a, grid, lds, st);
-    return launch_s<MMVQ, OUT, L, 5, PRE>(a, grid, lds, st);
+    if (nch <= ST_T) return launch_s<MMVQ, OUT, L, 1, PRE, TA>(a, grid, lds, st);
+    if constexpr (PRE == PRE_RMS) {
+        return launch_s<MMVQ, OUT, L, 2, PRE, TA>(a, grid, lds, st);
+    } else {
+        if (nch <= 2 * ST_T) return launch_s<MMVQ, OUT, L, 2, PRE, TA>(a, grid, lds, st);
+        return launch_s<MMVQ, OUT, L, 5, PRE, TA>(a, grid, lds, st);
+    }
+}
+
+// Q5_K rows exist only in float mode
+template <bool MMVQ, int OUT, int L, int PRE = PRE_NONE>
+static hipError_t launch_nx(const StreamArgs& a, int grid, size_t lds, hipStream_t st, bool q5) {
+    if constexpr (MMVQ) {
+        if (q5) return hipErrorInvalidValue;
+        return launch_nx_t<true, OUT, L, PRE, TYPE_Q4_K>(a, grid, lds, st);
+    } else {
+        if (q5) return launch_nx_t<false, OUT, L, PRE, TYPE_Q5_K>(a, grid, lds, st);
+        return launch_nx_t<false, OUT, L, PRE, TYPE_Q4_K>(a, grid, lds, st);
+    }
 }
 
 static constexpr size_t LDS_CU = 160 * 1024;
@@ -803,22 +872,41 @@ constexpr int ST_L = 4;
 
 hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t st) {
     if (out_kind == OUT_ADD && in.nseg != 1) return hipErrorInvalidValue;
+    bool has4 = false, has5 = false;
+    for (int i = 0; i < in.nseg; i++) {
+        has4 |= in.seg[i].type == TYPE_Q4_K && in.seg[i].M > 0;
+        has5 |= in.seg[i].type == TYPE_Q5_K && in.seg[i].M > 0;
+    }
+    if (has5 && mmvq) return hipErrorInvalidValue;
+    if (has4 && has5) {
+        // one launch per first-class type: the Q5_K (and Q6_K) rows, then the Q4_K rows
+        GemvArgs p = in, r = in;
+        p.nseg = r.nseg = 0;
+        for (int i = 0; i < in.nseg; i++) {
+            if (in.seg[i].type == TYPE_Q4_K) r.seg[r.nseg++] = in.seg[i];
+            else p.seg[p.nseg++] = in.seg[i];
+        }
+        const hipError_t e = gemv_launch(p, mmvq, out_kind, st);
+        return e != hipSuccess ? e : gemv_launch(r, mmvq, out_kind, st);
+    }
+    const int ta = has5 ? TYPE_Q5_K : TYPE_Q4_K;
     StreamArgs a;
     a.K = in.K;
     a.x = in.x;
     a.nb = in.K / QK_K;
-    // Q4_K segments first, then Q6_K (stable); unused slots are empty
+    // first-class (Q4_K or Q5_K) segments first, then Q6_K (stable); unused slots are empty
     int n = 0;
-    for (int i = 0; i < in.nseg; i++) if (in.seg[i].type == TYPE_Q4_K) a.seg[n++] = in.seg[i];
+    for (int i = 0; i < in.nseg; i++) if (in.seg[i].type == ta) a.seg[n++] = in.seg[i];
     const int nseg4 = n;
-    for (int i = 0; i < in.nseg; i++) if (in.seg[i].type != TYPE_Q4_K) a.seg[n++] = in.seg[i];
+    for (int i = 0; i < in.nseg; i++) if (in.seg[i].type == TYPE_Q6_K) a.seg[n++] = in.seg[i];
+    if (n == 0) return hipSuccess;
     for (int i = n; i < 3; i++) { a.seg[i] = a.seg[n - 1]; a.seg[i].M = 0; }
     a.row_off[0] = 0;
     for (int i = 0; i < 3; i++) a.row_off[i + 1] = a.row_off[i] + a.seg[i].M;
     const int64_t rows4 = a.row_off[nseg4], rows6 = a.row_off[3] - rows4;
     if (rows4 + rows6 <= 0) return hipSuccess;
     a.row_split = (int)rows4;
-    const int64_t bytes4 = rows4 * a.nb * Q4K_BYTES, bytes6 = rows6 * a.nb * Q6K_BYTES;
+    const int64_t bytes4 = rows4 * a.nb * (has5 ? Q5K_BYTES : Q4K_BYTES), bytes6 = rows6 * a.nb * Q6K_BYTES;
     a.xlds_bytes = (int)((gemv_lds_bytes(mmvq, a.K) + 15) & ~(size_t)15);
     const size_t wbuf = ST_W * (size_t)(64 * 16 * ST_L);
     // waves: ST_W per workgroup, JLLM_GEMV_WG_PER_CU workgroups per CU when
@@ -864,20 +952,20 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     a.pre = in.pre;
     if (in.pre.kind == PRE_RMS) {      // the sum of squares needs the whole x in the first staging pass
         if (a.K > 2 * ST_T * 8) return hipErrorInvalidValue;
-        if (mmvq && out_kind == OUT_HALF) return launch_nx<true, OUT_HALF, ST_L, PRE_RMS>(a, g, lds, st);
-        if (mmvq && out_kind == OUT_F32)  return launch_nx<true, OUT_F32, ST_L, PRE_RMS>(a, g, lds, st);
-        if (!mmvq && out_kind == OUT_F32) return launch_nx<false, OUT_F32, ST_L, PRE_RMS>(a, g, lds, st);
-        if (!mmvq && out_kind == OUT_HALF) return launch_nx<false, OUT_HALF, ST_L, PRE_RMS>(a, g, lds, st);
+        if (mmvq && out_kind == OUT_HALF) return launch_nx<true, OUT_HALF, ST_L, PRE_RMS>(a, g, lds, st, has5);
+        if (mmvq && out_kind == OUT_F32)  return launch_nx<true, OUT_F32, ST_L, PRE_RMS>(a, g, lds, st, has5);
+        if (!mmvq && out_kind == OUT_F32) return launch_nx<false, OUT_F32, ST_L, PRE_RMS>(a, g, lds, st, has5);
+        if (!mmvq && out_kind == OUT_HALF) return launch_nx<false, OUT_HALF, ST_L, PRE_RMS>(a, g, lds, st, has5);
         return hipErrorInvalidValue;
     }
     if (mmvq) {
-        if (out_kind == OUT_HALF) return launch_nx<true, OUT_HALF, ST_L>(a, g, lds, st);
-        if (out_kind == OUT_F32)  return launch_nx<true, OUT_F32, ST_L>(a, g, lds, st);
-        return launch_nx<true, OUT_ADD, ST_L>(a, g, lds, st);
+        if (out_kind == OUT_HALF) return launch_nx<true, OUT_HALF, ST_L>(a, g, lds, st, has5);
+        if (out_kind == OUT_F32)  return launch_nx<true, OUT_F32, ST_L>(a, g, lds, st, has5);
+        return launch_nx<true, OUT_ADD, ST_L>(a, g, lds, st, has5);
     }
-    if (out_kind == OUT_HALF) return launch_nx<false, OUT_HALF, ST_L>(a, g, lds, st);
-    if (out_kind == OUT_F32)  return launch_nx<false, OUT_F32, ST_L>(a, g, lds, st);
-    return launch_nx<false, OUT_ADD, ST_L>(a, g, lds, st);
+    if (out_kind == OUT_HALF) return launch_nx<false, OUT_HALF, ST_L>(a, g, lds, st, has5);
+    if (out_kind == OUT_F32)  return launch_nx<false, OUT_F32, ST_L>(a, g, lds, st, has5);
+    return launch_nx<false, OUT_ADD, ST_L>(a, g, lds, st, has5);
 }
 
 hipError_t quantize_q8_1_aos_launch(const uint16_t* x, void* y, int K, hipStream_t st) {

@@ -9,7 +9,9 @@ namespace jllm_hip {
 constexpr int QK_K = 256;
 constexpr int Q4K_BYTES = 144;   // u16 d, u16 dmin, u8 scales[12], u8 qs[128]
 constexpr int Q6K_BYTES = 210;   // u8 ql[128], u8 qh[64], i8 scales[16], u16 d
+constexpr int Q5K_BYTES = 176;   // u16 d, u16 dmin, u8 scales[12], u8 qh[32], u8 qs[128]
 constexpr int TYPE_Q4_K = 12;
+constexpr int TYPE_Q5_K = 13;
 constexpr int TYPE_Q6_K = 14;
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));

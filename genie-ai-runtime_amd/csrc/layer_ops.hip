@@ -356,6 +356,22 @@ __global__ __launch_bounds__(256) void embed_kernel(uint16_t* __restrict__ dst, 
             const int qv = l64 < 32 ? (qs[e] & 0xF) : (qs[e] >> 4);
             val[e] = dall * (float)sc * (float)qv - dmin * (float)mn;
         }
+    } else if (TYPE == 13) {      // the engine's host Q5_K row dequant, decode.cu:230-266
+        const uint8_t* blk = W + ((int64_t)tok * nb + b) * 176;
+        const float dall = f16_bits_to_f32(blk[0] | (blk[1] << 8));
+        const float dmin = f16_bits_to_f32(blk[2] | (blk[3] << 8));
+        const int il = i >> 6, l64 = i & 63, l32 = l64 & 31, hi = l64 >= 32;
+        int sc, mn;
+        q4k_sc_min(blk + 4, 2 * il + hi, sc, mn);
+        const float d1 = dall * (float)sc, dm1 = dmin * (float)mn;
+        const uint8_t* qs = blk + 48 + 32 * il + l32;
+        const uint8_t* qh = blk + 16 + l32;
+        const int ub = 2 * il + hi;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int qv = (hi ? (qs[e] >> 4) : (qs[e] & 0xF)) + (((qh[e] >> ub) & 1) ? 16 : 0);
+            val[e] = d1 * (float)qv - dm1;
+        }
     } else {
         const uint8_t* blk = W + ((int64_t)tok * nb + b) * 210;
         const float d = f16_bits_to_f32(blk[208] | (blk[209] << 8));
@@ -385,6 +401,7 @@ hipError_t embed_launch(uint16_t* dst, const void* W, int type, const int32_t* t
     if (groups <= 0) return hipSuccess;
     const dim3 g((unsigned)((groups + 7) / 8));
     if (type == 12) hipLaunchKernelGGL((embed_kernel<12>), g, dim3(256), 0, st, dst, (const uint8_t*)W, tokens, token0, N, nb, vocab);
+    else if (type == 13) hipLaunchKernelGGL((embed_kernel<13>), g, dim3(256), 0, st, dst, (const uint8_t*)W, tokens, token0, N, nb, vocab);
     else hipLaunchKernelGGL((embed_kernel<14>), g, dim3(256), 0, st, dst, (const uint8_t*)W, tokens, token0, N, nb, vocab);
     return hipGetLastError();
 }

@@ -26,4 +26,9 @@ inline size_t mmq_scales_bytes(int K, int Npad) { return (size_t)(K / 32) * Npad
 hipError_t mmq_launch(void* y, const uint8_t* W, int type, const uint16_t* codes, const uint32_t* scl, int M, int N,
                       int K, int Npad, int out_kind, hipStream_t st);
 
+// Q5_K batched GEMM (fp16 activation, no quantisation): out_kind 0 = fp16
+// y[N x M], 1 = fp32 y[N x M]
+hipError_t gemm_q5k_launch(void* y, const uint8_t* W, const uint16_t* x, int M, int N, int K, int out_kind,
+                           hipStream_t st);
+
 }  // namespace jllm_hip

@@ -72,31 +72,55 @@ def q4km_types(shape, layer):
     return t
 
 
+def q5km_types(shape, layer):
+    """A Q5_K_M-style layout: Q5_K everywhere, Q6_K for attn_v and ffn_down
+    on every other layer."""
+    t = {m: 13 for m in MATS}
+    if layer % 2 == 0:
+        t["wv"] = t["w_down"] = 14
+    return t
+
+
+PRESETS = {"q4km": q4km_types, "q5km": q5km_types}
+
+
 # Block scales chosen so the dequantised weights have mean ~0 and a
 # standard deviation of about 0.02 (a transformer's usual init): Q4_K
 # w = d*sc*q - dmin*m with sc, m ~ U[0,63], q ~ U[0,15], so dmin = 7.5 d
 # centres it; Q6_K w = d*sc*(q-32) with sc ~ U[-32,31] is centred already.
+# Q5_K (q ~ U[0,31]) the same with dmin = 15.5 d.
 Q4_D, Q4_DMIN, Q6_D = 1e-4, 7.5e-4, 6e-5
+Q5_D, Q5_DMIN = 5e-5, 7.75e-4
 
 
-def synth_np(shape, seed):
-    """Numpy model (host bytes) for shapes small enough to keep on the host."""
+def _synth_mat(synth, g, t, M, K):
+    if t == 12:
+        return synth.q4k(g, M, K, Q4_D, Q4_DMIN)
+    if t == 13:
+        return synth.q5k(g, M, K, Q5_D, Q5_DMIN)
+    return synth.q6k(g, M, K, Q6_D)
+
+
+def synth_np(shape, seed, preset="q4km"):
+    """Numpy model (host bytes) for shapes small enough to keep on the host.
+    preset q4km: Q4_K embedding; q5km: Q5_K embedding; Q6_K output in both."""
     import synth
     g = synth.rng(seed)
     layers = []
     for l in range(shape.n_layers):
-        types = q4km_types(shape, l)
+        types = PRESETS[preset](shape, l)
         L = {"types": types}
         for m in MATS:
             M, K = shape.mat_shape(m)
-            L[m] = synth.q4k(g, M, K, Q4_D, Q4_DMIN) if types[m] == 12 else synth.q6k(g, M, K, Q6_D)
+            L[m] = _synth_mat(synth, g, types[m], M, K)
         for n, dim in (("rms_attn", shape.hidden_dim), ("rms_ffn", shape.hidden_dim),
                        ("q_norm", shape.head_dim), ("k_norm", shape.head_dim)):
             L[n] = (1.0 + 0.02 * g.standard_normal(dim)).astype(np.float32)
         layers.append(L)
-    emb = synth.q4k(g, shape.vocab_size, shape.hidden_dim, Q4_D, Q4_DMIN)
+    et = 13 if preset == "q5km" else 12
+    emb = _synth_mat(synth, g, et, shape.vocab_size, shape.hidden_dim)
     out = synth.q6k(g, shape.vocab_size, shape.hidden_dim, Q6_D)
-    return {"layers": layers, "tok_embd": emb, "embd_type": 12, "output": out, "output_type": 14,
+    return {"layers": layers, "tok_embd": emb, "embd_type": et, "output": out, "output_type": 14,
             "output_norm": (1.0 + 0.02 * g.standard_normal(shape.hidden_dim)).astype(np.float32)}
 
 

@@ -4,6 +4,8 @@ Weights are raw GGUF K-quant blocks (uint8 arrays, rows contiguous):
   Q4_K (144 B / 256 weights): d, dmin = fp16(|N(0, 0.02)|); 12 random scale
       bytes (all 16 six-bit scale/min fields uniform in [0, 63]); 128 random
       qs bytes (nibbles uniform in [0, 15]).
+  Q5_K (176 B / 256 weights): Q4_K header (d, dmin, scales) as above, 32
+      random qh bytes (fifth code bits) and 128 random qs bytes.
   Q6_K (210 B / 256 weights): random ql/qh bytes (codes uniform in [0, 63]);
       int8 sub-block scales uniform in [-32, 31]; d = fp16(|N(0, 0.01)|).
 Activations: fp32 N(0, 1) rounded to fp16 (RNE), returned as uint16 bits.
@@ -11,7 +13,7 @@ Activations: fp32 N(0, 1) rounded to fp16 (RNE), returned as uint16 bits.
 import numpy as np
 
 QK_K = 256
-BLOCK_BYTES = {12: 144, 14: 210}
+BLOCK_BYTES = {12: 144, 13: 176, 14: 210}
 
 
 def rng(seed):
@@ -32,6 +34,16 @@ def q4k(g, rows, K, d_sigma=0.02, dmin_sigma=0.02):
     return blk.reshape(rows, nb * 144)
 
 
+def q5k(g, rows, K, d_sigma=0.01, dmin_sigma=0.02):
+    nb = K // QK_K
+    blk = np.frombuffer(g.bytes(rows * nb * 176), dtype=np.uint8).reshape(rows, nb, 176).copy()
+    d = _f16_bits(np.abs(g.standard_normal((rows, nb), dtype=np.float32)) * d_sigma)
+    dm = _f16_bits(np.abs(g.standard_normal((rows, nb), dtype=np.float32)) * dmin_sigma)
+    blk[:, :, 0:2] = d.reshape(rows, nb, 1).view(np.uint8)
+    blk[:, :, 2:4] = dm.reshape(rows, nb, 1).view(np.uint8)
+    return blk.reshape(rows, nb * 176)
+
+
 def q6k(g, rows, K, d_sigma=0.01):
     nb = K // QK_K
     blk = np.frombuffer(g.bytes(rows * nb * 210), dtype=np.uint8).reshape(rows, nb, 210).copy()
@@ -42,7 +54,7 @@ def q6k(g, rows, K, d_sigma=0.01):
 
 
 def weights(g, ggml_type, rows, K):
-    return q4k(g, rows, K) if ggml_type == 12 else q6k(g, rows, K)
+    return {12: q4k, 13: q5k, 14: q6k}[ggml_type](g, rows, K)
 
 
 def x_f16(g, shape):

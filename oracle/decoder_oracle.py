@@ -9,10 +9,13 @@ Follows src/engine/decode.cu of genie-ai-runtime:
   prefill       Path B :2779-2807 -> transformer_prefill :1760-1884, first
                 token from the last prefill row :2950-2990
   sampling      sample_greedy, src/engine/sample.cpp:160-170
-and the GEMV dispatch of gemv_q4.cu: gemv_quant / _pair (both Q4_K) /
-_triple -> int8 MMVQ on the q8_1-quantised activation; gemv_quant_add and
-gemv_quant_f32 of Q6_K -> float dequant (gemv_quant_cpu arithmetic);
-gemm_quant_batched -> MMQ for N > 1, gemv_quant for N == 1.
+and the GEMV dispatch of gemv_q4.cu: gemv_quant of Q4_K / Q6_K (:1263-1290),
+_pair of Q4_K+Q4_K (:1391), _triple of the four instantiated Q4_K/Q6_K
+combinations (:1475-1490) and gemv_quant_f32 of Q4_K -> int8 MMVQ on the
+q8_1-quantised activation; everything else (Q5_K anywhere, gemv_quant_add)
+-> float dequant (gemv_quant_cpu arithmetic); gemm_quant_batched -> MMQ
+for Q4_K / Q6_K with N > 1, the float Q5_K batched kernel (:1703-1762, per
+token the gemv_quant_cpu arithmetic) for Q5_K, gemv_quant for N == 1.
 
 A model is the dict of decoder.synth_np (raw GGUF block bytes as numpy).
 """
@@ -34,10 +37,17 @@ def mmvq_f16(W, t, x, M, K):
     return _f16(oracle.mmvq(W, t, oracle.quantize_q8_1(x, K), M, K))
 
 
+def float_f16(W, t, x, M, K):
+    return _f16(oracle.gemv_quant_cpu(W, t, x, M, K))
+
+
 def pair(W0, t0, W1, t1, x, M, K):
-    if t0 == 12 and t1 == 12:
-        return mmvq_f16(W0, t0, x, M, K), mmvq_f16(W1, t1, x, M, K)
-    return _f16(oracle.gemv_quant_cpu(W0, t0, x, M, K)), _f16(oracle.gemv_quant_cpu(W1, t1, x, M, K))
+    f = mmvq_f16 if (t0 == 12 and t1 == 12) else float_f16
+    return f(W0, t0, x, M, K), f(W1, t1, x, M, K)
+
+
+def triple_mmvq(t0, t1, t2):
+    return (t0, t1, t2) in ((12, 12, 14), (12, 12, 12), (14, 14, 14), (14, 12, 12))
 
 
 def gemv_add(W, t, x, res, M, K):
@@ -49,7 +59,10 @@ def gemv_add(W, t, x, res, M, K):
 def gemm(W, t, x, M, N, K):
     """gemm_quant_batched: [N][M] fp16."""
     if N == 1:
-        return mmvq_f16(W, t, x, M, K)
+        return (float_f16 if t == 13 else mmvq_f16)(W, t, x, M, K)
+    if t == 13:
+        xs = np.asarray(x, np.uint16).reshape(N, K)
+        return np.concatenate([float_f16(W, t, xs[i], M, K) for i in range(N)])
     Npad = (N + 63) // 64 * 64
     q8 = oracle.quantize_mmq(x, N, K, Npad, t == 12)
     return _f16(oracle.mmq(W, t, q8, M, N, K, Npad)).ravel()
@@ -73,8 +86,12 @@ class OracleDecoder:
     def _head(self, xrow):
         s = self.s
         normed = oracle.rmsnorm(xrow, None, self.m["output_norm"], 1, s.hidden_dim, s.rms_eps, True)
-        self.logits = oracle.gemv_quant_cpu(self.m["output"], self.m["output_type"], normed, s.vocab_size,
-                                            s.hidden_dim)
+        t = self.m["output_type"]
+        if t == 12:
+            self.logits = oracle.mmvq(self.m["output"], t, oracle.quantize_q8_1(normed, s.hidden_dim), s.vocab_size,
+                                      s.hidden_dim)
+        else:
+            self.logits = oracle.gemv_quant_cpu(self.m["output"], t, normed, s.vocab_size, s.hidden_dim)
         return oracle.argmax(self.logits)
 
     def _attn_front(self, l, L, q, k, v, start, N):
@@ -113,9 +130,10 @@ class OracleDecoder:
         for l, L in enumerate(self.m["layers"]):
             T = L["types"]
             normed = oracle.rmsnorm(x, None, L["rms_attn"], 1, H, s.rms_eps, True)
-            q = mmvq_f16(L["wq"], T["wq"], normed, QD, H)
-            k = mmvq_f16(L["wk"], T["wk"], normed, KVD, H)
-            v = mmvq_f16(L["wv"], T["wv"], normed, KVD, H)
+            f = mmvq_f16 if triple_mmvq(T["wq"], T["wk"], T["wv"]) else float_f16
+            q = f(L["wq"], T["wq"], normed, QD, H)
+            k = f(L["wk"], T["wk"], normed, KVD, H)
+            v = f(L["wv"], T["wv"], normed, KVD, H)
             q, k = self._attn_front(l, L, q, k, v, pos, 1)
             attn = oracle.attn_decode_int8(q, self.kc[l], self.vc[l], s.n_heads, s.n_kv_heads, s.head_dim,
                                            s.head_dim, pos + 1, 1.0 / np.sqrt(s.head_dim), self.ks[l], self.vs[l], 0,

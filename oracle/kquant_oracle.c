@@ -14,10 +14,12 @@
  *                                     patterns / 1e6 random floats.
  *   orc_get_scale_min_k4           : bit-level numpy unpack of all 16 six-bit
  *                                     fields (each of the 96 bits used once).
- *   orc_dequant_q4k/q6k            : numpy vectorised dequant written from the
+ *   orc_dequant_q4k/q5k/q6k        : numpy vectorised dequant written from the
  *                                     GGUF block spec; x = e_k column probes.
  *   orc_gemv_quant_cpu             : float64 numpy dot of the dequantised
- *                                     matrix; closed forms (d=0, qs=0).
+ *                                     matrix; closed forms (d=0, qs=0; Q5_K
+ *                                     with qh=0 equals Q4_K of the same
+ *                                     header and qs, qh=0xFF adds 16*d*sc*x).
  *   orc_quantize_q8_1*             : closed forms (amax element -> +-127,
  *                                     zero block -> d=0), numpy restatement.
  *   orc_mmvq_* / orc_mmq_*         : int32 dots brute-forced in numpy int64,
@@ -40,6 +42,7 @@
 #pragma pack(push, 1)
 typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[12]; uint8_t qs[128]; } orc_block_q4k;   /* 144 B */
 typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } orc_block_q6k;  /* 210 B */
+typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } orc_block_q5k;  /* 176 B */
 typedef struct { uint16_t d; uint16_t s; int8_t qs[32]; } orc_block_q8_1;                           /* 36 B  */
 typedef struct { uint16_t ds4[8]; int8_t qs[128]; } orc_block_q8_1_mmq;                             /* 144 B */
 #pragma pack(pop)
@@ -108,6 +111,30 @@ void orc_dequant_q4k(float* out, const void* W, int64_t n_blocks) {
     }
 }
 
+/* Q5_K: the Q4_K scale/min packing plus a fifth code bit from qh (bit 2*il
+ * for the low nibbles of qs[32*il..], bit 2*il+1 for the high nibbles),
+ * dot_q5k_row, gemv_q4.cu:318-363. */
+void orc_dequant_q5k(float* out, const void* W, int64_t n_blocks) {
+    const orc_block_q5k* B = (const orc_block_q5k*)W;
+    for (int64_t b = 0; b < n_blocks; b++) {
+        const orc_block_q5k* blk = &B[b];
+        const float dall = orc_f16_to_f32(blk->d), dmin = orc_f16_to_f32(blk->dmin);
+        float* o = out + b * QK_K;
+        uint8_t u1 = 1, u2 = 2;
+        for (int il = 0; il < 4; il++, u1 <<= 2, u2 <<= 2) {
+            uint8_t sc1, m1, sc2, m2;
+            orc_get_scale_min_k4(2 * il, blk->scales, &sc1, &m1);
+            orc_get_scale_min_k4(2 * il + 1, blk->scales, &sc2, &m2);
+            const float d1 = dall * sc1, dm1 = dmin * m1, d2 = dall * sc2, dm2 = dmin * m2;
+            const uint8_t* ql = blk->qs + 32 * il;
+            for (int l = 0; l < 32; l++) {
+                o[64 * il + l] = d1 * ((ql[l] & 0xF) + ((blk->qh[l] & u1) ? 16 : 0)) - dm1;
+                o[64 * il + 32 + l] = d2 * ((ql[l] >> 4) + ((blk->qh[l] & u2) ? 16 : 0)) - dm2;
+            }
+        }
+    }
+}
+
 void orc_dequant_q6k(float* out, const void* W, int64_t n_blocks) {
     const orc_block_q6k* B = (const orc_block_q6k*)W;
     for (int64_t b = 0; b < n_blocks; b++) {
@@ -131,7 +158,7 @@ void orc_dequant_q6k(float* out, const void* W, int64_t n_blocks) {
     }
 }
 
-/* gemv_quant_cpu, gemv_q4.cu:2519-2631 (Q4_K and Q6_K branches): one row at
+/* gemv_quant_cpu, gemv_q4.cu:2519-2631 (Q4_K, Q5_K and Q6_K branches): one row at
  * a time, fp32 accumulator, fp16 activations widened per element. Returns 0
  * on success, -1 for an unsupported type (the reference prints FATAL and the
  * caller zero-fills y). row0/row1 select a row range so a threaded caller can
@@ -155,6 +182,26 @@ static void gemv_rows(float* y, const void* W, int type, const uint16_t* x, int6
                     for (int l = 0; l < 32; l++) acc += (d1 * (q[l] & 0xF) - dm1) * orc_f16_to_f32(x[k + l]);
                     for (int l = 0; l < 32; l++) acc += (d2 * (q[l] >> 4) - dm2) * orc_f16_to_f32(x[k + 32 + l]);
                     q += 32; is += 2; k += 64;
+                }
+            }
+        } else if (type == 13) {
+            const orc_block_q5k* rb = (const orc_block_q5k*)W + row * nb;
+            for (int b = 0; b < nb; b++) {
+                const orc_block_q5k* blk = &rb[b];
+                const float dall = orc_f16_to_f32(blk->d), dmin = orc_f16_to_f32(blk->dmin);
+                const uint8_t* ql = blk->qs; const uint8_t* qh = blk->qh;
+                uint8_t u1 = 1, u2 = 2;
+                int is = 0, k = b * QK_K;
+                for (int j = 0; j < QK_K; j += 64) {
+                    uint8_t sc1, m1, sc2, m2;
+                    orc_get_scale_min_k4(is + 0, blk->scales, &sc1, &m1);
+                    orc_get_scale_min_k4(is + 1, blk->scales, &sc2, &m2);
+                    const float d1 = dall * sc1, dm1 = dmin * m1, d2 = dall * sc2, dm2 = dmin * m2;
+                    for (int l = 0; l < 32; l++)
+                        acc += (d1 * ((ql[l] & 0xF) + ((qh[l] & u1) ? 16 : 0)) - dm1) * orc_f16_to_f32(x[k + l]);
+                    for (int l = 0; l < 32; l++)
+                        acc += (d2 * ((ql[l] >> 4) + ((qh[l] & u2) ? 16 : 0)) - dm2) * orc_f16_to_f32(x[k + 32 + l]);
+                    ql += 32; is += 2; u1 <<= 2; u2 <<= 2; k += 64;
                 }
             }
         } else {
@@ -186,7 +233,7 @@ static void gemv_rows(float* y, const void* W, int type, const uint16_t* x, int6
 }
 
 int orc_gemv_quant_cpu(float* y, const void* W, int type, const uint16_t* x, int M, int K) {
-    if (type != 12 && type != 14) return -1;
+    if (type < 12 || type > 14) return -1;
     gemv_rows(y, W, type, x, 0, M, K);
     return 0;
 }
@@ -194,7 +241,7 @@ int orc_gemv_quant_cpu(float* y, const void* W, int type, const uint16_t* x, int
 /* Same arithmetic per row, rows split over `threads` OpenMP threads (the
  * all-cores CPU baseline; per-row results are identical to the 1-core path). */
 int orc_gemv_quant_cpu_mt(float* y, const void* W, int type, const uint16_t* x, int M, int K, int threads) {
-    if (type != 12 && type != 14) return -1;
+    if (type < 12 || type > 14) return -1;
 #ifdef _OPENMP
     #pragma omp parallel for num_threads(threads) schedule(static)
     for (int t = 0; t < threads; t++) {

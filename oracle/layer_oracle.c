@@ -33,6 +33,7 @@ float orc_f16_to_f32(uint16_t h);
 uint16_t orc_f32_to_f16(float f);
 void orc_dequant_q4k(float* out, const void* W, int64_t n_blocks);
 void orc_dequant_q6k(float* out, const void* W, int64_t n_blocks);
+void orc_dequant_q5k(float* out, const void* W, int64_t n_blocks);
 void orc_attn_decode_int8(uint16_t* out, const uint16_t* q, const int8_t* kc, const int8_t* vc,
                           int n_heads, int n_kv, int hd, int chd, int seq, float scale,
                           const float* ks, const float* vs, int window, int n_splits);
@@ -136,13 +137,15 @@ void orc_qk_post(uint16_t* q, uint16_t* k, const uint16_t* v, const void* q_norm
     free(tmp);
 }
 
-/* dequant_embedding_q4k_kernel / _q6k_kernel, gemv_q4.cu:793-864:
- * dst = half(dequantised row token of the table); same fp32 expressions as
- * the row dequant (dall*sc*q - dmin*m; d*sc*(q-32)). */
+/* dequant_embedding_q4k_kernel / _q6k_kernel, gemv_q4.cu:793-864, and the
+ * engine's host Q5_K row dequant, decode.cu:230-266: dst = half(dequantised
+ * row token of the table); same fp32 expressions as the row dequant
+ * (dall*sc*q - dmin*m; d*sc*(q-32)). */
 void orc_embed_row(uint16_t* dst, const void* W, int type, int token, int hidden) {
     const int nb = hidden / 256;
     float* row = (float*)malloc(sizeof(float) * (size_t)hidden);
     if (type == 12) orc_dequant_q4k(row, (const uint8_t*)W + (int64_t)token * nb * 144, nb);
+    else if (type == 13) orc_dequant_q5k(row, (const uint8_t*)W + (int64_t)token * nb * 176, nb);
     else orc_dequant_q6k(row, (const uint8_t*)W + (int64_t)token * nb * 210, nb);
     for (int i = 0; i < hidden; i++) dst[i] = orc_f32_to_f16(row[i]);
     free(row);

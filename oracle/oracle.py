@@ -32,6 +32,7 @@ def lib():
             "orc_f32_to_f16": (ctypes.c_uint16, [F]),
             "orc_dequant_q4k": (None, [P, P, ctypes.c_int64]),
             "orc_dequant_q6k": (None, [P, P, ctypes.c_int64]),
+            "orc_dequant_q5k": (None, [P, P, ctypes.c_int64]),
             "orc_gemv_quant_cpu": (I, [P, P, I, P, I, I]),
             "orc_gemv_quant_cpu_mt": (I, [P, P, I, P, I, I, I]),
             "orc_quantize_q8_1": (None, [P, P, I]),
@@ -78,7 +79,7 @@ def f16_bits_to_f32(h):
 def dequant(W, ggml_type, rows, K):
     W = _c(W, np.uint8)
     out = np.empty((rows, K), dtype=np.float32)
-    fn = lib().orc_dequant_q4k if ggml_type == 12 else lib().orc_dequant_q6k
+    fn = {12: lib().orc_dequant_q4k, 13: lib().orc_dequant_q5k, 14: lib().orc_dequant_q6k}[ggml_type]
     fn(_p(out), _p(W), rows * (K // 256))
     return out
 

@@ -39,6 +39,28 @@ def q4k_dequant(W, rows, K):
     return w.reshape(rows, K)
 
 
+def q5k_fields(W, rows, K):
+    """Q5_K: Q4_K header (d, dmin, 12 scale bytes), qh[32], qs[128]; code =
+    nibble + 16 * bit (2*il for the low nibbles, 2*il+1 for the high) of qh."""
+    nb = K // 256
+    b = np.asarray(W, dtype=np.uint8).reshape(rows, nb, 176)
+    hdr = np.concatenate([b[:, :, 0:16], np.zeros((rows, nb, 128), np.uint8)], axis=2)
+    d, dmin, sc, mn, _ = q4k_fields(hdr.reshape(rows, -1), rows, K)
+    qh = b[:, :, 16:48].astype(np.int64)
+    qs = b[:, :, 48:176].reshape(rows, nb, 4, 32).astype(np.int64)
+    q = np.empty((rows, nb, 8, 32), np.int64)
+    for il in range(4):
+        q[:, :, 2 * il, :] = (qs[:, :, il] & 15) + 16 * ((qh >> (2 * il)) & 1)
+        q[:, :, 2 * il + 1, :] = (qs[:, :, il] >> 4) + 16 * ((qh >> (2 * il + 1)) & 1)
+    return d, dmin, sc, mn, q
+
+
+def q5k_dequant(W, rows, K):
+    d, dmin, sc, mn, q = q5k_fields(W, rows, K)
+    w = d[..., None, None] * sc[..., None] * q - dmin[..., None, None] * mn[..., None]
+    return w.reshape(rows, K)
+
+
 def q6k_fields(W, rows, K):
     nb = K // 256
     b = np.asarray(W, dtype=np.uint8).reshape(rows, nb, 210)
@@ -61,7 +83,7 @@ def q6k_dequant(W, rows, K):
 
 
 def dequant(W, t, rows, K):
-    return q4k_dequant(W, rows, K) if t == 12 else q6k_dequant(W, rows, K)
+    return {12: q4k_dequant, 13: q5k_dequant, 14: q6k_dequant}[t](W, rows, K)
 
 
 def codes(W, t, rows, K):

@@ -1,5 +1,5 @@
-"""GPU parity of the decoder loop (jllm_hip_decoder_*): a random Q4_K_M
-model run through the C ABI against the CPU restatement of the reference
+"""GPU parity of the decoder loop (jllm_hip_decoder_*): random Q4_K_M and
+Q5_K_M-style models run through the C ABI against the CPU restatement of the reference
 engine's layer order (oracle/decoder_oracle.py).
 
 Bars: the greedy tokens of a free-running generation are identical to the
@@ -35,10 +35,12 @@ def _rel(got, want):
     return float(np.abs(got - want).max() / np.abs(want).max())
 
 
-@pytest.mark.parametrize("shape,n_prompt,n_gen,seed", [(TINY, 20, 8, 1), (TINY, 1, 4, 2), (WIDE, 6, 3, 3)])
-def test_decoder_vs_oracle(dev, shape, n_prompt, n_gen, seed):
-    print_case("decoder", shape.hidden_dim, shape.n_layers, n_prompt, n_gen)
-    model = decoder.synth_np(shape, seed)
+@pytest.mark.parametrize("shape,n_prompt,n_gen,seed,preset", [(TINY, 20, 8, 1, "q4km"), (TINY, 1, 4, 2, "q4km"),
+                                                               (WIDE, 6, 3, 3, "q4km"), (TINY, 20, 6, 4, "q5km"),
+                                                               (WIDE, 5, 3, 5, "q5km")])
+def test_decoder_vs_oracle(dev, shape, n_prompt, n_gen, seed, preset):
+    print_case("decoder", shape.hidden_dim, shape.n_layers, n_prompt, n_gen, preset)
+    model = decoder.synth_np(shape, seed, preset)
     prompt = synth.rng(seed + 100).integers(0, shape.vocab_size, n_prompt).astype(np.int32)
     max_seq = n_prompt + n_gen
     orc = decoder_oracle.OracleDecoder(shape, model, max_seq)
@@ -92,7 +94,7 @@ def test_decoder_rejects_bad_config(dev):
     model = decoder.to_device(decoder.synth_np(shape, 9), dev)
     bad = dict(model)
     bad["layers"] = [dict(L) for L in model["layers"]]
-    bad["layers"][1]["types"] = dict(bad["layers"][1]["types"], w_up=13)
+    bad["layers"][1]["types"] = dict(bad["layers"][1]["types"], w_up=15)
     with pytest.raises(Exception):
         decoder.Decoder(shape, bad, 16)
     d = decoder.Decoder(shape, model, 16)

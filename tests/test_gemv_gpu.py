@@ -47,7 +47,7 @@ def test_quantize_q8_1_bit_exact(dev, t):
         assert np.array_equal(from_dev(y), oracle.quantize_q8_1(x, K))
 
 
-@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("t", [12, 13, 14])
 @pytest.mark.parametrize("rows,K", SHAPES)
 def test_gemv_dequant_f32_vs_host_scalar(dev, t, rows, K):
     """float-dequant fp32 GEMV vs gemv_quant_cpu (the reference host path)."""
@@ -59,10 +59,10 @@ def test_gemv_dequant_f32_vs_host_scalar(dev, t, rows, K):
     assert rel_inf(from_dev(y), want) <= TOL
 
 
-@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("t", [12, 13, 14])
 @pytest.mark.parametrize("rows,K", SHAPES)
 def test_gemv_f32(dev, t, rows, K):
-    """gemv_quant_f32: Q4_K via MMVQ (oracle mmvq), Q6_K via float dequant."""
+    """gemv_quant_f32: Q4_K via MMVQ (oracle mmvq), Q5_K / Q6_K via float dequant."""
     print_case("gemv_f32", t, rows, K)
     W, x = _case(t, rows, K, 200 + rows)
     y = empty_f32(rows)
@@ -74,21 +74,25 @@ def test_gemv_f32(dev, t, rows, K):
     assert rel_inf(from_dev(y), want) <= TOL
 
 
-@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("t", [12, 13, 14])
 @pytest.mark.parametrize("rows,K", SHAPES)
 def test_gemv_half_mmvq(dev, t, rows, K):
+    """gemv_quant: MMVQ for Q4_K / Q6_K, float dequant for Q5_K (gemv_q4.cu:1263-1290)."""
     print_case("gemv_half", t, rows, K)
     W, x = _case(t, rows, K, 300 + rows)
     y = empty_f16(rows)
     jllm.gemv_quant(y, to_dev(W), t, to_dev(x), rows, K)
-    want = oracle.mmvq(W, t, oracle.quantize_q8_1(x, K), rows, K)
+    if t == 13:
+        want = oracle.gemv_quant_cpu(W, t, x, rows, K)
+    else:
+        want = oracle.mmvq(W, t, oracle.quantize_q8_1(x, K), rows, K)
     ok, err = _close_f16(from_dev(y, np.uint16), want)
     assert ok, err
 
 
-@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("t", [12, 13, 14])
 def test_gemv_add(dev, t):
-    rows, K = 2560, 4096 if t == 12 else 9728
+    rows, K = 2560, 9728 if t == 14 else 4096
     print_case("gemv_add", t, rows, K)
     W, x = _case(t, rows, K, 400)
     res = synth.x_f16(synth.rng(401), rows)
@@ -129,12 +133,66 @@ def test_gemv_pair_and_triple(dev):
         assert ok, (t, M, err)
 
 
+def test_q5k_in_fused_launches(dev):
+    """Launches holding Q5_K rows run in float mode for every segment
+    (gemv_q4.cu:1391-1441, :1527-1559); Q4_K + Q5_K segments in one call are
+    split over two launches of the same kernel family."""
+    K = 2560
+    g = synth.rng(520)
+    x = synth.x_f16(g, K)
+    Wa, Wb, Wc = synth.q5k(g, 4096, K), synth.q4k(g, 1024, K), synth.q6k(g, 1024, K)
+    ys = [empty_f16(4096), empty_f16(1024), empty_f16(1024)]
+    print_case("triple q5k/q4k/q6k")
+    jllm.gemv_quant_triple(ys[0], to_dev(Wa), 13, 4096, ys[1], to_dev(Wb), 12, 1024, ys[2], to_dev(Wc), 14, 1024,
+                           to_dev(x), K)
+    for y, W, t, M in zip(ys, (Wa, Wb, Wc), (13, 12, 14), (4096, 1024, 1024)):
+        ok, err = _close_f16(from_dev(y, np.uint16), oracle.gemv_quant_cpu(W, t, x, M, K))
+        assert ok, (t, M, err)
+    print_case("pair q5k/q5k")
+    Wg, Wu = synth.q5k(g, 9728, K), synth.q5k(g, 9728, K)
+    y0, y1 = empty_f16(9728), empty_f16(9728)
+    jllm.gemv_quant_pair(y0, to_dev(Wg), 13, 9728, y1, to_dev(Wu), 13, 9728, to_dev(x), K)
+    for y, W in ((y0, Wg), (y1, Wu)):
+        ok, err = _close_f16(from_dev(y, np.uint16), oracle.gemv_quant_cpu(W, 13, x, 9728, K))
+        assert ok, err
+    print_case("triple_rmsnorm q5k/q5k/q6k")
+    w = (1.0 + 0.02 * g.standard_normal(K)).astype(np.float32)
+    xn = oracle.rmsnorm(x, None, w, 1, K, 1e-6, True)
+    Wk = synth.q5k(g, 1024, K)
+    jllm.call("jllm_hip_gemv_quant_triple_rmsnorm", ys[0], to_dev(Wa), 13, 4096, ys[1], to_dev(Wk), 13, 1024,
+              ys[2], to_dev(Wc), 14, 1024, to_dev(x), to_dev(w), 1, 1e-6, K)
+    for y, W, t, M in zip(ys, (Wa, Wk, Wc), (13, 13, 14), (4096, 1024, 1024)):
+        ok, err = _close_f16(from_dev(y, np.uint16), oracle.gemv_quant_cpu(W, t, xn, M, K))
+        assert ok, (t, M, err)
+
+
+def test_triple_routes_like_the_reference(dev):
+    """A Q4_K/Q6_K triple outside the four MMVQ instantiations
+    (gemv_q4.cu:1475-1490), e.g. (Q4_K, Q6_K, Q4_K), runs in float mode."""
+    K = 2560
+    g = synth.rng(530)
+    x = synth.x_f16(g, K)
+    Ws = (synth.q4k(g, 512, K), synth.q6k(g, 256, K), synth.q4k(g, 256, K))
+    ys = [empty_f16(512), empty_f16(256), empty_f16(256)]
+    print_case("triple q4k/q6k/q4k")
+    jllm.gemv_quant_triple(ys[0], to_dev(Ws[0]), 12, 512, ys[1], to_dev(Ws[1]), 14, 256, ys[2], to_dev(Ws[2]), 12, 256,
+                           to_dev(x), K)
+    for y, W, t, M in zip(ys, Ws, (12, 14, 12), (512, 256, 256)):
+        got = f16_to_f64(from_dev(y, np.uint16))
+        fl = oracle.gemv_quant_cpu(W, t, x, M, K)
+        mq = oracle.mmvq(W, t, oracle.quantize_q8_1(x, K), M, K)
+        assert _close_f16(from_dev(y, np.uint16), fl)[0]
+        # and it is the float result, not the MMVQ one: closer to the former
+        assert np.abs(got - fl).max() < np.abs(got - mq).max()
+
+
 def test_gemv_errors(dev):
     x = to_dev(synth.x_f16(synth.rng(1), 512))
     W = to_dev(synth.q4k(synth.rng(2), 4, 512))
     y = empty_f16(4)
-    with pytest.raises(jllm.JllmError, match="unsupported"):
-        jllm.gemv_quant(y, W, 13, x, 4, 512)
+    for bad in (11, 15, 0):
+        with pytest.raises(jllm.JllmError, match="unsupported"):
+            jllm.gemv_quant(y, W, bad, x, 4, 512)
     with pytest.raises(jllm.JllmError, match="invalid"):
         jllm.gemv_quant(y, W, 12, x, 4, 300)
     host = torch.zeros(4 * 2 * 144, dtype=torch.uint8)           # plain host memory: no fallback
@@ -177,9 +235,9 @@ def test_triple_and_pair_rmsnorm(dev):
         assert ok, err
 
 
-@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("t", [12, 13, 14])
 def test_f32_rmsnorm_lm_head(dev, t):
-    K, M, eps = 2560, 151936 if t == 14 else 4000, 1e-6
+    K, M, eps = 2560, {12: 4000, 13: 20000, 14: 151936}[t], 1e-6
     print_case("f32_rmsnorm", t, M)
     g, x, w = _rms_case(710 + t, K)
     W = synth.weights(g, t, M, K)

@@ -178,8 +178,11 @@ def test_qk_post(dev, N, pos0, norm, kv_int8, chd):
 
 # ---- embedding / argmax -------------------------------------------------------------
 
-@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("t", [12, 13, 14])
 def test_embedding_rows_bit_exact(dev, t):
+    """Q4_K / Q6_K: dequant_embedding_q4k/q6k_kernel; Q5_K rows: the engine's
+    host dequant (decode.cu:230-266) -- the single-row entry point keeps the
+    reference's Q4_K/Q6_K-only contract (gemv_q4.cu:2777-2810)."""
     print_case("embedding", t)
     vocab, hidden = 300, 2560
     g = synth.rng(t)
@@ -193,6 +196,9 @@ def test_embedding_rows_bit_exact(dev, t):
         want = oracle.embed_row(W, t, tok, hidden) if 0 <= tok < vocab else np.zeros(hidden, np.uint16)
         assert np.array_equal(got[i], want), (i, tok)
     one = dev16(hidden, dev)
+    if t == 13:
+        assert jllm.lib().jllm_hip_dequant_embedding_row(jllm._ptr(one), jllm._ptr(Wd), 13, 123, hidden, None) != 0
+        return
     jllm.call("jllm_hip_dequant_embedding_row", one, Wd, t, 123, hidden)
     assert np.array_equal(from_dev(one, np.uint16), oracle.embed_row(W, t, 123, hidden))
 

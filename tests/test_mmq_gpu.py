@@ -101,3 +101,72 @@ def test_gemm_n1_routes_to_gemv(dev):
     want = oracle.mmvq(W, 12, oracle.quantize_q8_1(x, K), M, K)
     got = f16_to_f64(from_dev(y, np.uint16))
     assert np.all(np.abs(got - want) <= TOL * np.abs(want).max() + np.abs(want) * 2 ** -10)
+
+
+# ---- Q5_K batched GEMM (fp16 activation, float-dequant arithmetic) --------------
+
+def _oracle_q5_batched(W, x, M, N, K):
+    """gemm_quant_batched_q5k_kernel (gemv_q4.cu:1703-1762) per token is the
+    row arithmetic of gemv_quant_cpu's Q5_K branch."""
+    return np.stack([oracle.gemv_quant_cpu(W, 13, x[t], M, K) for t in range(N)])
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 70, 2560), (128, 64, 1024), (97, 130, 512), (256, 2, 256), (1, 3, 256),
+                                   (130, 65, 4096)])
+def test_q5k_batched_f32_and_f16(dev, M, N, K):
+    print_case("q5k_gemm", M, N, K)
+    g = synth.rng(3000 + M + N + K)
+    W = synth.q5k(g, M, K)
+    x = synth.x_f16(g, (N, K))
+    Wd, xd = to_dev(W), to_dev(x)
+    want = _oracle_q5_batched(W, x, M, N, K)
+    y32 = torch.empty(N * M, dtype=torch.float32, device=dev)
+    jllm.call("jllm_hip_gemm_quant_batched_f32", y32, Wd, 13, xd, M, N, K)
+    got = from_dev(y32).reshape(N, M)
+    assert rel_inf(got, want) <= TOL
+    # every product is exact and the sums are fp32: far inside the bar
+    assert rel_inf(got, want) <= 2e-5
+    y16 = torch.empty(N * M, dtype=torch.int16, device=dev)
+    jllm.call("jllm_hip_gemm_quant_batched", y16, Wd, 13, xd, M, N, K)
+    got16 = f16_to_f64(from_dev(y16, np.uint16)).reshape(N, M)
+    assert np.all(np.abs(got16 - want) <= TOL * np.abs(want).max() + np.abs(want) * 2 ** -10)
+
+
+def test_q5k_batched_column_probe(dev):
+    """Token t = e_k(t): row t of y is column k(t) of the dequantised matrix,
+    which pins the K order of the matrix-core mapping and the min term."""
+    M, K = 160, 512
+    W = synth.q5k(synth.rng(3100), M, K)
+    ks = np.array([0, 1, 7, 8, 15, 16, 31, 32, 33, 47, 48, 63, 64, 100, 127, 128, 200, 255, 256, 300, 383, 511])
+    N = len(ks)
+    x = np.zeros((N, K), np.uint16)
+    x[np.arange(N), ks] = 0x3C00
+    y = torch.empty(N * M, dtype=torch.float32, device=dev)
+    print_case("q5k_gemm_probe", M, N, K)
+    jllm.call("jllm_hip_gemm_quant_batched_f32", y, to_dev(W), 13, to_dev(x), M, N, K)
+    got = from_dev(y).reshape(N, M)
+    Wd = oracle.dequant(W, 13, M, K)
+    assert np.allclose(got, Wd[:, ks].T, rtol=2e-6, atol=1e-9)
+
+
+@pytest.mark.parametrize("N", [512, 1261])
+def test_q5k_batched_baseline_shape_sampled(dev, N):
+    M, K = 9728, 2560
+    print_case("q5k_gemm_full", M, N, K)
+    g = synth.rng(3200 + N)
+    W = synth.q5k(g, M, K)
+    x = synth.x_f16(g, (N, K))
+    y32 = torch.empty(N * M, dtype=torch.float32, device=dev)
+    jllm.call("jllm_hip_gemm_quant_batched_f32", y32, to_dev(W), 13, to_dev(x), M, N, K)
+    got = from_dev(y32).reshape(N, M)
+    rows = np.sort(g.choice(M, 24, replace=False))
+    rows[-1] = M - 1
+    want = _oracle_q5_batched(np.ascontiguousarray(W[rows]), x, len(rows), N, K)
+    assert rel_inf(got[:, rows], want) <= 2e-5
+
+
+def test_q5k_has_no_subdots(dev):
+    x = to_dev(synth.x_f16(synth.rng(1), (2, 256)))
+    W = to_dev(synth.q5k(synth.rng(2), 4, 256))
+    out = torch.zeros(64, dtype=torch.int32, device=dev)
+    assert jllm.lib().jllm_hip_mmq_subdots(jllm._ptr(out), jllm._ptr(W), 13, jllm._ptr(x), 4, 2, 256, None) != 0

@@ -41,7 +41,7 @@ def test_f32_to_f16_rne_matches_numpy():
 
 # ---- dequant / scale unpack -----------------------------------------------------
 
-@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("t", [12, 13, 14])
 def test_dequant_matches_spec_restatement(t):
     rows, K = 16, 1024
     W = synth.weights(synth.rng(1), t, rows, K)
@@ -68,7 +68,7 @@ def test_q4k_scale_fields_each_bit_once():
 
 # ---- host scalar GEMV (gemv_quant_cpu) ------------------------------------------
 
-@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("t", [12, 13, 14])
 def test_gemv_cpu_vs_float64(t):
     rows, K = 64, 2560
     g = synth.rng(2)
@@ -82,7 +82,7 @@ def test_gemv_cpu_vs_float64(t):
     assert np.all(np.abs(y - want) <= 2e-6 * bound + 1e-12)
 
 
-@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("t", [12, 13, 14])
 def test_gemv_cpu_column_probe(t):
     # x = e_k  =>  y = column k of the dequantised matrix (checks element order)
     rows, K = 8, 512
@@ -117,9 +117,54 @@ def test_gemv_cpu_multithread_identical():
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-def test_gemv_cpu_rejects_unsupported_type():
+@pytest.mark.parametrize("t", [11, 15, 8])
+def test_gemv_cpu_rejects_unsupported_type(t):
     with pytest.raises(ValueError):
-        oracle.gemv_quant_cpu(np.zeros(176, np.uint8), 13, np.zeros(256, np.uint16), 1, 256)
+        oracle.gemv_quant_cpu(np.zeros(256, np.uint8), t, np.zeros(256, np.uint16), 1, 256)
+
+
+def _q5_as_q4(W5, rows, K):
+    """The Q4_K tensor with the header and qs of a Q5_K tensor (qh dropped)."""
+    b = W5.reshape(rows, -1, 176)
+    return np.concatenate([b[:, :, 0:16], b[:, :, 48:176]], axis=2).reshape(rows, -1)
+
+
+@pytest.mark.parametrize("fill", [0x00, 0xFF])
+def test_q5k_closed_forms_vs_q4k(fill):
+    # qh = 0: the Q5_K row is the Q4_K row of the same header and qs.
+    # qh = 0xFF: every code gains 16, so y gains 16 * sum_j d*sc_j*sum(x over sub-block j).
+    rows, K = 6, 768
+    g = synth.rng(40)
+    W5 = synth.q5k(g, rows, K)
+    W5.reshape(rows, -1, 176)[:, :, 16:48] = fill
+    x = synth.x_f16(g, K)
+    y5 = oracle.gemv_quant_cpu(W5, 13, x, rows, K).astype(np.float64)
+    W4 = _q5_as_q4(W5, rows, K)
+    y4 = oracle.gemv_quant_cpu(W4, 12, x, rows, K).astype(np.float64)
+    if fill == 0:
+        assert np.array_equal(y5, y4)
+    else:
+        d, _, sc, _, _ = np_ref.q4k_fields(W4, rows, K)
+        xs = np_ref.f16(x).reshape(1, -1, 8, 32).sum(axis=3)
+        extra = 16 * (d[..., None] * sc * xs).sum(axis=(1, 2))
+        bound = np.abs(np_ref.dequant(W5, 13, rows, K)) @ np.abs(np_ref.f16(x))
+        assert np.all(np.abs(y5 - (y4 + extra)) <= 4e-6 * bound)
+
+
+def test_q5k_high_bit_positions():
+    # one qh bit b of byte l sets +16 on the code of sub-block b at position l
+    rows, K = 1, 256
+    W5 = np.zeros((rows, 176), np.uint8)
+    W5[0, 0:2] = np.array([0x3C00], np.uint16).view(np.uint8)     # d = 1
+    W5[0, 4:16] = 0x01                                             # sc = 1 for j < 4; j >= 4 gets low nibble 1
+    for bit in range(8):
+        for l in (0, 5, 31):
+            W5[0, 16:48] = 0
+            W5[0, 16 + l] = 1 << bit
+            w = oracle.dequant(W5, 13, rows, K)[0]
+            nz = np.nonzero(w)[0]
+            assert list(nz) == [32 * bit + l], (bit, l, nz)
+            assert w[32 * bit + l] == 16.0
 
 
 # ---- q8_1 quantisers -------------------------------------------------------------
