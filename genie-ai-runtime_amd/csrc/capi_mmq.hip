@@ -9,6 +9,7 @@ using namespace jllm_hip;
 
 namespace {
 DeviceScratch g_q8;     // quantised activations (fp16 codes + scale words), grown on demand, never freed
+DeviceScratch g_ws;     // split-K fp32 partials [splits][N][M], grown on demand, never freed
 
 int npad_of(int N) { return ((N + MMQ_TILE_N - 1) / MMQ_TILE_N) * MMQ_TILE_N; }
 
@@ -36,19 +37,36 @@ int run_mmq(const char* tag, void* y, const void* W, int type, const uint16_t* x
         return JLLM_ERR_POINTER;
     }
     if (!aligned16(Wd)) return JLLM_ERR_INVALID;
-    const int Npad = npad_of(N);
-    if (type == 13) return launch_status(gemm_q5k_launch(y, (const uint8_t*)Wd, x, M, N, K, out_kind, (hipStream_t)stream), tag);
-    const size_t cb = mmq_codes_bytes(K, Npad);
-    uint8_t* q8 = (uint8_t*)g_q8.get(cb + mmq_scales_bytes(K, Npad));
-    if (!q8) {
-        fprintf(stderr, "[%s] q8 scratch allocation failed\n", tag);
-        return JLLM_ERR_NOMEM;
-    }
-    uint16_t* codes = (uint16_t*)q8;
-    uint32_t* scl = (uint32_t*)(q8 + cb);
     hipStream_t st = (hipStream_t)stream;
-    hipError_t e = quantize_mmq_f16_launch(x, codes, scl, N, K, Npad, type == 12, st);
-    if (e == hipSuccess) e = mmq_launch(y, (const uint8_t*)Wd, type, codes, scl, M, N, K, Npad, out_kind, st);
+    // split-K when the tile grid alone does not cover the chip: partials to
+    // the workspace, then one ordered reduction into y
+    const int splits = out_kind == 2 ? 1 : mmq_splits(M, N, K);
+    void* dst = y;
+    if (splits > 1) {
+        dst = g_ws.get((size_t)splits * N * M * sizeof(float));
+        if (!dst) {
+            fprintf(stderr, "[%s] split-K workspace allocation failed\n", tag);
+            return JLLM_ERR_NOMEM;
+        }
+    }
+    const int kind = splits > 1 ? 1 : out_kind;
+    hipError_t e;
+    if (type == 13) {
+        e = gemm_q5k_launch(dst, (const uint8_t*)Wd, x, M, N, K, kind, splits, st);
+    } else {
+        const int Npad = npad_of(N);
+        const size_t cb = mmq_codes_bytes(K, Npad);
+        uint8_t* q8 = (uint8_t*)g_q8.get(cb + mmq_scales_bytes(K, Npad));
+        if (!q8) {
+            fprintf(stderr, "[%s] q8 scratch allocation failed\n", tag);
+            return JLLM_ERR_NOMEM;
+        }
+        uint16_t* codes = (uint16_t*)q8;
+        uint32_t* scl = (uint32_t*)(q8 + cb);
+        e = quantize_mmq_f16_launch(x, codes, scl, N, K, Npad, type == 12, st);
+        if (e == hipSuccess) e = mmq_launch(dst, (const uint8_t*)Wd, type, codes, scl, M, N, K, Npad, kind, splits, st);
+    }
+    if (e == hipSuccess && splits > 1) e = splitk_reduce_launch(y, (const float*)dst, (int64_t)N * M, splits, out_kind, st);
     return launch_status(e, tag);
 }
 }  // namespace

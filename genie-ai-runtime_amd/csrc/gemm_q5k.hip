@@ -121,12 +121,13 @@ __device__ __forceinline__ int xcd_tile_q5(int bid, int tiles) {
 template <int OUT>   // 0: fp16 y [N][M], 1: fp32 y [N][M]
 __global__ __launch_bounds__(THREADS, 2)
 void gemm_q5k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const uint16_t* __restrict__ x,
-                     int M, int N, int K) {
+                     int M, int N, int K, int sps) {
     __shared__ __attribute__((aligned(16))) uint16_t sX[2][TN * XS];
     __shared__ __attribute__((aligned(16))) uint16_t sS[2][TN * 16];     // per token: X/32 hi [8] | lo [8]
     __shared__ __attribute__((aligned(16))) float sD[4][32 * 2];         // per wave and row: dall, 32*dmin
 
     const int nb = K / QK_K;
+    const int sb0 = (int)blockIdx.y * sps, sb1 = min(nb, sb0 + sps);     // split-K range of super-blocks
     const int n_rt = (M + TM - 1) / TM, n_tt = (N + TN - 1) / TN;
     const int tile = xcd_tile_q5(blockIdx.x, n_rt * n_tt);
     const int row0 = (tile / n_tt) * TM, col0 = (tile % n_tt) * TN;
@@ -144,15 +145,15 @@ void gemm_q5k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const 
 
     ARegs A, An;
     XRegs Xn;
-    load_a(A, wrow, kg);
-    load_x(Xn, xsrc);
+    load_a(A, wrow + (int64_t)sb0 * Q5K_BYTES, kg);
+    load_x(Xn, xsrc + sb0 * QK_K);
     commit_x(Xn, sX[0], sS[0], xtok, xq);
     __syncthreads();
 
 #pragma unroll 1
-    for (int b = 0; b < nb; b++) {
-        const int st = b & 1;
-        const bool more = b + 1 < nb;
+    for (int b = sb0; b < sb1; b++) {
+        const int st = (b - sb0) & 1;
+        const bool more = b + 1 < sb1;
         if (more) {
             load_a(An, wrow + (int64_t)(b + 1) * Q5K_BYTES, kg);
             load_x(Xn, xsrc + (b + 1) * QK_K);
@@ -236,7 +237,7 @@ void gemm_q5k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const 
         for (int v = 0; v < 16; v++) {
             const int r = row0 + 32 * w + 8 * (v >> 2) + 4 * kg + (v & 3);
             if (r < M && tok < N) {
-                if (OUT == 1) ((float*)y)[(int64_t)tok * M + r] = acc[tt][v];
+                if (OUT == 1) ((float*)y)[(int64_t)blockIdx.y * N * M + (int64_t)tok * M + r] = acc[tt][v];
                 else          ((uint16_t*)y)[(int64_t)tok * M + r] = f32_to_f16_bits(acc[tt][v]);
             }
         }
@@ -246,13 +247,17 @@ void gemm_q5k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const 
 }  // namespace
 
 hipError_t gemm_q5k_launch(void* y, const uint8_t* W, const uint16_t* x, int M, int N, int K, int out_kind,
-                           hipStream_t st) {
+                           int splits, hipStream_t st) {
     if (M <= 0 || N <= 0) return hipSuccess;
     if (K <= 0 || K % QK_K != 0) return hipErrorInvalidValue;
+    const int nb = K / QK_K;
+    const int sps = (nb + splits - 1) / splits;
+    if (splits < 1 || (splits > 1 && out_kind != 1) || (splits - 1) * sps >= nb) return hipErrorInvalidValue;
     const int64_t tiles = (int64_t)((M + TM - 1) / TM) * ((N + TN - 1) / TN);
     if (tiles > 0x7FFFFFFF) return hipErrorInvalidValue;
-    if (out_kind == 1) hipLaunchKernelGGL(gemm_q5k_kernel<1>, dim3((unsigned)tiles), dim3(THREADS), 0, st, y, W, x, M, N, K);
-    else               hipLaunchKernelGGL(gemm_q5k_kernel<0>, dim3((unsigned)tiles), dim3(THREADS), 0, st, y, W, x, M, N, K);
+    const dim3 grid((unsigned)tiles, splits);
+    if (out_kind == 1) hipLaunchKernelGGL(gemm_q5k_kernel<1>, grid, dim3(THREADS), 0, st, y, W, x, M, N, K, sps);
+    else               hipLaunchKernelGGL(gemm_q5k_kernel<0>, grid, dim3(THREADS), 0, st, y, W, x, M, N, K, sps);
     return hipGetLastError();
 }
 

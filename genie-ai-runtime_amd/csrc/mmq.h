@@ -22,13 +22,23 @@ inline size_t mmq_codes_bytes(int K, int Npad) { return (size_t)K * Npad * 2; }
 inline size_t mmq_scales_bytes(int K, int Npad) { return (size_t)(K / 32) * Npad * 4; }
 
 // out_kind: 0 = fp16 y[N x M], 1 = fp32 y[N x M], 2 = raw int32 sub-block
-// dots [N][M][K/G] (G = 32 for Q4_K, 16 for Q6_K)
+// dots [N][M][K/G] (G = 32 for Q4_K, 16 for Q6_K).  splits > 1 (fp32 only):
+// K is cut into `splits` ranges of whole super-blocks and range s writes
+// its partial sums to y + s*N*M (reduce with splitk_reduce_launch).
 hipError_t mmq_launch(void* y, const uint8_t* W, int type, const uint16_t* codes, const uint32_t* scl, int M, int N,
-                      int K, int Npad, int out_kind, hipStream_t st);
+                      int K, int Npad, int out_kind, int splits, hipStream_t st);
+
+// Split count for an N x M x K GEMM: enough workgroups to cover the chip
+// when the tile grid alone does not (at least 2 super-blocks per range,
+// at most 16 ranges); a function of M, ceil(N / 64) and K only.
+int mmq_splits(int M, int N, int K);
+
+// y = sum of the `splits` fp32 partials ws[s][n], added in order s = 0, 1, ...
+hipError_t splitk_reduce_launch(void* y, const float* ws, int64_t n, int splits, int out_kind, hipStream_t st);
 
 // Q5_K batched GEMM (fp16 activation, no quantisation): out_kind 0 = fp16
 // y[N x M], 1 = fp32 y[N x M]
 hipError_t gemm_q5k_launch(void* y, const uint8_t* W, const uint16_t* x, int M, int N, int K, int out_kind,
-                           hipStream_t st);
+                           int splits, hipStream_t st);
 
 }  // namespace jllm_hip

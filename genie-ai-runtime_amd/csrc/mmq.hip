@@ -33,6 +33,7 @@
 // so that each XCD (blockIdx % 8) works on a contiguous range of row tiles.
 #include "kq_common.h"
 #include "mmq.h"
+#include <algorithm>
 
 namespace jllm_hip {
 
@@ -175,7 +176,7 @@ __device__ __forceinline__ f32x16m mfma16(h8m a, h8m b, f32x16m c) {
 template <int OUT>   // 0: fp16 y [N][M], 1: fp32 y [N][M], 2: int32 dots [N][M][K/32]
 __global__ __launch_bounds__(MMQ_THREADS, 2)
 void mmq_q4k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const uint16_t* __restrict__ codes,
-                    const uint32_t* __restrict__ scl, int M, int N, int K, int Npad) {
+                    const uint32_t* __restrict__ scl, int M, int N, int K, int Npad, int sps) {
     __shared__ __attribute__((aligned(16))) uint8_t sA[2][TM * A4_STRIDE];
     __shared__ __attribute__((aligned(16))) uint8_t sB[2][TN * B_STRIDE];
     __shared__ __attribute__((aligned(16))) _Float16 sDA[2][8 * TM];     // half(d*sc) per [j][row]
@@ -183,6 +184,8 @@ void mmq_q4k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const u
     __shared__ __attribute__((aligned(16))) uint32_t sS8[2][8 * TN];     // half d8 | half sum x << 16, per [j][token]
 
     const int nb = K / QK_K, nst = 2 * nb;
+    // split-K: this workgroup's stages [k0, k1) (whole super-blocks)
+    const int k0 = 2 * (int)blockIdx.y * sps, k1 = min(nst, k0 + 2 * sps);
     const int n_rt = (M + TM - 1) / TM, n_tt = Npad / TN;
     const int tile = xcd_tile(blockIdx.x, n_rt * n_tt);
     const int row0 = (tile / n_tt) * TM, col0 = (tile % n_tt) * TN;
@@ -353,19 +356,19 @@ void mmq_q4k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const u
 
     // stages come in pairs (s = 0, 1); each stage's loads are issued two stages
     // before it is written to LDS
-    fetch(R0, 0);
-    fetch(R1, 1);
-    commit(R0, 0);
+    fetch(R0, k0);
+    fetch(R1, k0 + 1);
+    commit(R0, k0);
     __syncthreads();
 #pragma unroll 1
-    for (int k = 0; k < nst; k += 2) {
-        if (k + 2 < nst) fetch(R0, k + 2);
+    for (int k = k0; k < k1; k += 2) {
+        if (k + 2 < k1) fetch(R0, k + 2);
         compute(k);
         commit(R1, k + 1);
         __syncthreads();
-        if (k + 3 < nst) fetch(R1, k + 3);
+        if (k + 3 < k1) fetch(R1, k + 3);
         compute(k + 1);
-        if (k + 2 < nst) commit(R0, k + 2);
+        if (k + 2 < k1) commit(R0, k + 2);
         __syncthreads();
     }
     if (OUT == 2) return;
@@ -376,7 +379,7 @@ void mmq_q4k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const u
         for (int v = 0; v < 16; v++) {
             const int r = row0 + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3);
             if (r < M && tok < N) {
-                if (OUT == 1) ((float*)y)[(int64_t)tok * M + r] = acc[tt][v];
+                if (OUT == 1) ((float*)y)[(int64_t)blockIdx.y * N * M + (int64_t)tok * M + r] = acc[tt][v];
                 else          ((uint16_t*)y)[(int64_t)tok * M + r] = f32_to_f16_bits(acc[tt][v]);
             }
         }
@@ -393,7 +396,7 @@ constexpr int R6_STRIDE = 104;          // LDS bytes per row: ql (64) + qh (32) 
 template <int OUT>   // 0: fp16 y, 1: fp32 y, 2: int32 group dots [N][M][K/16]
 __global__ __launch_bounds__(MMQ_THREADS, 2)
 void mmq_q6k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const uint16_t* __restrict__ codes,
-                    const uint32_t* __restrict__ scl, int M, int N, int K, int Npad) {
+                    const uint32_t* __restrict__ scl, int M, int N, int K, int Npad, int sps) {
     __shared__ __attribute__((aligned(16))) uint8_t sR[2][TM * R6_STRIDE];
     __shared__ __attribute__((aligned(16))) uint8_t sB[2][TN * B_STRIDE];
     __shared__ __attribute__((aligned(16))) _Float16 sSC[2][16 * TM];    // int8 scales as fp16, per [group][row]
@@ -401,6 +404,8 @@ void mmq_q6k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const u
     __shared__ __attribute__((aligned(16))) float sD8[2][8 * TN];        // d8 per [j][token]
 
     const int nb = K / QK_K, nst = 2 * nb;
+    // split-K: this workgroup's stages [k0, k1) (whole super-blocks)
+    const int k0 = 2 * (int)blockIdx.y * sps, k1 = min(nst, k0 + 2 * sps);
     const int n_rt = (M + TM - 1) / TM, n_tt = Npad / TN;
     const int tile = xcd_tile(blockIdx.x, n_rt * n_tt);
     const int row0 = (tile / n_tt) * TM, col0 = (tile % n_tt) * TN;
@@ -491,13 +496,13 @@ void mmq_q6k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const u
     acc[0] = f32x16m{};
     acc[1] = f32x16m{};
 
-    fetch(0);
-    commit(0);
+    fetch(k0);
+    commit(k0);
     __syncthreads();
 #pragma unroll 1
-    for (int k = 0; k < nst; k++) {
+    for (int k = k0; k < k1; k++) {
         const int b = k >> 1, s = k & 1, slot = b & 1;
-        if (k + 1 < nst) fetch(k + 1);
+        if (k + 1 < k1) fetch(k + 1);
         const uint8_t* Rw = &sR[s][arow * R6_STRIDE];
         const uint8_t* B = sB[s];
         f32x16m tmp[2];
@@ -556,7 +561,7 @@ void mmq_q6k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const u
 #pragma unroll
                 for (int v = 0; v < 16; v++) acc[tt][v] = __builtin_fmaf(tmp[tt][v], dA[v >> 2][v & 3], acc[tt][v]);
         }
-        if (k + 1 < nst) commit(k + 1);
+        if (k + 1 < k1) commit(k + 1);
         __syncthreads();
     }
     if (OUT == 2) return;
@@ -567,7 +572,7 @@ void mmq_q6k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const u
         for (int v = 0; v < 16; v++) {
             const int r = row0 + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3);
             if (r < M && tok < N) {
-                if (OUT == 1) ((float*)y)[(int64_t)tok * M + r] = acc[tt][v];
+                if (OUT == 1) ((float*)y)[(int64_t)blockIdx.y * N * M + (int64_t)tok * M + r] = acc[tt][v];
                 else          ((uint16_t*)y)[(int64_t)tok * M + r] = f32_to_f16_bits(acc[tt][v]);
             }
         }
@@ -575,18 +580,70 @@ void mmq_q6k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const u
 }
 
 hipError_t mmq_launch(void* y, const uint8_t* W, int type, const uint16_t* codes, const uint32_t* scl, int M, int N,
-                      int K, int Npad, int out_kind, hipStream_t st) {
+                      int K, int Npad, int out_kind, int splits, hipStream_t st) {
     const int tiles = ((M + TM - 1) / TM) * (Npad / TN);
+    const int nb = K / QK_K;
+    const int sps = (nb + splits - 1) / splits;
+    if (splits < 1 || (splits > 1 && out_kind != 1) || (splits - 1) * sps >= nb) return hipErrorInvalidValue;
+    const dim3 grid(tiles, splits);
     if (type == TYPE_Q4_K) {
-        if (out_kind == 0) hipLaunchKernelGGL(mmq_q4k_kernel<0>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad);
-        else if (out_kind == 1) hipLaunchKernelGGL(mmq_q4k_kernel<1>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad);
-        else hipLaunchKernelGGL(mmq_q4k_kernel<2>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad);
+        if (out_kind == 0) hipLaunchKernelGGL(mmq_q4k_kernel<0>, grid, dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad, sps);
+        else if (out_kind == 1) hipLaunchKernelGGL(mmq_q4k_kernel<1>, grid, dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad, sps);
+        else hipLaunchKernelGGL(mmq_q4k_kernel<2>, grid, dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad, sps);
     } else {
-        if (out_kind == 0) hipLaunchKernelGGL(mmq_q6k_kernel<0>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad);
-        else if (out_kind == 1) hipLaunchKernelGGL(mmq_q6k_kernel<1>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad);
-        else hipLaunchKernelGGL(mmq_q6k_kernel<2>, dim3(tiles), dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad);
+        if (out_kind == 0) hipLaunchKernelGGL(mmq_q6k_kernel<0>, grid, dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad, sps);
+        else if (out_kind == 1) hipLaunchKernelGGL(mmq_q6k_kernel<1>, grid, dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad, sps);
+        else hipLaunchKernelGGL(mmq_q6k_kernel<2>, grid, dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad, sps);
     }
     return hipGetLastError();
+}
+
+// y[i] = sum over s = 0..S-1 (in order) of ws[s][i]; fp16 or fp32 out
+template <int OUT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(void* __restrict__ y, const float* __restrict__ ws,
+                                                            int64_t n, int S) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= n) return;
+    if (i + 4 <= n && (n & 3) == 0) {
+        f32x4m a = *(const f32x4m*)(ws + i);
+        for (int s = 1; s < S; s++) {
+            const f32x4m b = *(const f32x4m*)(ws + (int64_t)s * n + i);
+            a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+        }
+        if (OUT == 1) {
+            *(f32x4m*)((float*)y + i) = a;
+        } else {
+            const u32x2m o = u32x2m{(uint32_t)f32_to_f16_bits(a.x) | ((uint32_t)f32_to_f16_bits(a.y) << 16),
+                                    (uint32_t)f32_to_f16_bits(a.z) | ((uint32_t)f32_to_f16_bits(a.w) << 16)};
+            *(u32x2m*)((uint16_t*)y + i) = o;
+        }
+        return;
+    }
+    for (int64_t e = i; e < i + 4 && e < n; e++) {
+        float a = ws[e];
+        for (int s = 1; s < S; s++) a += ws[(int64_t)s * n + e];
+        if (OUT == 1) ((float*)y)[e] = a;
+        else          ((uint16_t*)y)[e] = f32_to_f16_bits(a);
+    }
+}
+
+hipError_t splitk_reduce_launch(void* y, const float* ws, int64_t n, int splits, int out_kind, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = (n + 1023) / 1024;
+    if (out_kind == 1) hipLaunchKernelGGL(splitk_reduce_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, st, y, ws, n, splits);
+    else               hipLaunchKernelGGL(splitk_reduce_kernel<0>, dim3((unsigned)blocks), dim3(256), 0, st, y, ws, n, splits);
+    return hipGetLastError();
+}
+
+int mmq_splits(int M, int N, int K) {
+    const int64_t tiles = (int64_t)((M + TM - 1) / TM) * ((N + TN - 1) / TN);
+    const int nb = K / QK_K;
+    if (tiles >= 384 || nb < 4) return 1;
+    int S = (int)std::min<int64_t>((512 + tiles - 1) / tiles, 16);
+    S = std::min(S, nb / 2);
+    if (S < 2) return 1;
+    const int sps = (nb + S - 1) / S;
+    return (nb + sps - 1) / sps;
 }
 
 }  // namespace jllm_hip
