@@ -220,6 +220,32 @@ int jllm_hip_gemv_quant_f32_rmsnorm(float* y, const void* W, int type, const uin
     return run("GEMV", a, type == 12, OUT_F32, stream);
 }
 
+// gate/up pair with the SwiGLU in the epilogue: act = half(silu(half(W_gate x)) * half(W_up x))
+static int pair_swiglu(uint16_t* act, const void* Wg, int tg, const void* Wu, int tu, int M, const uint16_t* x,
+                       const void* norm_weight, int weight_fp32, float eps, bool rms, int K, void* stream) {
+    int st = check_common("GEMV", K, x); if (st) return st;
+    if (tg != tu || (tg != 12 && tg != 13)) {
+        fprintf(stderr, "[GEMV] fused SwiGLU pair needs gate and up of one type, Q4_K or Q5_K (got %d, %d)\n", tg, tu);
+        return JLLM_ERR_UNSUPPORTED;
+    }
+    GemvArgs a{}; a.nseg = 2; a.K = K; a.x = x;
+    if (rms && (st = set_rms("GEMV", a, norm_weight, weight_fp32, eps))) return st;
+    if ((st = make_seg("GEMV", a.seg[0], act, Wg, tg, M, nullptr))) return st;
+    if ((st = make_seg("GEMV", a.seg[1], act, Wu, tu, M, nullptr))) return st;
+    return run("GEMV", a, mmvq_pair(tg, tu), OUT_SWIGLU, stream);
+}
+
+int jllm_hip_gemv_quant_pair_swiglu(uint16_t* act, const void* W_gate, int type_gate, const void* W_up, int type_up,
+                                    int M, const uint16_t* x, int K, void* stream) {
+    return pair_swiglu(act, W_gate, type_gate, W_up, type_up, M, x, nullptr, 0, 0.0f, false, K, stream);
+}
+
+int jllm_hip_gemv_quant_pair_rmsnorm_swiglu(uint16_t* act, const void* W_gate, int type_gate, const void* W_up,
+                                            int type_up, int M, const uint16_t* x, const void* norm_weight,
+                                            int weight_fp32, float eps, int K, void* stream) {
+    return pair_swiglu(act, W_gate, type_gate, W_up, type_up, M, x, norm_weight, weight_fp32, eps, true, K, stream);
+}
+
 int jllm_hip_quantize_q8_1(const uint16_t* x, void* y, int K, void* stream) {
     int st = check_common("GEMV", K, x); if (st) return st;
     if (!y || ((uintptr_t)y & 3u)) return JLLM_ERR_INVALID;

@@ -85,10 +85,16 @@ int decode_layer(jllm_hip_decoder* d, int l, int pos, void* st) {
                                         c.kv_int8 ? layer_ks(d, l) : nullptr, c.kv_int8 ? layer_vs(d, l) : nullptr, 0,
                                         st));
     TRY(jllm_hip_gemv_quant_add(d->x2, w.wo, w.type_wo, d->attn, d->x, H, QD, st));
-    // FFN RMSNorm fused into the gate/up GEMV
-    TRY(jllm_hip_gemv_quant_pair_rmsnorm(d->gate, w.w_gate, w.type_w_gate, I, d->up, w.w_up, w.type_w_up, I, d->x2,
-                                         w.rms_ffn, c.norm_fp32, c.rms_eps, H, st));
-    TRY(jllm_hip_fused_swiglu(d->act, d->gate, d->up, 1, I, st));
+    // FFN RMSNorm fused into the gate/up GEMV's staging, SwiGLU into its epilogue
+    // (when gate and up share a Q4_K / Q5_K type; otherwise pair + SwiGLU)
+    if (w.type_w_gate == w.type_w_up && (w.type_w_gate == 12 || w.type_w_gate == 13)) {
+        TRY(jllm_hip_gemv_quant_pair_rmsnorm_swiglu(d->act, w.w_gate, w.type_w_gate, w.w_up, w.type_w_up, I, d->x2,
+                                                    w.rms_ffn, c.norm_fp32, c.rms_eps, H, st));
+    } else {
+        TRY(jllm_hip_gemv_quant_pair_rmsnorm(d->gate, w.w_gate, w.type_w_gate, I, d->up, w.w_up, w.type_w_up, I,
+                                             d->x2, w.rms_ffn, c.norm_fp32, c.rms_eps, H, st));
+        TRY(jllm_hip_fused_swiglu(d->act, d->gate, d->up, 1, I, st));
+    }
     TRY(jllm_hip_gemv_quant_add(d->x, w.w_down, w.type_w_down, d->act, d->x2, H, I, st));
     return JLLM_OK;
 }

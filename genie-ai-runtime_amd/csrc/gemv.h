@@ -6,7 +6,10 @@
 
 namespace jllm_hip {
 
-enum OutKind { OUT_HALF = 0, OUT_F32 = 1, OUT_ADD = 2 };
+// OUT_SWIGLU: a gate/up pair (segments 0 and 1, same M and type) whose rows
+// r are computed by the same wave; y of segment 0 receives
+// half(silu(half(gate_r)) * half(up_r)), segment 1's y is not written.
+enum OutKind { OUT_HALF = 0, OUT_F32 = 1, OUT_ADD = 2, OUT_SWIGLU = 3 };
 
 // Activation prologue applied while the activation is staged: none or
 // RMSNorm of x (x <- half(x / sqrt(mean(x^2) + eps) * w)), with the values
@@ -51,6 +54,7 @@ struct StreamArgs {
     int rows_q[2], rows_r[2];       // rows per wave (quotient, remainder) per type
     int slots_per_wave;     // LDS block slots per wave (max rows per wave * nb)
     int wg_rows;            // residual rows staged per workgroup (waves * max rows per wave)
+    int swiglu;             // OUT_SWIGLU launch: row sequence = the M (gate, up) row pairs
     GemvPre pre;
 };
 

@@ -604,10 +604,24 @@ __device__ __forceinline__ void wave_rows(const StreamArgs& a, int gw, int& g0, 
     g1 = g0 + q + (w < rr ? 1 : 0);
 }
 
-template <int TYPE, int L>
+template <int TYPE, int L, int OUT>
 __device__ __forceinline__ int make_pieces(const StreamArgs& a, int g0, int g1, Piece (&pc)[3]) {
     constexpr int NB = WGeom<TYPE, L>::NBLK;
     int nr = 0, slot = 0;
+    if (OUT == OUT_SWIGLU) {
+        // row pairs [g0, g1): the gate rows, then the same up rows
+#pragma unroll
+        for (int s = 0; s < 3; s++) {
+            pc[s].r0 = s < 2 ? g0 : 0;
+            pc[s].r1 = s < 2 ? g1 : 0;
+            pc[s].slot0 = slot;
+            const int nblk = (pc[s].r1 - pc[s].r0) * a.nb;
+            slot += nblk;
+            pc[s].rounds = (nblk + NB - 1) / NB;
+            nr += pc[s].rounds;
+        }
+        return nr;
+    }
 #pragma unroll
     for (int s = 0; s < 3; s++) {
         pc[s].r0 = max(g0, a.row_off[s]) - a.row_off[s];
@@ -666,7 +680,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
                                           uint16_t* res_lds, int wg_g0) {
     const int nb = a.nb, K = a.K;
     Piece pc[3];
-    const int nr = make_pieces<TYPE, L>(a, g0, g1, pc);
+    const int nr = make_pieces<TYPE, L, OUT>(a, g0, g1, pc);
     u32x4 R0[L], R1[L];
     {
         // activation (and residual) loads first, on every wave, then a barrier,
@@ -775,6 +789,27 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
     // rows: 8 lanes per row add the row's slots (lane j the blocks b = j mod 8,
     // in order), then a fixed butterfly
     const int nrow = g1 - g0, j = lane & 7;
+    if (OUT == OUT_SWIGLU) {
+        for (int t0 = 0; t0 < nrow; t0 += 8) {
+            const int t = t0 + (lane >> 3);
+            float vg = 0.0f, vu = 0.0f;
+            if (t < nrow) {
+                const float* p = slots + t * nb;
+                const float* q = slots + (nrow + t) * nb;
+                for (int b = j; b < nb; b += 8) { vg += p[b]; vu += q[b]; }
+            }
+            vg += dpp_x1(vg); vu += dpp_x1(vu);
+            vg += dpp_x2(vg); vu += dpp_x2(vu);
+            vg += __shfl_xor(vg, 4, 64); vu += __shfl_xor(vu, 4, 64);
+            if (j == 0 && t < nrow) {
+                // half(silu(g) * u) of the half-rounded pair outputs (swiglu_kernel, convert.cu:85-112)
+#pragma clang fp contract(off)
+                const float g = round_to_f16(vg), u = round_to_f16(vu);
+                ((uint16_t*)a.seg[0].y)[g0 + t] = f32_to_f16_bits(g / (1.0f + expf(-g)) * u);
+            }
+        }
+        return;
+    }
     for (int t0 = 0; t0 < nrow; t0 += 8) {
         const int t = t0 + (lane >> 3);
         float v = 0.0f;
@@ -827,8 +862,12 @@ void gemv_stream_kernel(StreamArgs a_in) {
     }
     uint16_t* res_lds = (uint16_t*)(lds + a.xlds_bytes + ST_W * (64 * 16 * L) + ST_W * 4 * a.slots_per_wave);
     // (both bodies hold the same two workgroup barriers)
-    if (q4) wave_body<MMVQ, OUT, TA, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
-    else    wave_body<MMVQ, OUT, TYPE_Q6_K, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
+    if constexpr (OUT == OUT_SWIGLU) {
+        wave_body<MMVQ, OUT, TA, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
+    } else {
+        if (q4) wave_body<MMVQ, OUT, TA, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
+        else    wave_body<MMVQ, OUT, TYPE_Q6_K, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
+    }
 }
 
 template <bool MMVQ, int OUT, int L, int NX, int PRE, int TA>
@@ -872,13 +911,17 @@ constexpr int ST_L = 4;
 
 hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t st) {
     if (out_kind == OUT_ADD && in.nseg != 1) return hipErrorInvalidValue;
+    const bool sw = out_kind == OUT_SWIGLU;
+    if (sw && (in.nseg != 2 || in.seg[0].type != in.seg[1].type || in.seg[0].M != in.seg[1].M ||
+               (in.seg[0].type != TYPE_Q4_K && in.seg[0].type != TYPE_Q5_K)))
+        return hipErrorInvalidValue;
     bool has4 = false, has5 = false;
     for (int i = 0; i < in.nseg; i++) {
         has4 |= in.seg[i].type == TYPE_Q4_K && in.seg[i].M > 0;
         has5 |= in.seg[i].type == TYPE_Q5_K && in.seg[i].M > 0;
     }
     if (has5 && mmvq) return hipErrorInvalidValue;
-    if (has4 && has5) {
+    if (has4 && has5 && !sw) {
         // one launch per first-class type: the Q5_K (and Q6_K) rows, then the Q4_K rows
         GemvArgs p = in, r = in;
         p.nseg = r.nseg = 0;
@@ -903,7 +946,10 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     for (int i = n; i < 3; i++) { a.seg[i] = a.seg[n - 1]; a.seg[i].M = 0; }
     a.row_off[0] = 0;
     for (int i = 0; i < 3; i++) a.row_off[i + 1] = a.row_off[i] + a.seg[i].M;
-    const int64_t rows4 = a.row_off[nseg4], rows6 = a.row_off[3] - rows4;
+    a.swiglu = sw;
+    // OUT_SWIGLU: the row sequence is the M row pairs (two rows' slots per pair)
+    const int64_t rows4 = sw ? in.seg[0].M : a.row_off[nseg4], rows6 = sw ? 0 : a.row_off[3] - rows4;
+    const int64_t slot_rows = sw ? 2 : 1;
     if (rows4 + rows6 <= 0) return hipSuccess;
     a.row_split = (int)rows4;
     const int64_t bytes4 = rows4 * a.nb * (has5 ? Q5K_BYTES : Q4K_BYTES), bytes6 = rows6 * a.nb * Q6K_BYTES;
@@ -926,7 +972,7 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     };
     auto lds_of = [&]() {
         const size_t res = out_kind == OUT_ADD ? (size_t)ST_W * max_rows * 2 : 0;
-        return (size_t)a.xlds_bytes + wbuf + (size_t)ST_W * 4 * max_rows * a.nb + res;
+        return (size_t)a.xlds_bytes + wbuf + (size_t)ST_W * 4 * slot_rows * max_rows * a.nb + res;
     };
     // (the residual rows of a workgroup are staged one per lane)
     auto fits = [&](int per_cu) { return (size_t)per_cu * lds_of() <= LDS_CU && !(out_kind == OUT_ADD && ST_W * max_rows > ST_T); };
@@ -945,7 +991,7 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     a.wave_split = (int)w4;
     a.rows_q[0] = w4 > 0 ? (int)(rows4 / w4) : 0; a.rows_r[0] = w4 > 0 ? (int)(rows4 % w4) : 0;
     a.rows_q[1] = w6 > 0 ? (int)(rows6 / w6) : 0; a.rows_r[1] = w6 > 0 ? (int)(rows6 % w6) : 0;
-    a.slots_per_wave = (int)(max_rows * a.nb);
+    a.slots_per_wave = (int)(slot_rows * max_rows * a.nb);
     a.wg_rows = (int)(ST_W * max_rows);
     const size_t lds = lds_of();
     const int g = (int)grid;
@@ -956,7 +1002,13 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
         if (mmvq && out_kind == OUT_F32)  return launch_nx<true, OUT_F32, ST_L, PRE_RMS>(a, g, lds, st, has5);
         if (!mmvq && out_kind == OUT_F32) return launch_nx<false, OUT_F32, ST_L, PRE_RMS>(a, g, lds, st, has5);
         if (!mmvq && out_kind == OUT_HALF) return launch_nx<false, OUT_HALF, ST_L, PRE_RMS>(a, g, lds, st, has5);
+        if (mmvq && sw) return launch_nx<true, OUT_SWIGLU, ST_L, PRE_RMS>(a, g, lds, st, has5);
+        if (!mmvq && sw) return launch_nx<false, OUT_SWIGLU, ST_L, PRE_RMS>(a, g, lds, st, has5);
         return hipErrorInvalidValue;
+    }
+    if (sw) {
+        if (mmvq) return launch_nx<true, OUT_SWIGLU, ST_L>(a, g, lds, st, has5);
+        return launch_nx<false, OUT_SWIGLU, ST_L>(a, g, lds, st, has5);
     }
     if (mmvq) {
         if (out_kind == OUT_HALF) return launch_nx<true, OUT_HALF, ST_L>(a, g, lds, st, has5);

@@ -28,7 +28,7 @@ extern "C" {
 enum {
     JLLM_OK = 0,
     JLLM_ERR_INVALID = -1,      /* bad size, null or misaligned pointer */
-    JLLM_ERR_UNSUPPORTED = -2,  /* ggml type other than Q4_K / Q6_K     */
+    JLLM_ERR_UNSUPPORTED = -2,  /* ggml type not supported by the call  */
     JLLM_ERR_LAUNCH = -3,       /* the HIP runtime rejected a launch    */
     JLLM_ERR_NOMEM = -4,        /* scratch allocation failed            */
     JLLM_ERR_POINTER = -5       /* weight pointer not visible to the GPU */
@@ -43,8 +43,9 @@ int         jllm_hip_register_mapped_weight_region(const void* host_base, const 
 void        jllm_hip_clear_mapped_weight_region(const void* host_base);
 const void* jllm_hip_resolve_mapped_weight_device_ptr(const void* host_ptr);
 
-/* y[M] (fp16) = W[M x K] . x[K].  Q4_K and Q6_K use the int8 MMVQ path
- * (activation quantised to q8_1).  Replaces gemv_quant, jllm_kernels.h:64
+/* y[M] (fp16) = W[M x K] . x[K]; ggml_type 12 (Q4_K), 13 (Q5_K) or 14
+ * (Q6_K).  Q4_K and Q6_K use the int8 MMVQ path (activation quantised to
+ * q8_1), Q5_K the float-dequant path.  Replaces gemv_quant, jllm_kernels.h:64
  * (dispatch gemv_q4.cu:1245-1306). */
 int jllm_hip_gemv_quant(uint16_t* y, const void* W, int ggml_type, const uint16_t* x,
                         int M, int K, void* stream);
@@ -55,7 +56,9 @@ int jllm_hip_gemv_quant_add(uint16_t* y, const void* W, int ggml_type, const uin
                             const uint16_t* residual, int M, int K, void* stream);
 
 /* Two / three outputs sharing one activation.  MMVQ when both are Q4_K
- * (pair) or all are Q4_K/Q6_K (triple).  Replaces gemv_quant_pair :92 and
+ * (pair) or the types are (Q4_K, Q4_K, Q4_K|Q6_K), (Q6_K, Q6_K, Q6_K) or
+ * (Q6_K, Q4_K, Q4_K) (triple, the reference's instantiations); float
+ * dequant otherwise (any Q5_K).  Replaces gemv_quant_pair :92 and
  * gemv_quant_triple :106 (gemv_q4.cu:1375-1560). */
 int jllm_hip_gemv_quant_pair(uint16_t* y0, const void* W0, int ggml_type0, int M0,
                              uint16_t* y1, const void* W1, int ggml_type1, int M1,
@@ -65,7 +68,7 @@ int jllm_hip_gemv_quant_triple(uint16_t* y0, const void* W0, int ggml_type0, int
                                uint16_t* y2, const void* W2, int ggml_type2, int M2,
                                const uint16_t* x, int K, void* stream);
 
-/* fp32 output.  Q4_K: MMVQ; Q6_K: float dequant.  Replaces gemv_quant_f32,
+/* fp32 output.  Q4_K: MMVQ; Q5_K / Q6_K: float dequant.  Replaces gemv_quant_f32,
  * jllm_kernels.h:148 (gemv_q4.cu:1323-1369). */
 int jllm_hip_gemv_quant_f32(float* y, const void* W, int ggml_type, const uint16_t* x,
                             int M, int K, void* stream);
@@ -98,17 +101,35 @@ int jllm_hip_gemv_quant_pair_rmsnorm(uint16_t* y0, const void* W0, int ggml_type
 int jllm_hip_gemv_quant_f32_rmsnorm(float* y, const void* W, int ggml_type, const uint16_t* x,
                                     const void* norm_weight, int weight_fp32, float eps, int M, int K, void* stream);
 
+/* The decode FFN's gate/up pair with the SwiGLU fused into its epilogue (no
+ * reference counterpart: replaces gemv_quant_pair + swiglu, decode.cu:1234-
+ * 1242).  act[r] = half(silu(g) * u) with g = half(W_gate[r] . x), u =
+ * half(W_up[r] . x): the values of jllm_hip_gemv_quant_pair followed by
+ * jllm_hip_fused_swiglu.  W_gate and W_up: one type, Q4_K or Q5_K (else
+ * JLLM_ERR_UNSUPPORTED), M rows each; the _rmsnorm form normalises x first
+ * as jllm_hip_gemv_quant_pair_rmsnorm does. */
+int jllm_hip_gemv_quant_pair_swiglu(uint16_t* act, const void* W_gate, int type_gate, const void* W_up, int type_up,
+                                    int M, const uint16_t* x, int K, void* stream);
+int jllm_hip_gemv_quant_pair_rmsnorm_swiglu(uint16_t* act, const void* W_gate, int type_gate, const void* W_up,
+                                            int type_up, int M, const uint16_t* x, const void* norm_weight,
+                                            int weight_fp32, float eps, int K, void* stream);
+
 /* q8_1 quantiser in the reference block layout {u16 d, u16 s, i8 qs[32]}
  * (36 B per 32 values).  Replaces quantize_q8_1, gemv_q4.cu:468. */
 int jllm_hip_quantize_q8_1(const uint16_t* x, void* y, int K, void* stream);
 
 /* Batched GEMM y[N x M] (fp16, token-major) = x[N x K] . W^T.  N == 1 routes
- * to jllm_hip_gemv_quant; otherwise the activation is quantised to q8_1 (the
- * reference's DS4 values for Q4_K, D4 for Q6_K) and multiplied on the matrix
- * cores with every 32-weight sub-block (Q4_K) / 16-weight group (Q6_K) dot
- * formed exactly, then scaled as the reference does.  Uses a
- * library-owned q8 scratch buffer (grown on demand, never freed); calls on
- * one device must be serialised (one stream), as in the reference.
+ * to jllm_hip_gemv_quant; otherwise, for Q4_K / Q6_K, the activation is
+ * quantised to q8_1 (the reference's DS4 values for Q4_K, D4 for Q6_K) and
+ * multiplied on the matrix cores with every 32-weight sub-block (Q4_K) /
+ * 16-weight group (Q6_K) dot formed exactly, then scaled as the reference
+ * does; Q5_K multiplies the fp16 activation itself (the reference's float
+ * Q5_K path, gemv_q4.cu:1703-1762) with exact products and fp32 sums.
+ * When the tile grid does not cover the GPU, K is split over workgroups and
+ * the fp32 partials are added in a fixed order (a function of M, ceil(N/64)
+ * and K).  Uses library-owned scratch buffers (q8 codes, split-K partials;
+ * grown on demand, never freed); calls on one device must be serialised
+ * (one stream), as in the reference.
  * Replaces gemm_quant_batched, jllm_kernels.h:135 (gemv_q4.cu:2478-2517),
  * and the internal gemm_q4k_mmq_llama / gemm_q6k_mmq_llama
  * (mmq_q4k_llama.cu:479, mmq_q6k_llama.cu:497). */
@@ -241,15 +262,18 @@ int jllm_hip_qk_norm_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v, 
                                    int kv_int8, void* stream);
 
 /* dst[hidden_dim] (fp16, 16-byte aligned) = dequantised row token_id of a
- * Q4_K / Q6_K embedding table.  Returns a status instead of the reference's
+ * Q4_K / Q6_K embedding table (other types: JLLM_ERR_UNSUPPORTED, as the
+ * reference returns false).  Returns a status instead of the reference's
  * bool.  Replaces dequant_embedding_row, jllm_kernels.h:160
  * (gemv_q4.cu:793-864, :2803-2828). */
 int jllm_hip_dequant_embedding_row(uint16_t* dst, const void* W, int ggml_type, int token_id, int hidden_dim,
                                    void* stream);
 
 /* The same for N tokens whose ids are in DEVICE memory (tokens[N]); an id
- * outside [0, vocab) gives a zero row.  No single reference counterpart: the
- * engine loops dequant_embedding per prompt token (decode.cu:2796-2801);
+ * outside [0, vocab) gives a zero row; Q5_K tables too (the values of the
+ * engine's host Q5_K row dequant, decode.cu:230-266).  No single reference
+ * counterpart: the engine loops dequant_embedding per prompt token
+ * (decode.cu:2796-2801);
  * reading ids on the device lets a greedy decode loop run without a host
  * round trip. */
 int jllm_hip_dequant_embedding_rows(uint16_t* dst, const void* W, int ggml_type, const int32_t* tokens, int N,
@@ -285,7 +309,7 @@ typedef struct {
 } jllm_hip_layer_weights;
 
 typedef struct {
-    const void* tok_embd;  int embd_type;      /* [vocab][hidden] Q4_K/Q6_K (may alias output) */
+    const void* tok_embd;  int embd_type;      /* [vocab][hidden] Q4_K/Q5_K/Q6_K (may alias output) */
     const void* output_norm;                   /* [hidden]                                      */
     const void* output;    int output_type;    /* lm_head [vocab][hidden]                       */
 } jllm_hip_model_weights;

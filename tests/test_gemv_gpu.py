@@ -257,3 +257,56 @@ def test_fused_prologue_argument_checks(dev):
     # K above the single-pass staging limit of the fused RMSNorm
     assert l.jllm_hip_gemv_quant_f32_rmsnorm(jllm._ptr(y), jllm._ptr(W), 12, jllm._ptr(x), jllm._ptr(w), 1,
                                              1e-6, 16, 4352, None) == -1
+
+
+# ---- gate/up pair with the SwiGLU epilogue ----------------------------------------
+
+@pytest.mark.parametrize("t,M,K,rms", [(12, 9728, 2560, True), (12, 9728, 2560, False), (13, 9728, 2560, True),
+                                       (12, 37, 512, False), (13, 1000, 1280, True), (12, 4000, 4096, True)])
+def test_pair_swiglu_matches_pair_then_swiglu(dev, t, M, K, rms):
+    """Bit-identical to the unfused pair (+ RMSNorm) followed by the SwiGLU
+    kernel, and within the GEMV bar of the oracle composition."""
+    print_case("pair_swiglu", t, M, K, rms)
+    g = synth.rng(800 + M + t)
+    x = synth.x_f16(g, K)
+    w = (1.0 + 0.02 * g.standard_normal(K)).astype(np.float32)
+    # block scales 20x below the BASELINE ones, so that silu(g) * u stays in fp16 range
+    mk = (lambda: synth.q4k(g, M, K, 1e-3, 1e-3)) if t == 12 else (lambda: synth.q5k(g, M, K, 5e-4, 1e-3))
+    Wg, Wu = mk(), mk()
+    Wgd, Wud, xd, wd = to_dev(Wg), to_dev(Wu), to_dev(x), to_dev(w)
+    act = empty_f16(M)
+    y0, y1, act2 = empty_f16(M), empty_f16(M), empty_f16(M)
+    if rms:
+        jllm.call("jllm_hip_gemv_quant_pair_rmsnorm_swiglu", act, Wgd, t, Wud, t, M, xd, wd, 1, 1e-6, K)
+        jllm.call("jllm_hip_gemv_quant_pair_rmsnorm", y0, Wgd, t, M, y1, Wud, t, M, xd, wd, 1, 1e-6, K)
+    else:
+        jllm.call("jllm_hip_gemv_quant_pair_swiglu", act, Wgd, t, Wud, t, M, xd, K)
+        jllm.gemv_quant_pair(y0, Wgd, t, M, y1, Wud, t, M, xd, K)
+    jllm.call("jllm_hip_fused_swiglu", act2, y0, y1, 1, M)
+    got = from_dev(act, np.uint16)
+    assert np.array_equal(got, from_dev(act2, np.uint16))
+    xn = oracle.rmsnorm(x, None, w, 1, K, 1e-6, True) if rms else x
+    if t == 12:
+        xq = oracle.quantize_q8_1(xn, K)
+        gy, uy = oracle.mmvq(Wg, t, xq, M, K), oracle.mmvq(Wu, t, xq, M, K)
+    else:
+        gy, uy = oracle.gemv_quant_cpu(Wg, t, xn, M, K), oracle.gemv_quant_cpu(Wu, t, xn, M, K)
+    want = f16_to_f64(oracle.swiglu(gy.astype(np.float16).view(np.uint16), uy.astype(np.float16).view(np.uint16)))
+    # gate/up carry the GEMV bar; silu(g)*u then scales it by at most ~|u| + |g|
+    assert np.all(np.isfinite(want))
+    err = np.abs(f16_to_f64(got) - want)
+    bound = 4 * TOL * np.abs(want).max() + np.abs(want) * 2 ** -9
+    assert np.all(err <= bound), float(err.max())
+
+
+def test_pair_swiglu_rejects_mixed_types(dev):
+    K, M = 512, 64
+    x = to_dev(synth.x_f16(synth.rng(1), K))
+    Wg, Wu = to_dev(synth.q4k(synth.rng(2), M, K)), to_dev(synth.q6k(synth.rng(3), M, K))
+    act = empty_f16(M)
+    l = jllm.lib()
+    assert l.jllm_hip_gemv_quant_pair_swiglu(jllm._ptr(act), jllm._ptr(Wg), 12, jllm._ptr(Wu), 14, M, jllm._ptr(x),
+                                             K, None) == -2     # JLLM_ERR_UNSUPPORTED
+    W6 = to_dev(synth.q6k(synth.rng(4), M, K))
+    assert l.jllm_hip_gemv_quant_pair_swiglu(jllm._ptr(act), jllm._ptr(W6), 14, jllm._ptr(W6), 14, M, jllm._ptr(x),
+                                             K, None) == -2
