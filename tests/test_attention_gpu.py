@@ -140,3 +140,42 @@ def test_fp16_to_int8_known_answer(dev):
     assert abs(s[0] - 0.5 / 127) < 1e-3
     d = from_dev(dst)
     assert np.all(d[:128] == 127) and np.all(d[128:] == -127)
+
+
+def test_attention_repeats_and_graph_replays(dev):
+    """Back-to-back split-K calls sharing the partials scratch, and graph
+    replays of them with eager work in between, give the eager result every
+    time."""
+    ctx = 500                                        # 16 splits
+    print_case("attn_repeat_graph", ctx)
+    q, k, v, ks, vs = _case(11, ctx)
+    qd, kd, vd, ksd, vsd = to_dev(q), to_dev(k), to_dev(v), to_dev(ks), to_dev(vs)
+    outs = [torch.zeros(H * HD, dtype=torch.int16, device=dev) for _ in range(2)]
+
+    def calls():
+        for i, o in enumerate(outs):
+            jllm.call("jllm_hip_flash_attention_decode", o, qd, kd, vd, H, KV, HD, HD, ctx - 37 * i,
+                      1.0 / np.sqrt(HD), 1, ksd, vsd, 0)
+    calls()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    want = f16_to_f64(oracle.attn_decode_int8(q, k, v, H, KV, HD, HD, ctx, 1.0 / np.sqrt(HD), ks, vs, 0,
+                                              oracle.decode_attn_splits(ctx)))
+    assert _close(f16_to_f64(from_dev(eager[0], np.uint16)), want)[0]
+    for _ in range(3):
+        calls()
+    torch.cuda.synchronize()
+    for o, e in zip(outs, eager):
+        assert torch.equal(o, e)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        calls()
+    for r in range(4):
+        for o in outs:
+            o.zero_()
+        gr.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), r
+        calls()                                      # eager work between replays
+        torch.cuda.synchronize()
