@@ -42,4 +42,12 @@ struct DeviceScratch {
     }
 };
 
+// Several batched GEMMs of one activation x [N x K] (the decoder's Q/K/V and
+// gate/up): the activation is quantised once per quantiser kind present
+// (DS4 for Q4_K, D4 for Q6_K; Q5_K needs none), then each product runs as
+// jllm_hip_gemm_quant_batched would (fp16 out).  Types and shapes are
+// checked as there.
+struct GemmOut { uint16_t* y; const void* W; int type; int M; };
+int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uint16_t* x, int N, int K, void* stream);
+
 }  // namespace jllm_hip

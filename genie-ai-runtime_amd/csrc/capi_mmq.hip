@@ -29,15 +29,10 @@ int check_gemm(const char* tag, const void* y, int type, const uint16_t* x, int 
     return JLLM_OK;
 }
 
-int run_mmq(const char* tag, void* y, const void* W, int type, const uint16_t* x, int M, int N, int K,
-            int out_kind, void* stream) {
-    const void* Wd = resolve_weight(W);
-    if (!Wd) {
-        fprintf(stderr, "[%s] weight pointer %p is not device-visible (no host fallback)\n", tag, W);
-        return JLLM_ERR_POINTER;
-    }
-    if (!aligned16(Wd)) return JLLM_ERR_INVALID;
-    hipStream_t st = (hipStream_t)stream;
+// The product of an already quantised activation (q8 = codes + scale words
+// of the right kind, or null for Q5_K) into y.
+int mmq_after_quant(const char* tag, void* y, const void* Wd, int type, const uint16_t* x, const uint16_t* codes,
+                    const uint32_t* scl, int M, int N, int K, int out_kind, hipStream_t st) {
     // split-K when the tile grid alone does not cover the chip: partials to
     // the workspace, then one ordered reduction into y
     const int splits = out_kind == 2 ? 1 : mmq_splits(M, N, K);
@@ -51,25 +46,91 @@ int run_mmq(const char* tag, void* y, const void* W, int type, const uint16_t* x
     }
     const int kind = splits > 1 ? 1 : out_kind;
     hipError_t e;
-    if (type == 13) {
-        e = gemm_q5k_launch(dst, (const uint8_t*)Wd, x, M, N, K, kind, splits, st);
-    } else {
-        const int Npad = npad_of(N);
-        const size_t cb = mmq_codes_bytes(K, Npad);
-        uint8_t* q8 = (uint8_t*)g_q8.get(cb + mmq_scales_bytes(K, Npad));
-        if (!q8) {
-            fprintf(stderr, "[%s] q8 scratch allocation failed\n", tag);
-            return JLLM_ERR_NOMEM;
-        }
-        uint16_t* codes = (uint16_t*)q8;
-        uint32_t* scl = (uint32_t*)(q8 + cb);
-        e = quantize_mmq_f16_launch(x, codes, scl, N, K, Npad, type == 12, st);
-        if (e == hipSuccess) e = mmq_launch(dst, (const uint8_t*)Wd, type, codes, scl, M, N, K, Npad, kind, splits, st);
-    }
+    if (type == 13) e = gemm_q5k_launch(dst, (const uint8_t*)Wd, x, M, N, K, kind, splits, st);
+    else e = mmq_launch(dst, (const uint8_t*)Wd, type, codes, scl, M, N, K, npad_of(N), kind, splits, st);
     if (e == hipSuccess && splits > 1) e = splitk_reduce_launch(y, (const float*)dst, (int64_t)N * M, splits, out_kind, st);
     return launch_status(e, tag);
 }
+
+const void* device_weight(const char* tag, const void* W) {
+    const void* Wd = resolve_weight(W);
+    if (!Wd) fprintf(stderr, "[%s] weight pointer %p is not device-visible (no host fallback)\n", tag, W);
+    return Wd;
+}
+
+// q8 scratch: codes, then the scale words of up to two quantiser kinds
+int q8_scratch(const char* tag, int N, int K, uint16_t*& codes, uint32_t* (&scl)[2]) {
+    const int Npad = npad_of(N);
+    const size_t cb = mmq_codes_bytes(K, Npad), sb = mmq_scales_bytes(K, Npad);
+    uint8_t* q8 = (uint8_t*)g_q8.get(cb + 2 * sb);
+    if (!q8) {
+        fprintf(stderr, "[%s] q8 scratch allocation failed\n", tag);
+        return JLLM_ERR_NOMEM;
+    }
+    codes = (uint16_t*)q8;
+    scl[0] = (uint32_t*)(q8 + cb);
+    scl[1] = (uint32_t*)(q8 + cb + sb);
+    return JLLM_OK;
+}
+
+int run_mmq(const char* tag, void* y, const void* W, int type, const uint16_t* x, int M, int N, int K,
+            int out_kind, void* stream) {
+    const void* Wd = device_weight(tag, W);
+    if (!Wd) return JLLM_ERR_POINTER;
+    if (!aligned16(Wd)) return JLLM_ERR_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    uint16_t* codes = nullptr;
+    uint32_t* scl[2] = {nullptr, nullptr};
+    if (type != 13) {
+        int r = q8_scratch(tag, N, K, codes, scl); if (r) return r;
+        const hipError_t e = quantize_mmq_f16_launch(x, codes, scl[0], N, K, npad_of(N), type == 12, st);
+        if (e != hipSuccess) return launch_status(e, tag);
+    }
+    return mmq_after_quant(tag, y, Wd, type, x, codes, scl[0], M, N, K, out_kind, st);
+}
 }  // namespace
+
+namespace jllm_hip {
+int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uint16_t* x, int N, int K, void* stream) {
+    for (int i = 0; i < n; i++) {
+        int st = check_gemm(tag, outs[i].y, outs[i].type, x, outs[i].M, N, K, true); if (st) return st;
+    }
+    if (N == 0) return JLLM_OK;
+    if (N == 1) {
+        for (int i = 0; i < n; i++) {
+            int st = jllm_hip_gemv_quant(outs[i].y, outs[i].W, outs[i].type, x, outs[i].M, K, stream); if (st) return st;
+        }
+        return JLLM_OK;
+    }
+    hipStream_t hs = (hipStream_t)stream;
+    uint16_t* codes = nullptr;
+    uint32_t* scl[2] = {nullptr, nullptr};
+    bool need[2] = {false, false};                   // DS4 (Q4_K), D4 (Q6_K)
+    for (int i = 0; i < n; i++) {
+        if (outs[i].M == 0) continue;
+        if (outs[i].type == 12) need[0] = true;
+        if (outs[i].type == 14) need[1] = true;
+    }
+    if (need[0] || need[1]) {
+        int st = q8_scratch(tag, N, K, codes, scl); if (st) return st;
+        for (int k = 0; k < 2; k++) {
+            if (!need[k]) continue;
+            const hipError_t e = quantize_mmq_f16_launch(x, codes, scl[k], N, K, npad_of(N), k == 0, hs);
+            if (e != hipSuccess) return launch_status(e, tag);
+        }
+    }
+    for (int i = 0; i < n; i++) {
+        if (outs[i].M == 0) continue;
+        const void* Wd = device_weight(tag, outs[i].W);
+        if (!Wd) return JLLM_ERR_POINTER;
+        if (!aligned16(Wd)) return JLLM_ERR_INVALID;
+        const uint32_t* sc = outs[i].type == 12 ? scl[0] : scl[1];
+        int st = mmq_after_quant(tag, outs[i].y, Wd, outs[i].type, x, codes, sc, outs[i].M, N, K, 0, hs);
+        if (st) return st;
+    }
+    return JLLM_OK;
+}
+}  // namespace jllm_hip
 
 extern "C" {
 
@@ -92,6 +153,15 @@ int jllm_hip_quantize_mmq_q8_1(const uint16_t* x, void* q8, int N, int K, int Np
     if (!x || !q8 || N < 0 || K <= 0 || K % 128 != 0 || Npad < N || Npad % MMQ_REF_NPAD != 0) return JLLM_ERR_INVALID;
     if (Npad == 0) return JLLM_OK;
     return launch_status(quantize_mmq_launch(x, q8, N, K, Npad, ds4 != 0, (hipStream_t)stream), "GEMM");
+}
+
+int jllm_hip_quantize_mmq_f16(const uint16_t* x, uint16_t* codes, uint32_t* scales, int N, int K, int Npad, int ds4,
+                              void* stream) {
+    if (!x || !codes || !scales || N < 0 || K <= 0 || K % 256 != 0 || Npad < N || Npad % MMQ_TILE_N != 0 ||
+        !aligned16(x) || !aligned16(codes))
+        return JLLM_ERR_INVALID;
+    if (Npad == 0) return JLLM_OK;
+    return launch_status(quantize_mmq_f16_launch(x, codes, scales, N, K, Npad, ds4 != 0, (hipStream_t)stream), "GEMM");
 }
 
 int jllm_hip_mmq_subdots(int32_t* out, const void* W, int type, const uint16_t* x, int M, int N, int K,

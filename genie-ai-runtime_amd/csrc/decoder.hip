@@ -26,6 +26,8 @@
 #include "capi_common.h"
 
 using jllm_hip::launch_status;
+using jllm_hip::GemmOut;
+using jllm_hip::gemm_batched_shared_x;
 
 struct jllm_hip_decoder {
     jllm_hip_decoder_config cfg;
@@ -107,9 +109,9 @@ int prefill_layer(jllm_hip_decoder* d, int l, int start, int N, void* st) {
     const int H = c.hidden_dim, QD = c.n_heads * c.head_dim, KVD = c.n_kv_heads * c.head_dim, I = c.intermediate_dim;
     const size_t row = (size_t)KVD * (c.kv_int8 ? 1 : 2);
     TRY(jllm_hip_fused_rmsnorm_residual(d->normed, d->x, nullptr, w.rms_attn, N, H, c.rms_eps, c.norm_fp32, st));
-    TRY(jllm_hip_gemm_quant_batched(d->q, w.wq, w.type_wq, d->normed, QD, N, H, st));
-    TRY(jllm_hip_gemm_quant_batched(d->k, w.wk, w.type_wk, d->normed, KVD, N, H, st));
-    TRY(jllm_hip_gemm_quant_batched(d->v, w.wv, w.type_wv, d->normed, KVD, N, H, st));
+    // Q, K, V of one quantised activation
+    const GemmOut qkv[3] = {{d->q, w.wq, w.type_wq, QD}, {d->k, w.wk, w.type_wk, KVD}, {d->v, w.wv, w.type_wv, KVD}};
+    TRY(gemm_batched_shared_x("decoder", qkv, 3, d->normed, N, H, st));
     TRY(jllm_hip_qk_norm_rope_store_kv(d->q, d->k, d->v, w.q_norm, w.k_norm, c.qk_norm_fp32, c.rms_eps,
                                        layer_k(d, l) + (size_t)start * row, layer_v(d, l) + (size_t)start * row,
                                        layer_ks(d, l) + (size_t)start * c.n_kv_heads,
@@ -122,8 +124,8 @@ int prefill_layer(jllm_hip_decoder* d, int l, int start, int N, void* st) {
     TRY(jllm_hip_gemm_quant_batched(d->proj, w.wo, w.type_wo, d->attn, H, N, QD, st));
     TRY(jllm_hip_vec_add(d->x2, d->x, d->proj, (int64_t)N * H, st));
     TRY(jllm_hip_fused_rmsnorm_residual(d->normed, d->x2, nullptr, w.rms_ffn, N, H, c.rms_eps, c.norm_fp32, st));
-    TRY(jllm_hip_gemm_quant_batched(d->gate, w.w_gate, w.type_w_gate, d->normed, I, N, H, st));
-    TRY(jllm_hip_gemm_quant_batched(d->up, w.w_up, w.type_w_up, d->normed, I, N, H, st));
+    const GemmOut gu[2] = {{d->gate, w.w_gate, w.type_w_gate, I}, {d->up, w.w_up, w.type_w_up, I}};
+    TRY(gemm_batched_shared_x("decoder", gu, 2, d->normed, N, H, st));
     TRY(jllm_hip_fused_swiglu(d->act, d->gate, d->up, N, I, st));
     TRY(jllm_hip_gemm_quant_batched(d->proj, w.w_down, w.type_w_down, d->act, H, N, I, st));
     TRY(jllm_hip_vec_add(d->x, d->x2, d->proj, (int64_t)N * H, st));

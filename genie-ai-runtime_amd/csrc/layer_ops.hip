@@ -408,45 +408,74 @@ hipError_t embed_launch(uint16_t* dst, const void* W, int type, const int32_t* t
 
 // ---------------------------------------------------------------------------
 // Greedy argmax over fp32 logits: the lowest index of the largest finite
-// value (0 when none is finite), i.e. the host loop of sample_greedy run as
-// one 1024-thread workgroup (float4 loads over the aligned body).
+// value (0 when none is finite), i.e. the host loop of sample_greedy.  Two
+// launches: AM_BLOCKS workgroups each reduce a contiguous chunk (float4
+// loads over the aligned body) to one (value, index) candidate in a
+// file-scope device array, then one wave merges the candidates in index
+// order.  Calls on one device share that array: they must be serialised
+// (one stream), like the library's other scratch users.
+constexpr int AM_BLOCKS = 128, AM_THREADS = 256;
+__device__ float g_am_val[AM_BLOCKS];
+__device__ int g_am_idx[AM_BLOCKS];
+
 __device__ __forceinline__ void arg_better(float v, int i, float& bv, int& bi) {
     if (isfinite(v) && (v > bv || (v == bv && i < bi))) { bv = v; bi = i; }
 }
+__device__ __forceinline__ void arg_merge(float ov, int oi, float& bv, int& bi) {
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
 
-__global__ __launch_bounds__(1024) void argmax_kernel(int32_t* out, const float* __restrict__ x, int n) {
-    __shared__ float sv[16];
-    __shared__ int si[16];
+__global__ __launch_bounds__(AM_THREADS) void argmax_part_kernel(const float* __restrict__ x, int n, int chunk) {
+    __shared__ float sv[AM_THREADS / 64];
+    __shared__ int si[AM_THREADS / 64];
     const int t = threadIdx.x;
+    const int b0 = blockIdx.x * chunk, b1 = min(n, b0 + chunk);      // chunk is a multiple of 4
     float bv = -INFINITY;
     int bi = INT_MAX;
-    const bool v4 = ((uintptr_t)x & 15) == 0;
-    const int n4 = v4 ? n / 4 : 0;
-    for (int j = t; j < n4; j += 1024) {
-        const float4 f = ((const float4*)x)[j];
-        arg_better(f.x, 4 * j, bv, bi);
-        arg_better(f.y, 4 * j + 1, bv, bi);
-        arg_better(f.z, 4 * j + 2, bv, bi);
-        arg_better(f.w, 4 * j + 3, bv, bi);
+    if (((uintptr_t)x & 15) == 0) {
+        const int q1 = b0 + ((b1 - b0) & ~3);
+        for (int j = b0 + 4 * t; j < q1; j += 4 * AM_THREADS) {
+            const float4 f = *(const float4*)(x + j);
+            arg_better(f.x, j, bv, bi);
+            arg_better(f.y, j + 1, bv, bi);
+            arg_better(f.z, j + 2, bv, bi);
+            arg_better(f.w, j + 3, bv, bi);
+        }
+        for (int j = q1 + t; j < b1; j += AM_THREADS) arg_better(x[j], j, bv, bi);
+    } else {
+        for (int j = b0 + t; j < b1; j += AM_THREADS) arg_better(x[j], j, bv, bi);
     }
-    for (int j = 4 * n4 + t; j < n; j += 1024) arg_better(x[j], j, bv, bi);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
+    for (int o = 32; o > 0; o >>= 1) arg_merge(__shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64), bv, bi);
     if ((t & 63) == 0) { sv[t >> 6] = bv; si[t >> 6] = bi; }
     __syncthreads();
     if (t == 0) {
-        for (int w = 1; w < 16; w++)
-            if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) { bv = sv[w]; bi = si[w]; }
-        out[0] = bi == INT_MAX ? 0 : bi;
+        for (int w = 1; w < AM_THREADS / 64; w++) arg_merge(sv[w], si[w], bv, bi);
+        g_am_val[blockIdx.x] = bv;
+        g_am_idx[blockIdx.x] = bi;
     }
 }
 
+__global__ __launch_bounds__(64) void argmax_final_kernel(int32_t* out, int nblocks) {
+    const int t = threadIdx.x;
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+    for (int b = t; b < nblocks; b += 64) arg_merge(g_am_val[b], g_am_idx[b], bv, bi);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) arg_merge(__shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64), bv, bi);
+    if (t == 0) out[0] = bi == INT_MAX ? 0 : bi;
+}
+
 hipError_t argmax_launch(int32_t* out, const float* x, int n, hipStream_t st) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, st, out, x, n);
+    if (n <= 0) return hipErrorInvalidValue;
+    // chunks of a multiple of 4 elements (16-byte aligned starts when x is)
+    int chunk = (n + AM_BLOCKS - 1) / AM_BLOCKS;
+    chunk = (chunk + 3) & ~3;
+    const int nblocks = (n + chunk - 1) / chunk;
+    hipLaunchKernelGGL(argmax_part_kernel, dim3(nblocks), dim3(AM_THREADS), 0, st, x, n, chunk);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(64), 0, st, out, nblocks);
     return hipGetLastError();
 }
 

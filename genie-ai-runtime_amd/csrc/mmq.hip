@@ -95,35 +95,62 @@ hipError_t quantize_mmq_launch(const uint16_t* x, void* q8, int N, int K, int Np
 // layout the MMQ kernels read: codes as fp16 values, [K/256][Npad][256], and
 // one 32-bit scale word per 32 values, [K/32][Npad] (DS4: half d | half sum
 // << 16; D4: float d).  One thread per value, 32 lanes per block.
+// Four lanes per 32-value block, 8 values (one 16-byte load) per lane.  The
+// block sum is added in the order of a 32-lane butterfly (xor 16, 8, 4, 2,
+// 1 over the value index), the order of the reference-layout quantiser
+// above: index bit 4 pairs lanes sub ^ 2, bit 3 lanes sub ^ 1, bits 2..0
+// stay within the lane -- so d and the sum are the same floats.
 __global__ __launch_bounds__(256) void quantize_mmq_f16_kernel(const uint16_t* __restrict__ x,
                                                                uint16_t* __restrict__ codes,
                                                                uint32_t* __restrict__ scl, int N, int K, int Npad,
                                                                int ds4) {
-    const int blk = blockIdx.x * 8 + (threadIdx.x >> 5);       // (kb32, col)
-    const int nblk = (K / 32) * Npad;
-    if (blk >= nblk) return;                                   // whole 32-lane groups exit together
-    const int kb32 = blk / Npad, col = blk % Npad, lane = threadIdx.x & 31;
-    const float v = col < N ? f16_bits_to_f32(x[(int64_t)col * K + kb32 * 32 + lane]) : 0.0f;
-    float amax = fabsf(v), sum = v;
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-        sum += __shfl_xor(sum, o, 64);
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;     // (col, kb32, sub), sub fastest
+    const int kb = K / 32;
+    const int64_t nthr = (int64_t)Npad * kb * 4;
+    if (gid >= nthr) return;                                          // whole 4-lane groups exit together
+    const int sub = (int)(gid & 3);
+    const int64_t cb = gid >> 2;
+    const int kb32 = (int)(cb % kb), col = (int)(cb / kb);
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    if (col < N) {
+        const u32x4m u = *(const u32x4m*)(x + (int64_t)col * K + kb32 * 32 + 8 * sub);
+        w[0] = u.x; w[1] = u.y; w[2] = u.z; w[3] = u.w;
     }
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; e++) { v[2 * e] = f16_bits_to_f32(w[e] & 0xFFFFu); v[2 * e + 1] = f16_bits_to_f32(w[e] >> 16); }
+    float amax = 0.0f, t[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) { amax = fmaxf(amax, fabsf(v[e])); t[e] = v[e]; }
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+#pragma unroll
+    for (int e = 0; e < 8; e++) t[e] += __shfl_xor(t[e], 2, 64);       // index bit 4
+#pragma unroll
+    for (int e = 0; e < 8; e++) t[e] += __shfl_xor(t[e], 1, 64);       // index bit 3
+    const float s2[4] = {t[0] + t[4], t[1] + t[5], t[2] + t[6], t[3] + t[7]};
+    const float s1[2] = {s2[0] + s2[2], s2[1] + s2[3]};
+    const float sum = s1[0] + s1[1];
     const float d = amax / 127.0f;
     const float dinv = d > 0.0f ? 1.0f / d : 0.0f;
-    const int q = (int)__builtin_rintf(v * dinv);
-    codes[((int64_t)(kb32 >> 3) * Npad + col) * 256 + (kb32 & 7) * 32 + lane] = f32_to_f16_bits((float)q);
-    if (lane == 0)
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int q0 = (int)__builtin_rintf(v[2 * e] * dinv), q1 = (int)__builtin_rintf(v[2 * e + 1] * dinv);
+        o[e] = (uint32_t)f32_to_f16_bits((float)q0) | ((uint32_t)f32_to_f16_bits((float)q1) << 16);
+    }
+    *(u32x4m*)(codes + ((int64_t)(kb32 >> 3) * Npad + col) * 256 + (kb32 & 7) * 32 + 8 * sub) =
+        u32x4m{o[0], o[1], o[2], o[3]};
+    if (sub == 0)
         scl[(int64_t)kb32 * Npad + col] =
             ds4 ? ((uint32_t)f32_to_f16_bits(d) | ((uint32_t)f32_to_f16_bits(sum) << 16)) : __builtin_bit_cast(uint32_t, d);
 }
 
 hipError_t quantize_mmq_f16_launch(const uint16_t* x, uint16_t* codes, uint32_t* scl, int N, int K, int Npad,
                                    bool ds4, hipStream_t st) {
-    const int nblk = (K / 32) * Npad;
-    hipLaunchKernelGGL(quantize_mmq_f16_kernel, dim3((nblk + 7) / 8), dim3(256), 0, st, x, codes, scl, N, K, Npad,
-                       ds4 ? 1 : 0);
+    const int64_t nthr = (int64_t)Npad * (K / 32) * 4;
+    hipLaunchKernelGGL(quantize_mmq_f16_kernel, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, st, x, codes, scl,
+                       N, K, Npad, ds4 ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -148,6 +148,15 @@ int jllm_hip_gemm_quant_batched_f32(float* y, const void* W, int ggml_type, cons
  * Npad is a multiple of 64 and >= N; columns >= N are written as zeros. */
 int jllm_hip_quantize_mmq_q8_1(const uint16_t* x, void* q8, int N, int K, int Npad, int ds4, void* stream);
 
+/* The production MMQ kernels' activation quantiser (same codes and scales
+ * as jllm_hip_quantize_mmq_q8_1, in the kernels' layout): codes fp16
+ * [K/256][Npad][256] (integers -127..127), scale words [K/32][Npad] (ds4:
+ * half d | half sum << 16; else float d).  K a multiple of 256, Npad a
+ * multiple of 64, x and codes 16-byte aligned.  No reference counterpart;
+ * exposed so the layout can be checked against the reference quantiser. */
+int jllm_hip_quantize_mmq_f16(const uint16_t* x, uint16_t* codes, uint32_t* scales, int N, int K, int Npad, int ds4,
+                              void* stream);
+
 /* Test hook: the exact sub-block dots the production MMQ kernels form,
  * out [N][M][K/G] int32 (G = 32 for Q4_K sub-blocks, 16 for Q6_K groups),
  * for activations x [N x K] quantised by the production quantiser.  No
@@ -281,7 +290,9 @@ int jllm_hip_dequant_embedding_rows(uint16_t* dst, const void* W, int ggml_type,
 
 /* out[0] (device int32) = the lowest index of the largest finite logit (0
  * when none is finite).  The GPU form of the host greedy sampler
- * sample_greedy, src/engine/sample.cpp:160-170. */
+ * sample_greedy, src/engine/sample.cpp:160-170.  Two launches sharing a
+ * small library-owned device array of per-chunk candidates: calls on one
+ * device must be serialised (one stream). */
 int jllm_hip_argmax_f32(int32_t* out, const float* logits, int n, void* stream);
 
 /* ---- decoder loop (the engine-side caller of the kernels above) ---- */

@@ -38,6 +38,30 @@ def test_quantize_mmq_bit_exact(dev, ds4, N, K):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("ds4", [True, False])
+@pytest.mark.parametrize("N,K", [(1, 256), (70, 512), (130, 2560)])
+def test_kernel_layout_quantizer_matches_reference_layout(dev, ds4, N, K):
+    """The production quantiser (fp16 codes, packed scale words) holds the
+    same codes, d and sum bits as the reference-layout quantiser (which is
+    bit-exact against the oracle)."""
+    print_case("quantize_mmq_f16", ds4, N, K)
+    x = synth.x_f16(synth.rng(N + K + ds4), (N, K))
+    x[0, 32:64] = 0
+    Npad = _npad(N)
+    codes = torch.zeros(K * Npad, dtype=torch.int16, device=dev)
+    scl = torch.zeros(K // 32 * Npad, dtype=torch.int32, device=dev)
+    jllm.call("jllm_hip_quantize_mmq_f16", to_dev(x), codes, scl, N, K, Npad, 1 if ds4 else 0)
+    c = f16_to_f64(from_dev(codes, np.uint16)).reshape(K // 256, Npad, 256)
+    sw = from_dev(scl).view(np.uint32).reshape(K // 32, Npad)
+    ref = oracle.quantize_mmq(x, N, K, Npad, ds4).reshape(K // 128, Npad, 144)
+    rq = ref[:, :, 16:].view(np.int8).astype(np.float64)           # [K/128][Npad][128]
+    want_c = rq.reshape(K // 256, 2, Npad, 128).transpose(0, 2, 1, 3).reshape(K // 256, Npad, 256)
+    assert np.array_equal(c, want_c)
+    rs = ref[:, :, 0:16].copy().view(np.uint32)                    # [K/128][Npad][4]
+    want_s = rs.transpose(0, 2, 1).reshape(K // 32, Npad)
+    assert np.array_equal(sw, want_s)
+
+
 @pytest.mark.parametrize("t", [12, 14])
 @pytest.mark.parametrize("M,N,K", [(128, 64, 256), (200, 70, 512), (33, 5, 2560), (64, 129, 768)])
 def test_mmq_int32_dots_bit_exact(dev, t, M, N, K):
