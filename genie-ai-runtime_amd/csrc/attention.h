@@ -19,10 +19,14 @@ struct AttnArgs {
     // query tokens (grid z): token t attends to keys [0, seq + t) and reads
     // q / writes out at t * n_heads * head_dim.  tokens > 1 needs n_splits 1.
     int tokens;
+    // query tokens per wave (prefill): the wave's columns are tq tokens x
+    // the G heads of its KV head, tq * G <= ATTN_MAX_COLUMNS; 1 for decode.
+    int tq;
 
 };
 
 constexpr int ATTN_MAX_SPLITS = 256;
+constexpr int ATTN_MAX_COLUMNS = 16;   // (token, head) columns per wave
 int attn_splits(int seq_len, int n_kv);
 size_t attn_partials_floats(int n_heads, int n_splits, int head_dim);
 // Scratch layout: ATTN_COUNTER_BYTES of per-KV-head counters (fixed offset,

@@ -13,9 +13,11 @@
 //
 // Prefill (flash_attention_prefill_batched_kernel, attention.cu:382-514)
 // is the same computation per query token t with the causal bound
-// seq = start_pos + t + 1: grid z runs over the tokens, one split each, and
-// the wave writes its normalised output directly (no partials, no reduce);
-// a decode call with a single split does the same.
+// seq = start_pos + t + 1: grid z runs over blocks of tq tokens, one split
+// each; a wave's MFMA columns are its tq tokens x G heads (each column with
+// its own causal bound, so a K/V tile read once serves all of them) and the
+// wave writes the normalised outputs directly (no partials, no reduce); a
+// decode call with a single split does the same for its one token.
 //
 // MI355X mapping: one wave64 per (KV head, split[, token]) computes ALL
 // query heads of its GQA group, so each KV byte is read from HBM once.
@@ -86,14 +88,18 @@ size_t attn_scratch_bytes(int n_heads, int n_splits, int head_dim) {
     return ATTN_COUNTER_BYTES + attn_partials_floats(n_heads, n_splits, head_dim) * sizeof(float);
 }
 
-__host__ __device__ size_t attn_lds_bytes(int n_heads, int n_kv, int head_dim) {
-    const int G = n_heads / n_kv;
+__host__ __device__ size_t attn_lds_bytes(int n_heads, int n_kv, int head_dim, int tq) {
+    const int G = n_heads / n_kv * tq;                                // columns of a wave
     const size_t loop = (size_t)32 * AT_KEYS * 2 + 96 * 4;            // P' rows (fp16) + corr/ks/vs
     const size_t outb = (size_t)2 * G * head_dim * 4;                 // final hi/lo rows (fp32)
     return loop > outb ? loop : outb;
 }
 
-// One wave per (KV head, split).  Lane (li = lane & 31, lg = lane >> 5).
+// One wave per (KV head, split[, block of tq query tokens]).  The wave's
+// "columns" are its (token, head) pairs: column c = token tok0 + c / G, head
+// kvh * G + c % G, GC = tq * G <= 16 of them; each has its own causal bound
+// (and window), so one key tile serves tq tokens.  Lane (li = lane & 31,
+// lg = lane >> 5); below, "head li" means column li.
 //   Q.K^T : C = K.q^T (rows = the tile's 32 keys, cols = query heads, K = d);
 //           lane group lg covers d in [lg*hd/2, (lg+1)*hd/2), 8 at a time
 //   V^T   : the V rows are turned into columns on the matrix cores: with A =
@@ -104,7 +110,9 @@ __host__ __device__ size_t attn_lds_bytes(int n_heads, int n_kv, int head_dim) {
 //           order the transpose delivers them), B = those V columns
 // The K and V rows of the next tile are loaded into registers while the
 // current tile is computed.
-template <bool INT8, int HD>
+// MT: several query tokens per wave (per-column causal bounds); the
+// single-token form (decode, or tq == 1) compiles without the column masks.
+template <bool INT8, int HD, bool MT>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_partial_kernel(AttnArgs a) {
     constexpr int EB = INT8 ? 1 : 2;
@@ -114,13 +122,19 @@ void attn_partial_kernel(AttnArgs a) {
     constexpr int VW = NDT * EB;                        // V: 16-byte chunks per lane
     constexpr int NST = half / 8;                       // Q.K^T MFMA steps
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int kvh = blockIdx.x, split = blockIdx.y, tok = blockIdx.z;
+    const int kvh = blockIdx.x, split = blockIdx.y, tok0 = MT ? blockIdx.z * a.tq : blockIdx.z;
     const int G = a.n_heads / a.n_kv;
-    const int seq = a.seq + tok;
-    const uint16_t* qt = a.q + (int64_t)tok * a.n_heads * hd;
+    const int ntok = MT ? min(a.tq, a.tokens - tok0) : 1;       // tokens of this wave
+    const int GC = ntok * G;                                    // live columns
     const int l = threadIdx.x, li = l & 31, lg = l >> 5;
+    // column li: its token, causal bound and window start
+    const int ctok = MT ? tok0 + (li < GC ? li / G : 0) : tok0;
+    const int seq_c = a.seq + ctok;
+    const int lo_c = a.window > 0 ? max(0, seq_c - a.window) : 0;
+    // the wave's key range covers every column's
+    const int seq = a.seq + tok0 + ntok - 1;
     const int kv_dim = a.n_kv * a.cache_head_dim, hoff = kvh * a.cache_head_dim;
-    const int lo_pos = a.window > 0 ? max(0, seq - a.window) : 0;
+    const int lo_pos = a.window > 0 ? max(0, a.seq + tok0 - a.window) : 0;
     const int span = seq - lo_pos;
     const int S = a.n_splits;
     const int per = (span + S - 1) / S;
@@ -134,8 +148,9 @@ void attn_partial_kernel(AttnArgs a) {
     h8 qa[NST];
 #pragma unroll
     for (int st = 0; st < NST; st++)
-        qa[st] = li < G ? __builtin_bit_cast(h8, *(const u32x4a*)(qt + (int64_t)(kvh * G + li) * hd + lg * half + 8 * st))
-                        : h8{};
+        qa[st] = li < GC ? __builtin_bit_cast(h8, *(const u32x4a*)(a.q + (int64_t)ctok * a.n_heads * hd +
+                                                                    (int64_t)(kvh * G + li % G) * hd + lg * half + 8 * st))
+                         : h8{};
     for (int i = l; i < 32 * AT_KEYS; i += 64) sP[i] = (_Float16)0.0f;
 
     // identity operands of the V transpose.  int8: lane (col li, lg) holds
@@ -154,7 +169,7 @@ void attn_partial_kernel(AttnArgs a) {
             for (int e = 0; e < 8; e++) eyeh[hh][e] = (_Float16)((16 * hh + 8 * lg + e == li) ? 1.0f : 0.0f);
     }
 
-    // running softmax state of head li (meaningful in lanes li < G; both
+    // running softmax state of column li (meaningful in lanes li < GC; both
     // lane halves keep identical copies)
     float run_m = -FLT_MAX, run_l = 0.0f;
     f32x16 acc[NDT];
@@ -211,12 +226,14 @@ void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; r++) { kscl[4 * m4 + r] = k4[r]; vscl[4 * m4 + r] = v4[r]; }
         }
-        // 2. online softmax for head li (lanes li < G do the useful work)
+        // 2. online softmax for column li (lanes li < GC do the useful work)
         float mx = -FLT_MAX;
 #pragma unroll
         for (int vv = 0; vv < 16; vv++) {
             const int key = 8 * (vv >> 2) + 4 * lg + (vv & 3);
-            sc[vv] = key < n ? sc[vv] * kscl[vv] : -INFINITY;
+            const int pos = p0 + key;
+            const bool live = MT ? (key < n && pos < seq_c && pos >= lo_c) : key < n;
+            sc[vv] = live ? sc[vv] * kscl[vv] : -INFINITY;
             mx = fmaxf(mx, sc[vv]);
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -237,13 +254,13 @@ void attn_partial_kernel(AttnArgs a) {
         ps += __shfl_xor(ps, 32, 64);
         run_l = run_l * corr + ps;
         run_m = m_new;
-        if (li < G) {
+        if (li < GC) {
             // keys 8m + 4lg + [0,4) for m = 0..3: four consecutive keys per 8-byte store
 #pragma unroll
             for (int m4 = 0; m4 < 4; m4++) {
                 const int key0 = 8 * m4 + 4 * lg;
                 *(u32x2a*)&sP[li * AT_KEYS + key0] = u32x2a{hi2[2 * m4], hi2[2 * m4 + 1]};
-                *(u32x2a*)&sP[(G + li) * AT_KEYS + key0] = u32x2a{lo2[2 * m4], lo2[2 * m4 + 1]};
+                *(u32x2a*)&sP[(GC + li) * AT_KEYS + key0] = u32x2a{lo2[2 * m4], lo2[2 * m4 + 1]};
             }
             if (lg == 0) sMisc[li] = corr;
         }
@@ -256,7 +273,7 @@ void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
         for (int vv = 0; vv < 16; vv++) {
             const int r = 8 * (vv >> 2) + 4 * lg + (vv & 3);
-            cr[vv] = r < 2 * G ? sMisc[r < G ? r : r - G] : 1.0f;
+            cr[vv] = r < 2 * GC ? sMisc[r < GC ? r : r - GC] : 1.0f;
         }
         h8 pa[2];
 #pragma unroll
@@ -323,18 +340,19 @@ void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
         for (int vv = 0; vv < 16; vv++) {
             const int r = 8 * (vv >> 2) + 4 * lg + (vv & 3);
-            if (r < 2 * G) sO[r * hd + 32 * dt + li] = acc[dt][vv];
+            if (r < 2 * GC) sO[r * hd + 32 * dt + li] = acc[dt][vv];
         }
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
     if (S == 1) {
         const float inv_l = run_l > 0.0f ? 1.0f / run_l : 0.0f;
-        uint16_t* ot = a.out + (int64_t)tok * a.n_heads * hd + (int64_t)pbase * hd;
-        for (int e = l; e < G * hd; e += 64) {
-            const int h = e / hd, d = e % hd;
-            const float il = __shfl(inv_l, h, 64);
-            ot[e] = f32_to_f16_bits((sO[h * hd + d] + sO[(G + h) * hd + d]) * il);
+        for (int e = l; e < GC * hd; e += 64) {
+            const int c = e / hd, d = e % hd;
+            const float il = __shfl(inv_l, c, 64);
+            const int ct = MT ? c / G : 0, ch = MT ? c % G : c;
+            uint16_t* ot = a.out + (int64_t)(tok0 + ct) * a.n_heads * hd + (int64_t)(pbase + ch) * hd;
+            ot[d] = f32_to_f16_bits((sO[c * hd + d] + sO[(GC + c) * hd + d]) * il);
         }
         return;
     }
@@ -419,20 +437,27 @@ void attn_reduce_kernel(uint16_t* __restrict__ out, const float* __restrict__ pa
 }
 
 hipError_t attn_launch(const AttnArgs& a, bool kv_int8, hipStream_t st) {
-    if (a.tokens < 1 || (a.tokens > 1 && a.n_splits != 1)) return hipErrorInvalidValue;
-    dim3 grid(a.n_kv, a.n_splits, a.tokens);
-    const size_t lds = attn_lds_bytes(a.n_heads, a.n_kv, a.head_dim);
+    if (a.tokens < 1 || a.tq < 1 || (a.tokens > 1 && a.n_splits != 1) || (a.n_splits > 1 && a.tq != 1) ||
+        (a.n_heads / a.n_kv) * a.tq > AT_MAXG)
+        return hipErrorInvalidValue;
+    dim3 grid(a.n_kv, a.n_splits, (a.tokens + a.tq - 1) / a.tq);
+    const size_t lds = attn_lds_bytes(a.n_heads, a.n_kv, a.head_dim, a.tq);
+    const bool mt = a.tq > 1;
+#define ATTN_CASE(I8, HDV)                                                                                   \
+    if (mt) hipLaunchKernelGGL((attn_partial_kernel<I8, HDV, true>), grid, dim3(64), lds, st, a);           \
+    else    hipLaunchKernelGGL((attn_partial_kernel<I8, HDV, false>), grid, dim3(64), lds, st, a);
     switch (a.head_dim * 2 + (kv_int8 ? 1 : 0)) {
-    case 64:  hipLaunchKernelGGL((attn_partial_kernel<false, 32>), grid, dim3(64), lds, st, a); break;
-    case 65:  hipLaunchKernelGGL((attn_partial_kernel<true, 32>), grid, dim3(64), lds, st, a); break;
-    case 128: hipLaunchKernelGGL((attn_partial_kernel<false, 64>), grid, dim3(64), lds, st, a); break;
-    case 129: hipLaunchKernelGGL((attn_partial_kernel<true, 64>), grid, dim3(64), lds, st, a); break;
-    case 192: hipLaunchKernelGGL((attn_partial_kernel<false, 96>), grid, dim3(64), lds, st, a); break;
-    case 193: hipLaunchKernelGGL((attn_partial_kernel<true, 96>), grid, dim3(64), lds, st, a); break;
-    case 256: hipLaunchKernelGGL((attn_partial_kernel<false, 128>), grid, dim3(64), lds, st, a); break;
-    case 257: hipLaunchKernelGGL((attn_partial_kernel<true, 128>), grid, dim3(64), lds, st, a); break;
+    case 64:  ATTN_CASE(false, 32) break;
+    case 65:  ATTN_CASE(true, 32) break;
+    case 128: ATTN_CASE(false, 64) break;
+    case 129: ATTN_CASE(true, 64) break;
+    case 192: ATTN_CASE(false, 96) break;
+    case 193: ATTN_CASE(true, 96) break;
+    case 256: ATTN_CASE(false, 128) break;
+    case 257: ATTN_CASE(true, 128) break;
     default: return hipErrorInvalidValue;
     }
+#undef ATTN_CASE
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.n_splits == 1) return e;
     hipLaunchKernelGGL(attn_reduce_kernel, dim3(a.n_heads), dim3(AT_RED_THREADS), 0, st, a.out, (const float*)a.part,
