@@ -20,6 +20,7 @@
 #include <math.h>
 #include "kq_common.h"
 #include "layer_ops.h"
+#include "qk_front.h"
 
 namespace jllm_hip {
 
@@ -251,8 +252,7 @@ hipError_t rope_launch(uint16_t* q, uint16_t* k, int n_heads, int n_kv, int head
 // Replaces decode.cu:1441-1478 (q/k norm, rope_inplace, fp16_to_int8 x2)
 // and the per-token loop of decode.cu:1806-1842.
 __global__ __launch_bounds__(256) void qk_post_kernel(QKPostArgs a) {
-#pragma clang fp contract(off)
-    const int hd = a.head_dim, h2 = hd / 2;
+    const int hd = a.head_dim;
     const int slots = a.n_heads + 2 * a.n_kv;
     const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int l = threadIdx.x & 63;
@@ -262,29 +262,14 @@ __global__ __launch_bounds__(256) void qk_post_kernel(QKPostArgs a) {
     const int head = kind == 0 ? slot : (kind == 1 ? slot - a.n_heads : slot - a.n_heads - a.n_kv);
     const uint16_t* src = kind == 0 ? a.q + ((int64_t)t * a.n_heads + head) * hd
                                     : (kind == 1 ? a.k : a.v) + ((int64_t)t * a.n_kv + head) * hd;
-    const bool act = l < h2;
-    const int i0 = a.neox ? l : 2 * l, i1 = a.neox ? l + h2 : 2 * l + 1;
-    float v0 = act ? f16_bits_to_f32(src[i0]) : 0.0f;
-    float v1 = act ? f16_bits_to_f32(src[i1]) : 0.0f;
-    if (kind < 2 && a.q_norm) {
-        const float ss = wave_sum(v0 * v0 + v1 * v1);
-        const float rrms = 1.0f / sqrtf(ss / (float)hd + a.eps);
-        const void* w = kind == 0 ? a.q_norm : a.k_norm;
-        float w0 = 0.0f, w1 = 0.0f;
-        if (act) {
-            if (a.norm_fp32) { w0 = ((const float*)w)[i0]; w1 = ((const float*)w)[i1]; }
-            else { w0 = f16_bits_to_f32(((const uint16_t*)w)[i0]); w1 = f16_bits_to_f32(((const uint16_t*)w)[i1]); }
-        }
-        v0 = round_to_f16(v0 * rrms * w0);
-        v1 = round_to_f16(v1 * rrms * w1);
-    }
     const int pos = a.start_pos + t;
-    if (kind < 2) {
-        float s, c;
-        sincosf((float)pos * a.fr.f[act ? l : 0], &s, &c);
-        rotate(v0, v1, c, s, v0, v1);
-    }
-    if (kind < 2 && act) {
+    float s = 0.0f, c = 1.0f;
+    if (kind < 2) sincosf((float)pos * a.fr.f[l < hd / 2 ? l : 0], &s, &c);
+    float v0, v1;
+    int i0, i1;
+    front_pair(src, hd, a.neox != 0, kind < 2 ? (kind == 0 ? a.q_norm : (a.q_norm ? a.k_norm : nullptr)) : nullptr,
+               a.norm_fp32 != 0, a.eps, kind < 2, c, s, l, v0, v1, i0, i1);
+    if (kind < 2 && l < hd / 2) {
         uint16_t* dq = kind == 0 ? a.q + ((int64_t)t * a.n_heads + head) * hd : a.k + ((int64_t)t * a.n_kv + head) * hd;
         dq[i0] = f32_to_f16_bits(v0);
         dq[i1] = f32_to_f16_bits(v1);
@@ -292,25 +277,9 @@ __global__ __launch_bounds__(256) void qk_post_kernel(QKPostArgs a) {
     if (kind == 0) return;
     const int64_t row = (int64_t)t * a.kv_stride + (int64_t)head * a.cache_head_dim;
     void* cache = kind == 1 ? a.k_dst : a.v_dst;
-    if (a.kv_int8) {
-        const float mx = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
-        const float scale = mx / 127.0f;
-        const float inv = scale > 0.0f ? 127.0f / mx : 0.0f;
-        if (act) {
-            int q0 = (int)__builtin_rintf(v0 * inv), q1 = (int)__builtin_rintf(v1 * inv);
-            q0 = q0 > 127 ? 127 : (q0 < -127 ? -127 : q0);
-            q1 = q1 > 127 ? 127 : (q1 < -127 ? -127 : q1);
-            int8_t* d = (int8_t*)cache + row;
-            d[i0] = (int8_t)q0;
-            d[i1] = (int8_t)q1;
-        }
-        float* sc = kind == 1 ? a.k_scales : a.v_scales;
-        if (l == 0 && sc) sc[(int64_t)t * a.n_kv + head] = scale;
-    } else if (act) {
-        uint16_t* d = (uint16_t*)cache + row;
-        d[i0] = f32_to_f16_bits(v0);
-        d[i1] = f32_to_f16_bits(v1);
-    }
+    float* sc = kind == 1 ? a.k_scales : a.v_scales;
+    front_store_kv(a.kv_int8 ? (void*)((int8_t*)cache + row) : (void*)((uint16_t*)cache + row),
+                   sc ? sc + (int64_t)t * a.n_kv + head : nullptr, a.kv_int8 != 0, hd, v0, v1, i0, i1, l);
 }
 
 hipError_t qk_post_launch(const QKPostArgs& a, hipStream_t st) {
