@@ -370,7 +370,10 @@ __device__ __forceinline__ float block_dot(const Raw& r, int b, int q, const Q4C
 // residual rows are loaded before any weight bytes, behind a barrier, so
 // that they do not queue behind the CU's weight traffic.
 
-constexpr int ST_T = GEMV_THREADS;
+#ifndef JLLM_GEMV_ST_THREADS
+#define JLLM_GEMV_ST_THREADS 256
+#endif
+constexpr int ST_T = JLLM_GEMV_ST_THREADS;
 constexpr int ST_W = ST_T / 64;        // waves per workgroup
 
 // lane ^ 1 and lane ^ 2 through DPP quad_perm (no LDS round trip)
@@ -728,7 +731,9 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-            const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+            float tot = 0.0f;
+#pragma unroll
+            for (int w = 0; w < ST_W; w++) tot += red[w];
             const float rrms = 1.0f / sqrtf(tot / (float)K + a.pre.eps);
 #pragma unroll
             for (int i = 0; i < NX; i++) {
