@@ -41,7 +41,8 @@ struct GemvArgs {
 };
 
 // Arguments of the streaming kernel (filled by gemv_launch).  Segments
-// are ordered Q4_K first; their rows form one sequence.
+// are ordered first class first; their rows form one sequence, split into
+// contiguous row ranges per workgroup.
 struct StreamArgs {
     GemvSeg seg[3];
     int K;
@@ -49,11 +50,10 @@ struct StreamArgs {
     int xlds_bytes;         // LDS bytes of the staged activation
     const uint16_t* x;
     int row_off[4];         // first row of each segment in the row sequence
-    int row_split;          // rows of Q4_K segments
-    int wave_split;         // waves (over the grid) serving the Q4_K rows
-    int rows_q[2], rows_r[2];       // rows per wave (quotient, remainder) per type
-    int slots_per_wave;     // LDS block slots per wave (max rows per wave * nb)
-    int wg_rows;            // residual rows staged per workgroup (waves * max rows per wave)
+    int row_split;          // rows of the first-class (Q4_K / Q5_K) segments
+    int wg_split;           // workgroups serving the first-class rows
+    int rows_q[2], rows_r[2];       // rows per workgroup (quotient, remainder) per class
+    int slots_per_wg;       // LDS block slots per workgroup (max rows per workgroup * nb, x2 for OUT_SWIGLU)
     int swiglu;             // OUT_SWIGLU launch: row sequence = the M (gate, up) row pairs
     GemvPre pre;
 };

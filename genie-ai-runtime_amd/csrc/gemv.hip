@@ -477,7 +477,10 @@ static int device_cus() {
 
 // The rows [r0, r1) (segment-relative) a wave owns inside one segment, its
 // first slot and its rounds.
-struct Piece { int r0, r1, slot0, rounds; };
+// The blocks [b0, b0 + nblk) of one segment (b0 counted from the segment's
+// first block) that a wave streams, the workgroup slot of its first block
+// and its number of rounds.
+struct Piece { int b0, nblk, slot0, rounds; };
 
 // A round: up to WGeom::NBLK blocks of one piece (contiguous bytes).
 struct RoundDesc {
@@ -512,12 +515,12 @@ __device__ __forceinline__ RoundDesc round_desc(const StreamArgs& a, const Piece
     for (int i = 0; i < 3; i++) {
         if (r >= 0 && r < pc[i].rounds) {
             const int f = r * NB;                                   // block offset in the piece
-            d.nblk = min(NB, (pc[i].r1 - pc[i].r0) * nb - f);
-            const uint8_t* start = a.seg[i].W + ((int64_t)pc[i].r0 * nb + f) * BB;
+            d.nblk = min(NB, pc[i].nblk - f);
+            const uint8_t* start = a.seg[i].W + ((int64_t)pc[i].b0 + f) * BB;
             d.delta = (int)((uintptr_t)start & 15u);
             d.base = start - d.delta;
             d.nrec = (d.delta + d.nblk * BB + 15) & ~15;
-            d.col0 = f % nb;
+            d.col0 = (pc[i].b0 + f) % nb;
             d.slot0 = pc[i].slot0 + f;
         }
         r -= pc[i].rounds;
@@ -597,42 +600,42 @@ __device__ __forceinline__ void compute_round(const RoundDesc& d, const uint8_t*
     }
 }
 
-// Rows of a wave: waves [0, wave_split) (over the whole grid) serve the Q4_K
-// rows, the rest the Q6_K rows; each type's rows are split evenly.
-__device__ __forceinline__ void wave_rows(const StreamArgs& a, int gw, int& g0, int& g1, bool& q4) {
-    q4 = gw < a.wave_split;
-    const int w = q4 ? gw : gw - a.wave_split;
+// Rows of a workgroup: workgroups [0, wg_split) serve the first-class rows,
+// the rest the Q6_K rows; each class's rows are split evenly.
+__device__ __forceinline__ void wg_rows(const StreamArgs& a, int wg, int& g0, int& g1, bool& q4) {
+    q4 = wg < a.wg_split;
+    const int w = q4 ? wg : wg - a.wg_split;
     const int q = q4 ? a.rows_q[0] : a.rows_q[1], rr = q4 ? a.rows_r[0] : a.rows_r[1];
     g0 = (q4 ? 0 : a.row_split) + w * q + min(w, rr);
     g1 = g0 + q + (w < rr ? 1 : 0);
 }
 
+// The workgroup's rows [g0, g1) as one sequence of blocks (OUT_SWIGLU: the
+// gate rows' blocks, then the up rows'), cut into ST_W equal contiguous
+// ranges, one per wave; the wave's range as up to three pieces, one per
+// segment it touches.  Slots are indexed by the block's place in the
+// workgroup sequence.
 template <int TYPE, int L, int OUT>
-__device__ __forceinline__ int make_pieces(const StreamArgs& a, int g0, int g1, Piece (&pc)[3]) {
+__device__ __forceinline__ int make_pieces(const StreamArgs& a, int g0, int g1, int wv, Piece (&pc)[3]) {
     constexpr int NB = WGeom<TYPE, L>::NBLK;
-    int nr = 0, slot = 0;
-    if (OUT == OUT_SWIGLU) {
-        // row pairs [g0, g1): the gate rows, then the same up rows
-#pragma unroll
-        for (int s = 0; s < 3; s++) {
-            pc[s].r0 = s < 2 ? g0 : 0;
-            pc[s].r1 = s < 2 ? g1 : 0;
-            pc[s].slot0 = slot;
-            const int nblk = (pc[s].r1 - pc[s].r0) * a.nb;
-            slot += nblk;
-            pc[s].rounds = (nblk + NB - 1) / NB;
-            nr += pc[s].rounds;
-        }
-        return nr;
-    }
+    const int nb = a.nb, nrow = g1 - g0;
+    const int seq = nrow * nb * (OUT == OUT_SWIGLU ? 2 : 1);
+    const int j0 = (int)((int64_t)seq * wv / ST_W), j1 = (int)((int64_t)seq * (wv + 1) / ST_W);
+    int nr = 0;
 #pragma unroll
     for (int s = 0; s < 3; s++) {
-        pc[s].r0 = max(g0, a.row_off[s]) - a.row_off[s];
-        pc[s].r1 = max(min(g1, a.row_off[s + 1]) - a.row_off[s], pc[s].r0);
-        pc[s].slot0 = slot;
-        const int nblk = (pc[s].r1 - pc[s].r0) * a.nb;
-        slot += nblk;
-        pc[s].rounds = (nblk + NB - 1) / NB;
+        int ra, rb, o, first;          // chunk: rows [ra, rb) of the sequence order, sequence offset o, first segment row
+        if (OUT == OUT_SWIGLU) {
+            ra = s < 2 ? g0 : g1; rb = g1; o = s == 1 ? nrow * nb : 0; first = g0;
+        } else {
+            ra = max(g0, a.row_off[s]); rb = max(min(g1, a.row_off[s + 1]), ra);
+            o = (ra - g0) * nb; first = ra - a.row_off[s];
+        }
+        const int lo = max(j0, o), hi = min(j1, o + (rb - ra) * nb);
+        pc[s].nblk = hi > lo ? hi - lo : 0;
+        pc[s].b0 = first * nb + (lo - o);
+        pc[s].slot0 = lo;
+        pc[s].rounds = (pc[s].nblk + NB - 1) / NB;
         nr += pc[s].rounds;
     }
     return nr;
@@ -680,10 +683,10 @@ __device__ __forceinline__ u32x4 rms8(const u32x4& a, float rrms, int w_fp32, co
 // Both weight types run the same two workgroup barriers (activation staging).
 template <bool MMVQ, int OUT, int TYPE, int L, int NX, int PRE>
 __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int g0, int g1, int lane, int wv,
-                                          uint16_t* res_lds, int wg_g0) {
+                                          uint16_t* res_lds) {
     const int nb = a.nb, K = a.K;
     Piece pc[3];
-    const int nr = make_pieces<TYPE, L, OUT>(a, g0, g1, pc);
+    const int nr = make_pieces<TYPE, L, OUT>(a, g0, g1, wv, pc);
     u32x4 R0[L], R1[L];
     {
         // activation (and residual) loads first, on every wave, then a barrier,
@@ -707,8 +710,8 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
             }
         }
         uint16_t rv = 0;
-        const int nres = OUT == OUT_ADD ? min(a.wg_rows, a.row_off[3] - wg_g0) : 0;   // nres <= ST_T
-        if (OUT == OUT_ADD && (int)threadIdx.x < nres) rv = a.seg[0].res[wg_g0 + threadIdx.x];
+        const int nres = OUT == OUT_ADD ? g1 - g0 : 0;   // the workgroup's rows, nres <= ST_T
+        if (OUT == OUT_ADD && (int)threadIdx.x < nres) rv = a.seg[0].res[g0 + threadIdx.x];
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         issue_round<L>(round_desc<TYPE, L>(a, pc, 0), R0, lane);
@@ -769,7 +772,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     const uint8_t* xlds = lds;
     uint8_t* buf = lds + a.xlds_bytes + wv * (64 * 16 * L);
-    float* slots = (float*)(lds + a.xlds_bytes + ST_W * (64 * 16 * L)) + wv * a.slots_per_wave;
+    float* slots = (float*)(lds + a.xlds_bytes + ST_W * (64 * 16 * L));    // the workgroup's block slots
     // Round r travels in register stage r mod 2.  Step k: compute round k
     // from the wave's LDS buffer, move round k+1 from its registers into the
     // buffer, and reuse those registers for round k+3 (round k+2 stays in
@@ -791,12 +794,16 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         step(k + 1, R0);
     }
     if (k < nr) step(k, R1);
+    // every wave's slots are written: LDS-only barrier (no wait on global loads)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     // rows: 8 lanes per row add the row's slots (lane j the blocks b = j mod 8,
-    // in order), then a fixed butterfly
-    const int nrow = g1 - g0, j = lane & 7;
+    // in order), then a fixed butterfly; ST_T / 8 rows per pass
+    const int nrow = g1 - g0, j = lane & 7, rg = (int)threadIdx.x >> 3;
     if (OUT == OUT_SWIGLU) {
-        for (int t0 = 0; t0 < nrow; t0 += 8) {
-            const int t = t0 + (lane >> 3);
+        for (int t0 = 0; t0 < nrow; t0 += ST_T / 8) {
+            const int t = t0 + rg;
             float vg = 0.0f, vu = 0.0f;
             if (t < nrow) {
                 const float* p = slots + t * nb;
@@ -815,8 +822,8 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         }
         return;
     }
-    for (int t0 = 0; t0 < nrow; t0 += 8) {
-        const int t = t0 + (lane >> 3);
+    for (int t0 = 0; t0 < nrow; t0 += ST_T / 8) {
+        const int t = t0 + rg;
         float v = 0.0f;
         if (t < nrow) {
             const float* p = slots + t * nb;
@@ -827,8 +834,8 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         v += __shfl_xor(v, 4, 64);
         if (j == 0 && t < nrow) {
             const int g = g0 + t;
-            const int s = g >= a.row_off[1] ? (g >= a.row_off[2] ? 2 : 1) : 0;
-            store_row<OUT>(a.seg[s], g - a.row_off[s], v, res_lds, g - wg_g0);
+            const int sg = g >= a.row_off[1] ? (g >= a.row_off[2] ? 2 : 1) : 0;
+            store_row<OUT>(a.seg[sg], g - a.row_off[sg], v, res_lds, t);
         }
     }
 }
@@ -848,30 +855,22 @@ void gemv_stream_kernel(StreamArgs a_in) {
     for (int i = 0; i < 3; i++) pin_sgpr(a.seg[i].W);
 #pragma unroll
     for (int i = 0; i < 4; i++) pin_sgpr(a.row_off[i]);
-    pin_sgpr(a.x); pin_sgpr(a.K); pin_sgpr(a.nb); pin_sgpr(a.xlds_bytes); pin_sgpr(a.row_split); pin_sgpr(a.wave_split);
-    pin_sgpr(a.slots_per_wave);
+    pin_sgpr(a.x); pin_sgpr(a.K); pin_sgpr(a.nb); pin_sgpr(a.xlds_bytes); pin_sgpr(a.row_split); pin_sgpr(a.wg_split);
+    pin_sgpr(a.slots_per_wg);
 #pragma unroll
     for (int i = 0; i < 2; i++) { pin_sgpr(a.rows_q[i]); pin_sgpr(a.rows_r[i]); }
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int gw = blockIdx.x * ST_W + wv;
     int g0, g1;
     bool q4;
-    wave_rows(a, gw, g0, g1, q4);
-    // rows of the whole workgroup (for the staged residual): waves are in row order per type
-    int wg_g0 = 0;
-    if (OUT == OUT_ADD) {
-        int h0, h1; bool hq;
-        wave_rows(a, blockIdx.x * ST_W, h0, h1, hq);
-        wg_g0 = h0;
-    }
-    uint16_t* res_lds = (uint16_t*)(lds + a.xlds_bytes + ST_W * (64 * 16 * L) + ST_W * 4 * a.slots_per_wave);
-    // (both bodies hold the same two workgroup barriers)
+    wg_rows(a, blockIdx.x, g0, g1, q4);
+    uint16_t* res_lds = (uint16_t*)(lds + a.xlds_bytes + ST_W * (64 * 16 * L) + 4 * a.slots_per_wg);
+    // (both bodies hold the same workgroup barriers; a workgroup serves one class)
     if constexpr (OUT == OUT_SWIGLU) {
-        wave_body<MMVQ, OUT, TA, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
+        wave_body<MMVQ, OUT, TA, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds);
     } else {
-        if (q4) wave_body<MMVQ, OUT, TA, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
-        else    wave_body<MMVQ, OUT, TYPE_Q6_K, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds, wg_g0);
+        if (q4) wave_body<MMVQ, OUT, TA, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds);
+        else    wave_body<MMVQ, OUT, TYPE_Q6_K, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds);
     }
 }
 
@@ -960,12 +959,12 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     const int64_t bytes4 = rows4 * a.nb * (has5 ? Q5K_BYTES : Q4K_BYTES), bytes6 = rows6 * a.nb * Q6K_BYTES;
     a.xlds_bytes = (int)((gemv_lds_bytes(mmvq, a.K) + 15) & ~(size_t)15);
     const size_t wbuf = ST_W * (size_t)(64 * 16 * ST_L);
-    // waves: ST_W per workgroup, JLLM_GEMV_WG_PER_CU workgroups per CU when
-    // LDS allows; split between the types by bytes
+    // JLLM_GEMV_WG_PER_CU workgroups per CU when LDS allows, split between
+    // the classes by bytes; a workgroup takes a contiguous row range
     int64_t grid = 0;
     int64_t w4 = 0, w6 = 0, max_rows = 0;
     auto split = [&](int64_t g) {
-        const int64_t w = g * ST_W;
+        const int64_t w = g;
         if (rows6 == 0) { w4 = w; w6 = 0; }
         else if (rows4 == 0) { w4 = 0; w6 = w; }
         else {
@@ -976,11 +975,11 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
         max_rows = std::max(w4 ? (rows4 + w4 - 1) / w4 : 0, w6 ? (rows6 + w6 - 1) / w6 : 0);
     };
     auto lds_of = [&]() {
-        const size_t res = out_kind == OUT_ADD ? (size_t)ST_W * max_rows * 2 : 0;
-        return (size_t)a.xlds_bytes + wbuf + (size_t)ST_W * 4 * slot_rows * max_rows * a.nb + res;
+        const size_t res = out_kind == OUT_ADD ? (size_t)max_rows * 2 : 0;
+        return (size_t)a.xlds_bytes + wbuf + (size_t)4 * slot_rows * max_rows * a.nb + res;
     };
     // (the residual rows of a workgroup are staged one per lane)
-    auto fits = [&](int per_cu) { return (size_t)per_cu * lds_of() <= LDS_CU && !(out_kind == OUT_ADD && ST_W * max_rows > ST_T); };
+    auto fits = [&](int per_cu) { return (size_t)per_cu * lds_of() <= LDS_CU && !(out_kind == OUT_ADD && max_rows > ST_T); };
     for (int per_cu = JLLM_GEMV_WG_PER_CU; per_cu >= 1 && grid == 0; per_cu--) {
         split((int64_t)device_cus() * per_cu);
         if (fits(per_cu)) grid = (int64_t)device_cus() * per_cu;
@@ -993,11 +992,10 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
             split(grid *= 2);
         }
     }
-    a.wave_split = (int)w4;
+    a.wg_split = (int)w4;
     a.rows_q[0] = w4 > 0 ? (int)(rows4 / w4) : 0; a.rows_r[0] = w4 > 0 ? (int)(rows4 % w4) : 0;
     a.rows_q[1] = w6 > 0 ? (int)(rows6 / w6) : 0; a.rows_r[1] = w6 > 0 ? (int)(rows6 % w6) : 0;
-    a.slots_per_wave = (int)(slot_rows * max_rows * a.nb);
-    a.wg_rows = (int)(ST_W * max_rows);
+    a.slots_per_wg = (int)(slot_rows * max_rows * a.nb);
     const size_t lds = lds_of();
     const int g = (int)grid;
     a.pre = in.pre;
