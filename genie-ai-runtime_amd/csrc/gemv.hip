@@ -911,7 +911,10 @@ static constexpr size_t LDS_CU = 160 * 1024;
 #ifndef JLLM_GEMV_WG_PER_CU
 #define JLLM_GEMV_WG_PER_CU 4
 #endif
-constexpr int ST_L = 4;
+#ifndef JLLM_GEMV_ROUND_KB
+#define JLLM_GEMV_ROUND_KB 4
+#endif
+constexpr int ST_L = JLLM_GEMV_ROUND_KB;   // 16-byte chunks per lane per round (KiB per wave round)
 
 hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t st) {
     if (out_kind == OUT_ADD && in.nseg != 1) return hipErrorInvalidValue;
