@@ -142,6 +142,24 @@ def test_fp16_to_int8_known_answer(dev):
     assert np.all(d[:128] == 127) and np.all(d[128:] == -127)
 
 
+@pytest.mark.parametrize("rows,cols", [(8, 128), (1, 64), (300, 1024)])
+def test_kv_int8_round_trip(dev, rows, cols):
+    """The reference's round-trip bar (test_kv_int8_convert.cu:154): codes
+    times scale reproduce every value within 2 % of its row's max |v|
+    (rounding error <= scale / 2 = max / 254)."""
+    print_case("kv_roundtrip", rows, cols)
+    g = synth.rng(rows + cols)
+    x = (g.uniform(-1.0, 1.0, (rows, cols)) * g.uniform(0.01, 10.0, (rows, 1))).astype(np.float16)
+    dst = torch.empty(rows * cols, dtype=torch.int8, device=dev)
+    sc = torch.empty(rows, dtype=torch.float32, device=dev)
+    jllm.call("jllm_hip_fp16_to_int8", dst, sc, to_dev(x.view(np.uint16)), rows, cols)
+    back = from_dev(dst).reshape(rows, cols).astype(np.float64) * from_dev(sc).astype(np.float64)[:, None]
+    xf = x.astype(np.float64)
+    amax = np.abs(xf).max(axis=1, keepdims=True)
+    assert np.all(np.abs(back - xf) <= 0.02 * amax)
+    assert np.all(np.abs(back - xf) <= amax / 254 * (1 + 1e-5))
+
+
 def test_attention_repeats_and_graph_replays(dev):
     """Back-to-back split-K calls sharing the partials scratch, and graph
     replays of them with eager work in between, give the eager result every

@@ -194,3 +194,44 @@ def test_q5k_has_no_subdots(dev):
     W = to_dev(synth.q5k(synth.rng(2), 4, 256))
     out = torch.zeros(64, dtype=torch.int32, device=dev)
     assert jllm.lib().jllm_hip_mmq_subdots(jllm._ptr(out), jllm._ptr(W), 13, jllm._ptr(x), 4, 2, 256, None) != 0
+
+
+# ---- the reference's own accuracy bar against the true fp16 x K-quant product -----
+
+def _reference_style_weights(g, t, M, K):
+    """Block distributions of the reference's MMQ tests: Q4_K d ~ U(0.005, 0.02),
+    dmin ~ U(0.001, 0.004), random scale / qs bytes (test_mmq_q4k_int8.cu:434-445);
+    Q6_K sc ~ U{-32..32}, d ~ U(0.001, 0.01) (test_mmq_q6k_int8.cu:257-266)."""
+    nb = K // 256
+    if t == 12:
+        b = np.frombuffer(g.bytes(M * nb * 144), np.uint8).reshape(M, nb, 144).copy()
+        b[:, :, 0:2] = g.uniform(0.005, 0.02, (M, nb, 1)).astype(np.float16).view(np.uint8)
+        b[:, :, 2:4] = g.uniform(0.001, 0.004, (M, nb, 1)).astype(np.float16).view(np.uint8)
+        return b.reshape(M, -1)
+    b = np.frombuffer(g.bytes(M * nb * 210), np.uint8).reshape(M, nb, 210).copy()
+    b[:, :, 192:208] = g.integers(-32, 33, (M, nb, 16)).astype(np.int8).view(np.uint8)
+    b[:, :, 208:210] = g.uniform(0.001, 0.01, (M, nb, 1)).astype(np.float16).view(np.uint8)
+    return b.reshape(M, -1)
+
+
+@pytest.mark.parametrize("t,M,N,K", [(12, 256, 64, 2560), (14, 256, 64, 2560), (12, 512, 130, 4096)])
+def test_mmq_vs_true_fp16_product(dev, t, M, N, K):
+    """The q8_1 quantisation error against the unquantised product, with the
+    reference's bar for its MMQ port (test_mmq_q4k_llama.cu:477-482): relRMS
+    < 0.01 and no element with rel > 0.02 and abs > 0.05 sigma; x ~ U(-1, 1)
+    (test_mmq_q4k_int8.cu:496-497)."""
+    import np_ref
+    print_case("mmq_vs_fp16", t, M, N, K)
+    g = synth.rng(0xC0FFEE + t)
+    W = _reference_style_weights(g, t, M, K)
+    x = g.uniform(-1.0, 1.0, (N, K)).astype(np.float16).view(np.uint16)
+    y = torch.empty(N * M, dtype=torch.float32, device=dev)
+    jllm.call("jllm_hip_gemm_quant_batched_f32", y, to_dev(W), t, to_dev(x), M, N, K)
+    got = from_dev(y).reshape(N, M).astype(np.float64)
+    ref = np_ref.f16(x).reshape(N, K) @ np_ref.dequant(W, t, M, K).T
+    err = got - ref
+    sigma = ref.std()
+    rel_rms = np.sqrt((err ** 2).mean()) / np.sqrt((ref ** 2).mean())
+    assert rel_rms < 0.01, rel_rms
+    bad = (np.abs(err) > 0.02 * np.abs(ref)) & (np.abs(err) > 0.05 * sigma)
+    assert not bad.any(), int(bad.sum())
