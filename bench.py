@@ -216,8 +216,12 @@ def bench_mmq(np, torch, jllm, synth, up, dev, g):
             torch.cuda.synchronize()
             us = e0.elapsed_time(e1) * 1e3 / 10
             tops = 2.0 * N * M * K / (us * 1e-6) / 1e12
+            # algorithmic bytes: weights + the activation as q8_1 (36 B per 32) + fp16 y
+            nbytes = mat_bytes(t, M, K) + N * K * 36 // 32 + N * M * 2
+            gbs = nbytes / (us * 1e-6) / 1e9
             res[f"{'q4k' if t == 12 else 'q6k'}_M{M}_K{K}_N{N}"] = {
-                "us": round(us, 2), "TOPS": round(tops, 2), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+                "us": round(us, 2), "TOPS": round(tops, 2), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
     return res
 
 
