@@ -202,7 +202,8 @@ __device__ __forceinline__ float mmvq_block<TYPE_Q4_K>(const Raw& r, int b, int 
     uint32_t sc0, m0, sc1, m1;
     q4_scales(c, r.a, 0, sc0, m0);
     q4_scales(c, r.a, 1, sc1, m1);
-    const float a = (float)(dl * (int)sc0) * d8.x + (float)(dh * (int)sc1) * d8.y;
+    // |dot| <= 32*15*127 and sc <= 63: the products fit the full-rate 24-bit multiply exactly
+    const float a = (float)__mul24(dl, (int)sc0) * d8.x + (float)__mul24(dh, (int)sc1) * d8.y;
     const float mm = (float)m0 * s8.x + (float)m1 * s8.y;
     const float dall = f16_bits_to_f32(r.a.x & 0xFFFFu), dmin = f16_bits_to_f32(r.a.x >> 16);
     return dall * a - dmin * mm;
@@ -501,7 +502,10 @@ struct WGeom {
     static constexpr int BYTES = 64 * 16 * L;                                  // one wave's round
     // Q4_K / Q5_K blocks are 16-byte multiples (rounds start aligned); a Q6_K
     // round may start up to 14 bytes into its first 16-byte chunk
-    static constexpr int NBLK = TYPE == TYPE_Q6_K ? (BYTES - 14) / BB : BYTES / BB;
+    static constexpr int NFIT = TYPE == TYPE_Q6_K ? (BYTES - 14) / BB : BYTES / BB;
+    // whole passes of the 16 quads: a round of 19 Q6_K blocks would leave 13
+    // of 16 quads idle in its second pass (measured: lm_head 74 -> 61 us)
+    static constexpr int NBLK = NFIT >= 16 ? NFIT / 16 * 16 : NFIT;
 };
 
 template <int TYPE, int L>
@@ -528,11 +532,14 @@ __device__ __forceinline__ RoundDesc round_desc(const StreamArgs& a, const Piece
     return d;
 }
 
+#ifndef JLLM_GEMV_CPOL
+#define JLLM_GEMV_CPOL 2   // nt: the weights are streamed once (measured 5 % faster than the default policy)
+#endif
 template <int L>
 __device__ __forceinline__ void issue_round(const RoundDesc& d, u32x4 (&v)[L], int lane) {
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)d.base, (short)0, d.nrec, 0x00020000);
 #pragma unroll
-    for (int i = 0; i < L; i++) v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane + 64 * i) * 16, 0, 0);
+    for (int i = 0; i < L; i++) v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane + 64 * i) * 16, 0, JLLM_GEMV_CPOL);
 }
 
 template <int L>
@@ -678,6 +685,15 @@ __device__ __forceinline__ u32x4 rms8(const u32x4& a, float rrms, int w_fp32, co
     return u32x4_make(o[0], o[1], o[2], o[3]);
 }
 
+#ifdef JLLM_GEMV_TRACE
+// debug build only: per-wave timestamps (s_memrealtime, 100 MHz) of the last launch
+__device__ uint64_t g_gemv_trace[8192 * 8];
+__device__ uint64_t g_gemv_rtrace[4096 * 48];
+#define GT_MARK(i) do { tr[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define GT_MARK(i) do { } while (0)
+#endif
+
 // One wave's rows: rounds stream through two register stages and the wave's
 // own LDS buffer; the slots of its rows are added up and stored at the end.
 // Both weight types run the same two workgroup barriers (activation staging).
@@ -685,6 +701,13 @@ template <bool MMVQ, int OUT, int TYPE, int L, int NX, int PRE>
 __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int g0, int g1, int lane, int wv,
                                           uint16_t* res_lds) {
     const int nb = a.nb, K = a.K;
+#ifdef JLLM_GEMV_TRACE
+    uint64_t tr[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#endif
+    GT_MARK(0);
+#ifdef JLLM_GEMV_TRACE
+    tr[7] = ((uint64_t)__builtin_amdgcn_s_getreg((31 << 11) | 20) << 32) | (uint64_t)__builtin_amdgcn_s_getreg((31 << 11) | 4);
+#endif
     Piece pc[3];
     const int nr = make_pieces<TYPE, L, OUT>(a, g0, g1, wv, pc);
     u32x4 R0[L], R1[L];
@@ -717,6 +740,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         issue_round<L>(round_desc<TYPE, L>(a, pc, 0), R0, lane);
         issue_round<L>(round_desc<TYPE, L>(a, pc, 1), R1, lane);
         __builtin_amdgcn_sched_barrier(0);
+        GT_MARK(1);
         if (PRE == PRE_RMS) {
             // sum of squares of the whole activation (K <= NX * ST_T * 8 here):
             // lanes, then waves through LDS (the first words of wave 0's round
@@ -741,12 +765,14 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
 #pragma unroll
             for (int i = 0; i < NX; i++) {
                 const int c = (int)threadIdx.x + ST_T * i;
-                if (c < nch) xv[i] = rms8(xv[i], rrms, a.pre.nw_fp32, nwv[2 * i], nwv[2 * i + 1]);
+                if (ST_T * i + 64 * wv < nch && c < nch) xv[i] = rms8(xv[i], rrms, a.pre.nw_fp32, nwv[2 * i], nwv[2 * i + 1]);
             }
         }
+        // (a wave whose chunks all lie beyond K skips the staging arithmetic: uniform branch)
 #pragma unroll
         for (int i = 0; i < NX; i++) {
             const int c = (int)threadIdx.x + ST_T * i;
+            if (ST_T * i + 64 * wv >= nch) continue;
             if (MMVQ) xstage_q8_1(xv[i], c, K, lds);
             else      xstage_f16(xv[i], c, K, lds);
         }
@@ -760,6 +786,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
 #pragma unroll
             for (int i = 0; i < NX; i++) {
                 const int c = c0 + (int)threadIdx.x + ST_T * i;
+                if (c0 + ST_T * i + 64 * wv >= nch) continue;
                 if (MMVQ) xstage_q8_1(xv[i], c, K, lds);
                 else      xstage_f16(xv[i], c, K, lds);
             }
@@ -770,6 +797,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    GT_MARK(2);
     const uint8_t* xlds = lds;
     uint8_t* buf = lds + a.xlds_bytes + wv * (64 * 16 * L);
     float* slots = (float*)(lds + a.xlds_bytes + ST_W * (64 * 16 * L));    // the workgroup's block slots
@@ -780,12 +808,24 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
     // (scalar arithmetic) rather than kept per stage.
     write_round<L>(buf, R0, lane);
     __builtin_amdgcn_wave_barrier();
+    GT_MARK(3);
     issue_round<L>(round_desc<TYPE, L>(a, pc, 2), R0, lane);
     auto step = [&](int k, u32x4 (&nxt)[L]) {
+#ifdef JLLM_GEMV_TRACE
+        const int64_t gw = (int64_t)blockIdx.x * ST_W + wv;
+        const bool rt = gw < 4096 && k < 16 && lane == 0;
+        if (rt) g_gemv_rtrace[gw * 48 + k * 3] = __builtin_amdgcn_s_memrealtime();
+#endif
         compute_round<MMVQ, TYPE>(round_desc<TYPE, L>(a, pc, k), buf, xlds, slots, K, nb, lane);
         __builtin_amdgcn_wave_barrier();
+#ifdef JLLM_GEMV_TRACE
+        if (rt) g_gemv_rtrace[gw * 48 + k * 3 + 1] = __builtin_amdgcn_s_memrealtime();
+#endif
         write_round<L>(buf, nxt, lane);
         __builtin_amdgcn_wave_barrier();
+#ifdef JLLM_GEMV_TRACE
+        if (rt) g_gemv_rtrace[gw * 48 + k * 3 + 2] = __builtin_amdgcn_s_memrealtime();
+#endif
         issue_round<L>(round_desc<TYPE, L>(a, pc, k + 3), nxt, lane);
     };
     int k = 0;
@@ -794,6 +834,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         step(k + 1, R0);
     }
     if (k < nr) step(k, R1);
+    GT_MARK(4);
     // every wave's slots are written: LDS-only barrier (no wait on global loads)
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
@@ -820,8 +861,18 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
                 ((uint16_t*)a.seg[0].y)[g0 + t] = f32_to_f16_bits(g / (1.0f + expf(-g)) * u);
             }
         }
+        GT_MARK(6);
+#ifdef JLLM_GEMV_TRACE
+        {
+            uint64_t tv = 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) if (lane == i) tv = tr[i];
+            if (lane < 8) g_gemv_trace[((int64_t)blockIdx.x * ST_W + wv) * 8 + lane] = tv;
+        }
+#endif
         return;
     }
+    GT_MARK(5);
     for (int t0 = 0; t0 < nrow; t0 += ST_T / 8) {
         const int t = t0 + rg;
         float v = 0.0f;
@@ -838,6 +889,15 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
             store_row<OUT>(a.seg[sg], g - a.row_off[sg], v, res_lds, t);
         }
     }
+    GT_MARK(6);
+#ifdef JLLM_GEMV_TRACE
+    {
+        uint64_t tv = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) if (lane == i) tv = tr[i];
+        if (lane < 8) g_gemv_trace[((int64_t)blockIdx.x * ST_W + wv) * 8 + lane] = tv;
+    }
+#endif
 }
 
 // Pin a uniform value into SGPRs here (kernel-argument loads are otherwise
@@ -1025,6 +1085,15 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     if (out_kind == OUT_F32)  return launch_nx<false, OUT_F32, ST_L>(a, g, lds, st, has5);
     return launch_nx<false, OUT_ADD, ST_L>(a, g, lds, st, has5);
 }
+
+#ifdef JLLM_GEMV_TRACE
+extern "C" int jllm_hip_gemv_trace_read(uint64_t* host, int n) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_gemv_trace), (size_t)n * 8, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+extern "C" int jllm_hip_gemv_rtrace_read(uint64_t* host) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_gemv_rtrace), (size_t)4096 * 48 * 8, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+#endif
 
 hipError_t quantize_q8_1_aos_launch(const uint16_t* x, void* y, int K, hipStream_t st) {
     const int n = (K / 32) * 8;
