@@ -971,15 +971,20 @@ static hipError_t launch_nx(const StreamArgs& a, int grid, size_t lds, hipStream
 }
 
 static constexpr size_t LDS_CU = 160 * 1024;
-// Workgroups per CU: 2 (8 waves per CU) for a decode-layer matrix -- fewer
-// waves reach the CU sooner and each streams more rounds (gate/up pair with
-// RMSNorm + SwiGLU 11.1 -> 9.3 us, down 8.95 -> 8.35 us against 4 per CU);
-// 4 for a launch of more than 64 MB (the lm_head, 63 -> 61 us).
+// Workgroups per CU by launch size (measured on MI355X, graphs of 36 layers):
+// 2 (8 waves per CU) for a decode-layer matrix -- fewer waves reach the CU
+// sooner and each streams more rounds (gate/up pair with RMSNorm + SwiGLU
+// 11.1 -> 9.3 us, down 8.95 -> 8.35 us against 4 per CU); 1 under 12 MB
+// (QKV triple 6.4 -> 6.05 us, O 6.05 -> 5.7 us); 4 above 64 MB (the
+// lm_head, 63 -> 61 us).
 #ifndef JLLM_GEMV_WG_PER_CU
 #define JLLM_GEMV_WG_PER_CU 2
 #endif
 #ifndef JLLM_GEMV_WG_PER_CU_BIG
 #define JLLM_GEMV_WG_PER_CU_BIG 4
+#endif
+#ifndef JLLM_GEMV_WG_PER_CU_SMALL
+#define JLLM_GEMV_WG_PER_CU_SMALL 1
 #endif
 #ifndef JLLM_GEMV_ROUND_KB
 #define JLLM_GEMV_ROUND_KB 4
@@ -1053,7 +1058,9 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     };
     // (the residual rows of a workgroup are staged one per lane)
     auto fits = [&](int per_cu) { return (size_t)per_cu * lds_of() <= LDS_CU && !(out_kind == OUT_ADD && max_rows > ST_T); };
-    const int per_cu0 = bytes4 + bytes6 > ((int64_t)64 << 20) ? JLLM_GEMV_WG_PER_CU_BIG : JLLM_GEMV_WG_PER_CU;
+    const int64_t wbytes = bytes4 + bytes6;
+    const int per_cu0 = wbytes > ((int64_t)64 << 20) ? JLLM_GEMV_WG_PER_CU_BIG
+                      : (wbytes < ((int64_t)12 << 20) ? JLLM_GEMV_WG_PER_CU_SMALL : JLLM_GEMV_WG_PER_CU);
     for (int per_cu = per_cu0; per_cu >= 1 && grid == 0; per_cu--) {
         split((int64_t)device_cus() * per_cu);
         if (fits(per_cu)) grid = (int64_t)device_cus() * per_cu;
