@@ -119,6 +119,27 @@ int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uin
             if (e != hipSuccess) return launch_status(e, tag);
         }
     }
+    // all-Q4_K products whose row tiles together cover the chip without
+    // split-K (e.g. Q/K/V, or gate/up, of a 512-token chunk): one launch --
+    // each tile is computed exactly as in its own launch without split-K
+    {
+        const uint8_t* Wm[3];
+        void* ym[3];
+        int Mm[3], nm = 0;
+        int64_t rtiles = 0;
+        bool all4 = n <= 3;
+        for (int i = 0; i < n && all4; i++) {
+            if (outs[i].M == 0) continue;
+            if (outs[i].type != 12) { all4 = false; break; }
+            const void* Wd = device_weight(tag, outs[i].W);
+            if (!Wd) return JLLM_ERR_POINTER;
+            if (!aligned16(Wd)) return JLLM_ERR_INVALID;
+            Wm[nm] = (const uint8_t*)Wd; ym[nm] = outs[i].y; Mm[nm] = outs[i].M; nm++;
+            rtiles += (outs[i].M + 127) / 128;
+        }
+        if (all4 && nm >= 2 && rtiles * (npad_of(N) / MMQ_TILE_N) >= MMQ_MULTI_MIN_TILES)
+            return launch_status(mmq_q4k_multi_launch(Wm, ym, Mm, nm, codes, scl[0], N, K, npad_of(N), hs), tag);
+    }
     for (int i = 0; i < n; i++) {
         if (outs[i].M == 0) continue;
         const void* Wd = device_weight(tag, outs[i].W);
@@ -142,6 +163,13 @@ int jllm_hip_gemm_quant_batched(uint16_t* y, const void* W, int type, const uint
     return run_mmq("GEMM", y, W, type, x, M, N, K, 0, stream);
 }
 
+int jllm_hip_gemm_quant_batched_multi(uint16_t* const* y, const void* const* W, const int* ggml_type, const int* M,
+                                      int n, const uint16_t* x, int N, int K, void* stream) {
+    if (!y || !W || !ggml_type || !M || n < 1 || n > 3) return JLLM_ERR_INVALID;
+    GemmOut outs[3];
+    for (int i = 0; i < n; i++) outs[i] = GemmOut{y[i], W[i], ggml_type[i], M[i]};
+    return gemm_batched_shared_x("GEMM", outs, n, x, N, K, stream);
+}
 int jllm_hip_gemm_quant_batched_f32(float* y, const void* W, int type, const uint16_t* x,
                                     int M, int N, int K, void* stream) {
     int st = check_gemm("GEMM", y, type, x, M, N, K, true); if (st) return st;

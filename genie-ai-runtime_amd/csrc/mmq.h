@@ -28,6 +28,24 @@ inline size_t mmq_scales_bytes(int K, int Npad) { return (size_t)(K / 32) * Npad
 hipError_t mmq_launch(void* y, const uint8_t* W, int type, const uint16_t* codes, const uint32_t* scl, int M, int N,
                       int K, int Npad, int out_kind, int splits, hipStream_t st);
 
+// Weight matrices of one multi-matrix launch (row tiles of segment s:
+// [rt0[s], rt0[s+1]) of the grid's row-tile index; unused segments M = 0).
+struct MmqSegs {
+    const uint8_t* W[3];
+    void* y[3];
+    int M[3];
+    int rt0[4];
+};
+
+// tile count from which a multi-matrix launch needs no split-K (the
+// threshold of mmq_splits)
+constexpr int MMQ_MULTI_MIN_TILES = 384;
+
+// Q4_K only, fp16 y, no split: the nseg (<= 3) products W[s] . x -> y[s]
+// of one quantised activation, one launch over all their row tiles.
+hipError_t mmq_q4k_multi_launch(const uint8_t* const* W, void* const* y, const int* M, int nseg, const uint16_t* codes,
+                                const uint32_t* scl, int N, int K, int Npad, hipStream_t st);
+
 // Split count for an N x M x K GEMM: enough workgroups to cover the chip
 // when the tile grid alone does not (at least 2 super-blocks per range,
 // at most 16 ranges); a function of M, ceil(N / 64) and K only.

@@ -200,10 +200,12 @@ __device__ __forceinline__ f32x16m mfma16(h8m a, h8m b, f32x16m c) {
 // ---------------------------------------------------------------------------
 // Q4_K
 
+// Up to three weight matrices (same K, same activation) in one launch: the
+// row tiles of segment s are [rt0[s], rt0[s+1]) of the grid's row-tile index.
 template <int OUT>   // 0: fp16 y [N][M], 1: fp32 y [N][M], 2: int32 dots [N][M][K/32]
 __global__ __launch_bounds__(MMQ_THREADS, 2)
-void mmq_q4k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const uint16_t* __restrict__ codes,
-                    const uint32_t* __restrict__ scl, int M, int N, int K, int Npad, int sps) {
+void mmq_q4k_kernel(MmqSegs sg, const uint16_t* __restrict__ codes,
+                    const uint32_t* __restrict__ scl, int N, int K, int Npad, int sps) {
     __shared__ __attribute__((aligned(16))) uint8_t sA[2][TM * A4_STRIDE];
     __shared__ __attribute__((aligned(16))) uint8_t sB[2][TN * B_STRIDE];
     __shared__ __attribute__((aligned(16))) _Float16 sDA[2][8 * TM];     // half(d*sc) per [j][row]
@@ -213,9 +215,14 @@ void mmq_q4k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const u
     const int nb = K / QK_K, nst = 2 * nb;
     // split-K: this workgroup's stages [k0, k1) (whole super-blocks)
     const int k0 = 2 * (int)blockIdx.y * sps, k1 = min(nst, k0 + 2 * sps);
-    const int n_rt = (M + TM - 1) / TM, n_tt = Npad / TN;
+    const int n_rt = sg.rt0[3], n_tt = Npad / TN;
     const int tile = xcd_tile(blockIdx.x, n_rt * n_tt);
-    const int row0 = (tile / n_tt) * TM, col0 = (tile % n_tt) * TN;
+    const int rt = tile / n_tt;
+    const int sgi = rt >= sg.rt0[1] ? (rt >= sg.rt0[2] ? 2 : 1) : 0;
+    void* __restrict__ y = sg.y[sgi];
+    const uint8_t* __restrict__ W = sg.W[sgi];
+    const int M = sg.M[sgi];
+    const int row0 = (rt - sg.rt0[sgi]) * TM, col0 = (tile % n_tt) * TN;
     const int t = threadIdx.x, w = t >> 6, l = t & 63, li = l & 31, g = l >> 5;
     const int arow = 32 * w + li;                    // A-operand row of this lane (wave w owns rows 32w..32w+31)
     const uint32_t gmask = g ? 0u : 0xFFFFu;         // keeps the low fp16 of a word in lanes g = 0 only
@@ -614,9 +621,13 @@ hipError_t mmq_launch(void* y, const uint8_t* W, int type, const uint16_t* codes
     if (splits < 1 || (splits > 1 && out_kind != 1) || (splits - 1) * sps >= nb) return hipErrorInvalidValue;
     const dim3 grid(tiles, splits);
     if (type == TYPE_Q4_K) {
-        if (out_kind == 0) hipLaunchKernelGGL(mmq_q4k_kernel<0>, grid, dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad, sps);
-        else if (out_kind == 1) hipLaunchKernelGGL(mmq_q4k_kernel<1>, grid, dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad, sps);
-        else hipLaunchKernelGGL(mmq_q4k_kernel<2>, grid, dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad, sps);
+        MmqSegs sg;
+        for (int i = 0; i < 3; i++) { sg.W[i] = W; sg.y[i] = y; sg.M[i] = i == 0 ? M : 0; }
+        sg.rt0[0] = 0;
+        for (int i = 1; i < 4; i++) sg.rt0[i] = (M + TM - 1) / TM;
+        if (out_kind == 0) hipLaunchKernelGGL(mmq_q4k_kernel<0>, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, sps);
+        else if (out_kind == 1) hipLaunchKernelGGL(mmq_q4k_kernel<1>, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, sps);
+        else hipLaunchKernelGGL(mmq_q4k_kernel<2>, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, sps);
     } else {
         if (out_kind == 0) hipLaunchKernelGGL(mmq_q6k_kernel<0>, grid, dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad, sps);
         else if (out_kind == 1) hipLaunchKernelGGL(mmq_q6k_kernel<1>, grid, dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad, sps);
@@ -662,10 +673,25 @@ hipError_t splitk_reduce_launch(void* y, const float* ws, int64_t n, int splits,
     return hipGetLastError();
 }
 
+hipError_t mmq_q4k_multi_launch(const uint8_t* const* W, void* const* y, const int* M, int nseg, const uint16_t* codes,
+                                const uint32_t* scl, int N, int K, int Npad, hipStream_t st) {
+    if (nseg < 1 || nseg > 3) return hipErrorInvalidValue;
+    MmqSegs sg;
+    sg.rt0[0] = 0;
+    for (int i = 0; i < 3; i++) {
+        const int j = i < nseg ? i : nseg - 1;
+        sg.W[i] = W[j]; sg.y[i] = y[j]; sg.M[i] = i < nseg ? M[i] : 0;
+        sg.rt0[i + 1] = sg.rt0[i] + (sg.M[i] + TM - 1) / TM;
+    }
+    const dim3 grid(sg.rt0[3] * (Npad / TN), 1);
+    hipLaunchKernelGGL(mmq_q4k_kernel<0>, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, K / QK_K);
+    return hipGetLastError();
+}
+
 int mmq_splits(int M, int N, int K) {
     const int64_t tiles = (int64_t)((M + TM - 1) / TM) * ((N + TN - 1) / TN);
     const int nb = K / QK_K;
-    if (tiles >= 384 || nb < 4) return 1;
+    if (tiles >= MMQ_MULTI_MIN_TILES || nb < 4) return 1;
     int S = (int)std::min<int64_t>((512 + tiles - 1) / tiles, 16);
     S = std::min(S, nb / 2);
     if (S < 2) return 1;

@@ -38,6 +38,7 @@ SIGNATURES = {
     "jllm_hip_gemv_quant_f32_rmsnorm": (I, [P, P, I, P, P, I, F, I, I, P]),
     "jllm_hip_gemm_quant_batched": (I, [P, P, I, P, I, I, I, P]),
     "jllm_hip_gemm_quant_batched_f32": (I, [P, P, I, P, I, I, I, P]),
+    "jllm_hip_gemm_quant_batched_multi": (I, [P, P, P, P, I, P, I, I, P]),
     "jllm_hip_quantize_mmq_q8_1": (I, [P, P, I, I, I, I, P]),
     "jllm_hip_mmq_subdots": (I, [P, P, I, P, I, I, I, P]),
     "jllm_hip_flash_attention_decode": (I, [P, P, P, P, I, I, I, I, I, F, I, P, P, I, P]),

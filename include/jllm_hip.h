@@ -141,6 +141,17 @@ int jllm_hip_gemm_quant_batched(uint16_t* y, const void* W, int ggml_type, const
 int jllm_hip_gemm_quant_batched_f32(float* y, const void* W, int ggml_type, const uint16_t* x,
                                     int M, int N, int K, void* stream);
 
+/* Several products of ONE activation: y[i] [N x M[i]] (fp16) = x . W[i]^T for
+ * i < n (n <= 3, shared K), the activation quantised once per kind.  When
+ * every W[i] is Q4_K and their row tiles together cover the GPU, all of them
+ * run as one launch without split-K (each output computed exactly as its own
+ * launch without split-K would); otherwise one product at a time as
+ * jllm_hip_gemm_quant_batched.  No reference counterpart: the engine issues
+ * Q/K/V and gate/up as separate gemm_quant_batched calls (decode.cu:1797-1880);
+ * this is the decoder's prefill path. */
+int jllm_hip_gemm_quant_batched_multi(uint16_t* const* y, const void* const* W, const int* ggml_type, const int* M,
+                                      int n, const uint16_t* x, int N, int K, void* stream);
+
 /* The MMQ activation quantiser on its own: x [N x K] fp16 -> q8 [K/128][Npad]
  * blocks of 144 B.  ds4 != 0: DS4 layout {half2 (d, sum x)[4], i8 qs[128]}
  * (quantize_mmq_q8_1_ds4, mmq_q4k_llama.cu:383); ds4 == 0: D4 layout

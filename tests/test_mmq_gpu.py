@@ -235,3 +235,47 @@ def test_mmq_vs_true_fp16_product(dev, t, M, N, K):
     assert rel_rms < 0.01, rel_rms
     bad = (np.abs(err) > 0.02 * np.abs(ref)) & (np.abs(err) > 0.05 * sigma)
     assert not bad.any(), int(bad.sum())
+
+
+def _multi(outs, Ws, types, Ms, x, N, K):
+    import ctypes
+    n = len(Ws)
+    ya = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+    wa = (ctypes.c_void_p * n)(*[w.data_ptr() for w in Ws])
+    ta = (ctypes.c_int * n)(*types)
+    ma = (ctypes.c_int * n)(*Ms)
+    jllm.call("jllm_hip_gemm_quant_batched_multi", ctypes.cast(ya, ctypes.c_void_p), ctypes.cast(wa, ctypes.c_void_p),
+              ctypes.cast(ta, ctypes.c_void_p), ctypes.cast(ma, ctypes.c_void_p), n, x, N, K)
+
+
+@pytest.mark.parametrize("Ms,types,N", [
+    ((9728, 9728), (12, 12), 512),          # gate/up of a 512-token chunk: one launch, 1216 tiles
+    ((4096, 1024, 1024), (12, 12, 12), 512),  # Q/K/V: one launch, 384 tiles
+    ((4096, 1024, 1024), (12, 12, 12), 40),   # too few tiles: one launch per matrix (split-K)
+    ((2560, 2560), (12, 14), 512),          # mixed types: one launch per matrix
+])
+def test_gemm_multi_matches_separate_products(dev, Ms, types, N):
+    """The multi-matrix product equals each matrix's own gemm_quant_batched
+    bit for bit where neither splits K; where the single launch splits K, the
+    two agree within the fp32 parity bar (and the fp32 single launch is pinned
+    against the oracle by the tests above)."""
+    print_case("gemm_multi", Ms, types, N)
+    K = 2560
+    g = synth.rng(sum(Ms) + N)
+    Ws = [to_dev(synth.weights(g, t, M, K)) for t, M in zip(types, Ms)]
+    x = to_dev(synth.x_f16(g, (N, K)))
+    outs = [torch.full((N * M,), 0x7C00, dtype=torch.int16, device=dev) for M in Ms]
+    _multi(outs, Ws, types, Ms, x, N, K)
+    for o, W, t, M in zip(outs, Ws, types, Ms):
+        single = torch.empty(N * M, dtype=torch.int16, device=dev)
+        jllm.call("jllm_hip_gemm_quant_batched", single, W, t, x, M, N, K)
+        ref32 = torch.empty(N * M, dtype=torch.float32, device=dev)
+        jllm.call("jllm_hip_gemm_quant_batched_f32", ref32, W, t, x, M, N, K)
+        torch.cuda.synchronize()
+        got = f16_to_f64(from_dev(o, np.uint16))
+        sgl = f16_to_f64(from_dev(single, np.uint16))
+        tiles = lambda m: ((m + 127) // 128) * _npad(N) // 64
+        one_launch = all(tt == 12 for tt in types) and sum(tiles(m) for m in Ms) >= 384
+        if not one_launch or tiles(M) >= 384:       # same arithmetic as the single launch
+            assert np.array_equal(got, sgl)
+        assert rel_inf(got, from_dev(ref32).astype(np.float64)) <= TOL
