@@ -49,5 +49,11 @@ struct DeviceScratch {
 // checked as there.
 struct GemmOut { uint16_t* y; const void* W; int type; int M; };
 int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uint16_t* x, int N, int K, void* stream);
+// y [N x M] = half(half(a . W^T) + res) with a = x, or, when up is given,
+// a = half(silu(x) * up) (the SwiGLU of gate x and up, formed inside the
+// activation quantiser; act_tmp [N x K] holds it where a path needs it in
+// memory): the engine's projection + residual add (decode.cu:1830-1884).
+int gemm_batched_res(const char* tag, uint16_t* y, const void* W, int type, const uint16_t* x, const uint16_t* up,
+                     uint16_t* act_tmp, const uint16_t* res, int M, int N, int K, void* stream);
 
 }  // namespace jllm_hip

@@ -4,6 +4,7 @@
 // fp16 GEMM (the reference runs Q5_K in float, gemv_q4.cu:2436-2440).
 #include "capi_common.h"
 #include "mmq.h"
+#include "layer_ops.h"
 
 using namespace jllm_hip;
 
@@ -32,7 +33,8 @@ int check_gemm(const char* tag, const void* y, int type, const uint16_t* x, int 
 // The product of an already quantised activation (q8 = codes + scale words
 // of the right kind, or null for Q5_K) into y.
 int mmq_after_quant(const char* tag, void* y, const void* Wd, int type, const uint16_t* x, const uint16_t* codes,
-                    const uint32_t* scl, int M, int N, int K, int out_kind, hipStream_t st) {
+                    const uint32_t* scl, int M, int N, int K, int out_kind, hipStream_t st,
+                    const uint16_t* res = nullptr) {
     // split-K when the tile grid alone does not cover the chip: partials to
     // the workspace, then one ordered reduction into y
     const int splits = out_kind == 2 ? 1 : mmq_splits(M, N, K);
@@ -48,7 +50,8 @@ int mmq_after_quant(const char* tag, void* y, const void* Wd, int type, const ui
     hipError_t e;
     if (type == 13) e = gemm_q5k_launch(dst, (const uint8_t*)Wd, x, M, N, K, kind, splits, st);
     else e = mmq_launch(dst, (const uint8_t*)Wd, type, codes, scl, M, N, K, npad_of(N), kind, splits, st);
-    if (e == hipSuccess && splits > 1) e = splitk_reduce_launch(y, (const float*)dst, (int64_t)N * M, splits, out_kind, st);
+    if (e == hipSuccess && splits > 1) e = splitk_reduce_launch(y, (const float*)dst, (int64_t)N * M, splits, out_kind, st, res);
+    else if (e == hipSuccess && res) e = vec_add_launch((uint16_t*)y, (const uint16_t*)y, res, (int64_t)N * M, st);
     return launch_status(e, tag);
 }
 
@@ -91,6 +94,37 @@ int run_mmq(const char* tag, void* y, const void* W, int type, const uint16_t* x
 }  // namespace
 
 namespace jllm_hip {
+int gemm_batched_res(const char* tag, uint16_t* y, const void* W, int type, const uint16_t* x, const uint16_t* up,
+                     uint16_t* act_tmp, const uint16_t* res, int M, int N, int K, void* stream) {
+    int st = check_gemm(tag, y, type, x, M, N, K, true); if (st) return st;
+    if (M == 0 || N == 0) return JLLM_OK;
+    if (!res || (up && (!act_tmp || !aligned16(up)))) return JLLM_ERR_INVALID;
+    hipStream_t hs = (hipStream_t)stream;
+    if (N == 1 || type == 13) {
+        // no fused form: the SwiGLU into act_tmp, the product, the residual add
+        if (up) {
+            const hipError_t e = swiglu_launch(act_tmp, x, up, (int64_t)N * K, hs);
+            if (e != hipSuccess) return launch_status(e, tag);
+            x = act_tmp;
+        }
+        if (N == 1) {
+            st = jllm_hip_gemv_quant_add(y, W, type, x, res, M, K, stream);
+            return st;
+        }
+    }
+    const void* Wd = device_weight(tag, W);
+    if (!Wd) return JLLM_ERR_POINTER;
+    if (!aligned16(Wd)) return JLLM_ERR_INVALID;
+    uint16_t* codes = nullptr;
+    uint32_t* scl[2] = {nullptr, nullptr};
+    if (type != 13) {
+        st = q8_scratch(tag, N, K, codes, scl); if (st) return st;
+        const hipError_t e = quantize_mmq_f16_launch(x, codes, scl[0], N, K, npad_of(N), type == 12, hs, up);
+        if (e != hipSuccess) return launch_status(e, tag);
+    }
+    return mmq_after_quant(tag, y, Wd, type, x, codes, scl[0], M, N, K, 0, hs, res);
+}
+
 int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uint16_t* x, int N, int K, void* stream) {
     for (int i = 0; i < n; i++) {
         int st = check_gemm(tag, outs[i].y, outs[i].type, x, outs[i].M, N, K, true); if (st) return st;

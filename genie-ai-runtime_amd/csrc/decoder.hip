@@ -28,6 +28,7 @@
 using jllm_hip::launch_status;
 using jllm_hip::GemmOut;
 using jllm_hip::gemm_batched_shared_x;
+using jllm_hip::gemm_batched_res;
 
 struct jllm_hip_decoder {
     jllm_hip_decoder_config cfg;
@@ -121,14 +122,11 @@ int prefill_layer(jllm_hip_decoder* d, int l, int start, int N, void* st) {
                                                  c.n_kv_heads, c.head_dim, c.head_dim, N, start, attn_scale(c),
                                                  c.kv_int8, c.kv_int8 ? layer_ks(d, l) : nullptr,
                                                  c.kv_int8 ? layer_vs(d, l) : nullptr, 0, st));
-    TRY(jllm_hip_gemm_quant_batched(d->proj, w.wo, w.type_wo, d->attn, H, N, QD, st));
-    TRY(jllm_hip_vec_add(d->x2, d->x, d->proj, (int64_t)N * H, st));
+    TRY(gemm_batched_res("decoder", d->x2, w.wo, w.type_wo, d->attn, nullptr, nullptr, d->x, H, N, QD, st));
     TRY(jllm_hip_fused_rmsnorm_residual(d->normed, d->x2, nullptr, w.rms_ffn, N, H, c.rms_eps, c.norm_fp32, st));
     const GemmOut gu[2] = {{d->gate, w.w_gate, w.type_w_gate, I}, {d->up, w.w_up, w.type_w_up, I}};
     TRY(gemm_batched_shared_x("decoder", gu, 2, d->normed, N, H, st));
-    TRY(jllm_hip_fused_swiglu(d->act, d->gate, d->up, N, I, st));
-    TRY(jllm_hip_gemm_quant_batched(d->proj, w.w_down, w.type_w_down, d->act, H, N, I, st));
-    TRY(jllm_hip_vec_add(d->x, d->x2, d->proj, (int64_t)N * H, st));
+    TRY(gemm_batched_res("decoder", d->x, w.w_down, w.type_w_down, d->gate, d->up, d->act, d->x2, H, N, I, st));
     return JLLM_OK;
 }
 

@@ -25,6 +25,12 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
 __device__ __forceinline__ float round_to_f16(float f) {
     return (float)(_Float16)f;
 }
+// silu(g) * u in fp32 as the reference's swiglu_kernel evaluates it
+// (convert.cu:85-112), no contraction
+__device__ __forceinline__ float silu_mul(float g, float u) {
+#pragma clang fp contract(off)
+    return g / (1.0f + expf(-g)) * u;
+}
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 __device__ __forceinline__ uint32_t h2_bits(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
 

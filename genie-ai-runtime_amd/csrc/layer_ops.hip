@@ -145,10 +145,6 @@ hipError_t rmsnorm_launch(uint16_t* out, const uint16_t* x, const uint16_t* res,
 // Element-wise: SwiGLU out = half(g / (1 + e^-g) * u) and the residual add
 // out = half(a + b).  Eight elements per thread (16-byte accesses) over the
 // aligned body, one element per thread for the tail.
-__device__ __forceinline__ float silu_mul(float g, float u) {
-#pragma clang fp contract(off)
-    return g / (1.0f + expf(-g)) * u;
-}
 
 template <int OP, bool V>
 __global__ __launch_bounds__(256) void eltwise_kernel(uint16_t* __restrict__ out, const uint16_t* __restrict__ a,

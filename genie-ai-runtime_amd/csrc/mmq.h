@@ -16,8 +16,9 @@ hipError_t quantize_mmq_launch(const uint16_t* x, void* q8, int N, int K, int Np
 
 // the same values in the kernels' layout: codes fp16 [K/256][Npad][256],
 // scale words [K/32][Npad] (DS4: half d | half sum << 16; D4: float d)
+// (up != null: the values are half(silu(x) * up), the SwiGLU of gate x and up)
 hipError_t quantize_mmq_f16_launch(const uint16_t* x, uint16_t* codes, uint32_t* scl, int N, int K, int Npad,
-                                   bool ds4, hipStream_t st);
+                                   bool ds4, hipStream_t st, const uint16_t* up = nullptr);
 inline size_t mmq_codes_bytes(int K, int Npad) { return (size_t)K * Npad * 2; }
 inline size_t mmq_scales_bytes(int K, int Npad) { return (size_t)(K / 32) * Npad * 4; }
 
@@ -52,7 +53,9 @@ hipError_t mmq_q4k_multi_launch(const uint8_t* const* W, void* const* y, const i
 int mmq_splits(int M, int N, int K);
 
 // y = sum of the `splits` fp32 partials ws[s][n], added in order s = 0, 1, ...
-hipError_t splitk_reduce_launch(void* y, const float* ws, int64_t n, int splits, int out_kind, hipStream_t st);
+// (fp16 out with res: y = half(half(sum) + res))
+hipError_t splitk_reduce_launch(void* y, const float* ws, int64_t n, int splits, int out_kind, hipStream_t st,
+                                const uint16_t* res = nullptr);
 
 // Q5_K batched GEMM (fp16 activation, no quantisation): out_kind 0 = fp16
 // y[N x M], 1 = fp32 y[N x M]

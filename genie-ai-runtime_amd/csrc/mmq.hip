@@ -100,7 +100,11 @@ hipError_t quantize_mmq_launch(const uint16_t* x, void* q8, int N, int K, int Np
 // 1 over the value index), the order of the reference-layout quantiser
 // above: index bit 4 pairs lanes sub ^ 2, bit 3 lanes sub ^ 1, bits 2..0
 // stay within the lane -- so d and the sum are the same floats.
+// SW: the values are half(silu(gate) * up) of two fp16 inputs (x = gate,
+// x2 = up), formed here exactly as the SwiGLU kernel rounds them.
+template <bool SW>
 __global__ __launch_bounds__(256) void quantize_mmq_f16_kernel(const uint16_t* __restrict__ x,
+                                                               const uint16_t* __restrict__ x2,
                                                                uint16_t* __restrict__ codes,
                                                                uint32_t* __restrict__ scl, int N, int K, int Npad,
                                                                int ds4) {
@@ -113,8 +117,17 @@ __global__ __launch_bounds__(256) void quantize_mmq_f16_kernel(const uint16_t* _
     const int kb32 = (int)(cb % kb), col = (int)(cb / kb);
     uint32_t w[4] = {0u, 0u, 0u, 0u};
     if (col < N) {
-        const u32x4m u = *(const u32x4m*)(x + (int64_t)col * K + kb32 * 32 + 8 * sub);
+        const int64_t off = (int64_t)col * K + kb32 * 32 + 8 * sub;
+        const u32x4m u = *(const u32x4m*)(x + off);
         w[0] = u.x; w[1] = u.y; w[2] = u.z; w[3] = u.w;
+        if (SW) {
+            const u32x4m u2 = *(const u32x4m*)(x2 + off);
+            const uint32_t w2[4] = {u2.x, u2.y, u2.z, u2.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                w[e] = (uint32_t)f32_to_f16_bits(silu_mul(f16_bits_to_f32(w[e] & 0xFFFFu), f16_bits_to_f32(w2[e] & 0xFFFFu))) |
+                       ((uint32_t)f32_to_f16_bits(silu_mul(f16_bits_to_f32(w[e] >> 16), f16_bits_to_f32(w2[e] >> 16))) << 16);
+        }
     }
     float v[8];
 #pragma unroll
@@ -147,10 +160,11 @@ __global__ __launch_bounds__(256) void quantize_mmq_f16_kernel(const uint16_t* _
 }
 
 hipError_t quantize_mmq_f16_launch(const uint16_t* x, uint16_t* codes, uint32_t* scl, int N, int K, int Npad,
-                                   bool ds4, hipStream_t st) {
+                                   bool ds4, hipStream_t st, const uint16_t* up) {
     const int64_t nthr = (int64_t)Npad * (K / 32) * 4;
-    hipLaunchKernelGGL(quantize_mmq_f16_kernel, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, st, x, codes, scl,
-                       N, K, Npad, ds4 ? 1 : 0);
+    const dim3 g((unsigned)((nthr + 255) / 256));
+    if (up) hipLaunchKernelGGL(quantize_mmq_f16_kernel<true>, g, dim3(256), 0, st, x, up, codes, scl, N, K, Npad, ds4 ? 1 : 0);
+    else    hipLaunchKernelGGL(quantize_mmq_f16_kernel<false>, g, dim3(256), 0, st, x, x, codes, scl, N, K, Npad, ds4 ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -637,9 +651,12 @@ hipError_t mmq_launch(void* y, const uint8_t* W, int type, const uint16_t* codes
 }
 
 // y[i] = sum over s = 0..S-1 (in order) of ws[s][i]; fp16 or fp32 out
+// OUT 0: fp16, 1: fp32, 2: fp16 of fp16(sum) + res (the engine's residual add
+// after the projection, one more fp16 rounding)
 template <int OUT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(void* __restrict__ y, const float* __restrict__ ws,
-                                                            int64_t n, int S) {
+                                                            int64_t n, int S, const uint16_t* __restrict__ res) {
+#pragma clang fp contract(off)
     const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= n) return;
     if (i + 4 <= n && (n & 3) == 0) {
@@ -650,6 +667,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(void* __restrict__ y
         }
         if (OUT == 1) {
             *(f32x4m*)((float*)y + i) = a;
+        } else if (OUT == 2) {
+            const u32x2m r = *(const u32x2m*)(res + i);
+            const float s0 = round_to_f16(a.x) + f16_bits_to_f32(r.x & 0xFFFFu), s1 = round_to_f16(a.y) + f16_bits_to_f32(r.x >> 16);
+            const float s2 = round_to_f16(a.z) + f16_bits_to_f32(r.y & 0xFFFFu), s3 = round_to_f16(a.w) + f16_bits_to_f32(r.y >> 16);
+            *(u32x2m*)((uint16_t*)y + i) = u32x2m{(uint32_t)f32_to_f16_bits(s0) | ((uint32_t)f32_to_f16_bits(s1) << 16),
+                                                  (uint32_t)f32_to_f16_bits(s2) | ((uint32_t)f32_to_f16_bits(s3) << 16)};
         } else {
             const u32x2m o = u32x2m{(uint32_t)f32_to_f16_bits(a.x) | ((uint32_t)f32_to_f16_bits(a.y) << 16),
                                     (uint32_t)f32_to_f16_bits(a.z) | ((uint32_t)f32_to_f16_bits(a.w) << 16)};
@@ -661,15 +684,18 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(void* __restrict__ y
         float a = ws[e];
         for (int s = 1; s < S; s++) a += ws[(int64_t)s * n + e];
         if (OUT == 1) ((float*)y)[e] = a;
+        else if (OUT == 2) ((uint16_t*)y)[e] = f32_to_f16_bits(round_to_f16(a) + f16_bits_to_f32(res[e]));
         else          ((uint16_t*)y)[e] = f32_to_f16_bits(a);
     }
 }
 
-hipError_t splitk_reduce_launch(void* y, const float* ws, int64_t n, int splits, int out_kind, hipStream_t st) {
+hipError_t splitk_reduce_launch(void* y, const float* ws, int64_t n, int splits, int out_kind, hipStream_t st,
+                                const uint16_t* res) {
     if (n <= 0) return hipSuccess;
     const int64_t blocks = (n + 1023) / 1024;
-    if (out_kind == 1) hipLaunchKernelGGL(splitk_reduce_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, st, y, ws, n, splits);
-    else               hipLaunchKernelGGL(splitk_reduce_kernel<0>, dim3((unsigned)blocks), dim3(256), 0, st, y, ws, n, splits);
+    if (out_kind == 1) hipLaunchKernelGGL(splitk_reduce_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, st, y, ws, n, splits, res);
+    else if (res)      hipLaunchKernelGGL(splitk_reduce_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, st, y, ws, n, splits, res);
+    else               hipLaunchKernelGGL(splitk_reduce_kernel<0>, dim3((unsigned)blocks), dim3(256), 0, st, y, ws, n, splits, res);
     return hipGetLastError();
 }
 
