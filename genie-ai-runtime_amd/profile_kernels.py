@@ -7,6 +7,7 @@
           of a 512-token prompt, then 32 greedy decode steps
   copy  : a plain device-to-device copy of 256 MiB (calibrates FETCH_SIZE /
           WRITE_SIZE against a known byte count)
+  mmq   : the Q4_K prefill GEMM 9728 x 2560 at N = 512 tokens (fp16 out), 5 calls
 """
 import os
 import sys
@@ -54,6 +55,12 @@ def main(mode):
         d.generate(prompt, 33, toks)
         torch.cuda.synchronize()
         d.close()
+    elif mode == "mmq":
+        W = up(synth.q4k(g, 9728, 2560))
+        x = up(synth.x_f16(g, (512, 2560)))
+        y = torch.empty(512 * 9728, dtype=torch.int16, device=dev)
+        for _ in range(5):
+            jllm.call("jllm_hip_gemm_quant_batched", y, W, 12, x, 9728, 512, 2560)
     elif mode == "copy":
         a = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
         b = torch.empty_like(a)
