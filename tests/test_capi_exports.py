@@ -78,6 +78,14 @@ def test_argument_validation_without_gpu():
     assert l.jllm_hip_gemv_quant(None, None, 13, None, 4, 256, None) != 0
     assert l.jllm_hip_gemm_quant_batched(None, None, 12, None, 4, 4, 300, None) == -1
     assert l.jllm_hip_quantize_mmq_q8_1(None, None, 1, 128, 64, 1, None) == -1
+    import ctypes
+    ys, ws = (ctypes.c_void_p * 4)(), (ctypes.c_void_p * 4)()
+    ts, ms = (ctypes.c_int * 4)(12, 12, 12, 12), (ctypes.c_int * 4)(256, 256, 256, 256)
+    args = [ctypes.cast(a, ctypes.c_void_p) for a in (ys, ws, ts, ms)]
+    assert l.jllm_hip_gemm_quant_batched_multi(*args, 4, None, 8, 256, None) == -1      # more than 3 products
+    assert l.jllm_hip_gemm_quant_batched_multi(*args, 0, None, 8, 256, None) == -1      # none
+    assert l.jllm_hip_gemm_quant_batched_multi(*args, 2, None, 8, 300, None) == -1      # K % 256
+    assert l.jllm_hip_gemm_quant_batched_multi(None, None, None, None, 2, None, 8, 256, None) == -1
 
 
 def test_layer_op_argument_validation_without_gpu():
