@@ -88,11 +88,16 @@ size_t attn_scratch_bytes(int n_heads, int n_splits, int head_dim) {
     return ATTN_COUNTER_BYTES + attn_partials_floats(n_heads, n_splits, head_dim) * sizeof(float);
 }
 
-__host__ __device__ size_t attn_lds_bytes(int n_heads, int n_kv, int head_dim, int tq) {
+// LDS of one wave (P' tile, per-key scales, then its final hi/lo rows)
+__host__ __device__ size_t attn_wave_lds_bytes(int n_heads, int n_kv, int head_dim, int tq) {
     const int G = n_heads / n_kv * tq;                                // columns of a wave
     const size_t loop = (size_t)32 * AT_KEYS * 2 + 96 * 4;            // P' rows (fp16) + corr/ks/vs
     const size_t outb = (size_t)2 * G * head_dim * 4;                 // final hi/lo rows (fp32)
-    return loop > outb ? loop : outb;
+    return ((loop > outb ? loop : outb) + 15) & ~(size_t)15;
+}
+// a workgroup of W waves: W wave regions, then (m, l) of each wave's columns
+__host__ __device__ size_t attn_lds_bytes(int n_heads, int n_kv, int head_dim, int tq, int W) {
+    return (size_t)W * attn_wave_lds_bytes(n_heads, n_kv, head_dim, tq) + (W > 1 ? (size_t)W * 2 * 32 * 4 : 0);
 }
 
 // One wave per (KV head, split[, block of tq query tokens]).  The wave's
@@ -113,7 +118,7 @@ __host__ __device__ size_t attn_lds_bytes(int n_heads, int n_kv, int head_dim, i
 // MT: several query tokens per wave (per-column causal bounds); the
 // single-token form (decode, or tq == 1) compiles without the column masks.
 template <bool INT8, int HD, bool MT>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(64 * ATTN_PREFILL_WAVES) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_partial_kernel(AttnArgs a) {
     constexpr int EB = INT8 ? 1 : 2;
     constexpr int hd = HD, half = HD / 2;
@@ -121,12 +126,16 @@ void attn_partial_kernel(AttnArgs a) {
     constexpr int NDT = HD / 32;                        // 32-wide d chunks
     constexpr int VW = NDT * EB;                        // V: 16-byte chunks per lane
     constexpr int NST = half / 8;                       // Q.K^T MFMA steps
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem_wg[];
+    const int W = MT ? a.wsplit : 1;
+    const int wv = MT ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
+    const size_t wave_lds = attn_wave_lds_bytes(a.n_heads, a.n_kv, a.head_dim, a.tq);
+    uint8_t* smem = smem_wg + (size_t)wv * wave_lds;
     const int kvh = blockIdx.x, split = blockIdx.y, tok0 = MT ? blockIdx.z * a.tq : blockIdx.z;
     const int G = a.n_heads / a.n_kv;
     const int ntok = MT ? min(a.tq, a.tokens - tok0) : 1;       // tokens of this wave
     const int GC = ntok * G;                                    // live columns
-    const int l = threadIdx.x, li = l & 31, lg = l >> 5;
+    const int l = (int)threadIdx.x & 63, li = l & 31, lg = l >> 5;
     // column li: its token, causal bound and window start
     const int ctok = MT ? tok0 + (li < GC ? li / G : 0) : tok0;
     const int seq_c = a.seq + ctok;
@@ -317,15 +326,17 @@ void attn_partial_kernel(AttnArgs a) {
     };
     // the next tile's rows load into (rk, rv) while the current one (a copy)
     // is computed
-    if (kv0 < kv1) load_tile(kv0, rk, rv, ksn, vsn);
-    for (int p0 = kv0; p0 < kv1; p0 += AT_KEYS) {
+    // wave wv of W takes tiles wv, wv + W, ... of the workgroup's key range
+    const int first = kv0 + wv * AT_KEYS, stride = W * AT_KEYS;
+    if (first < kv1) load_tile(first, rk, rv, ksn, vsn);
+    for (int p0 = first; p0 < kv1; p0 += stride) {
         u32x4a ck[KW], cv[VW];
 #pragma unroll
         for (int c = 0; c < KW; c++) ck[c] = rk[c];
 #pragma unroll
         for (int c = 0; c < VW; c++) cv[c] = rv[c];
         const float ksc = ksn * a.scale, vsc = vsn;
-        if (p0 + AT_KEYS < kv1) load_tile(p0 + AT_KEYS, rk, rv, ksn, vsn);
+        if (p0 + stride < kv1) load_tile(p0 + stride, rk, rv, ksn, vsn);
         tile(p0, ck, cv, ksc, vsc);
     }
 
@@ -345,6 +356,29 @@ void attn_partial_kernel(AttnArgs a) {
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
+    if (MT && W > 1) {
+        // combine the W waves' states per column, waves in order:
+        // out = sum_w acc_w e^(m_w - M) / sum_w l_w e^(m_w - M), M = max_w m_w
+        float* sML = (float*)(smem_wg + (size_t)W * wave_lds);     // [W][m[32] | l[32]]
+        if (lg == 0) { sML[wv * 64 + li] = run_m; sML[wv * 64 + 32 + li] = run_l; }
+        __syncthreads();
+        for (int e = (int)threadIdx.x; e < GC * hd; e += 64 * W) {
+            const int c = e / hd, d = e % hd;
+            float M = -FLT_MAX;
+            for (int u = 0; u < W; u++) M = fmaxf(M, sML[u * 64 + c]);
+            float num = 0.0f, den = 0.0f;
+            for (int u = 0; u < W; u++) {
+                const float f = expf(sML[u * 64 + c] - M);
+                const float* so = (const float*)(smem_wg + (size_t)u * wave_lds);
+                num += (so[c * hd + d] + so[(GC + c) * hd + d]) * f;
+                den += sML[u * 64 + 32 + c] * f;
+            }
+            const int ct = c / G, ch = c % G;
+            uint16_t* ot = a.out + (int64_t)(tok0 + ct) * a.n_heads * hd + (int64_t)(pbase + ch) * hd;
+            ot[d] = f32_to_f16_bits(den > 0.0f ? num / den : 0.0f);
+        }
+        return;
+    }
     if (S == 1) {
         const float inv_l = run_l > 0.0f ? 1.0f / run_l : 0.0f;
         for (int e = l; e < GC * hd; e += 64) {
@@ -441,10 +475,12 @@ hipError_t attn_launch(const AttnArgs& a, bool kv_int8, hipStream_t st) {
         (a.n_heads / a.n_kv) * a.tq > AT_MAXG)
         return hipErrorInvalidValue;
     dim3 grid(a.n_kv, a.n_splits, (a.tokens + a.tq - 1) / a.tq);
-    const size_t lds = attn_lds_bytes(a.n_heads, a.n_kv, a.head_dim, a.tq);
     const bool mt = a.tq > 1;
+    const int W = mt ? a.wsplit : 1;
+    if (W < 1 || W > ATTN_PREFILL_WAVES) return hipErrorInvalidValue;
+    const size_t lds = attn_lds_bytes(a.n_heads, a.n_kv, a.head_dim, a.tq, W);
 #define ATTN_CASE(I8, HDV)                                                                                   \
-    if (mt) hipLaunchKernelGGL((attn_partial_kernel<I8, HDV, true>), grid, dim3(64), lds, st, a);           \
+    if (mt) hipLaunchKernelGGL((attn_partial_kernel<I8, HDV, true>), grid, dim3(64 * W), lds, st, a);       \
     else    hipLaunchKernelGGL((attn_partial_kernel<I8, HDV, false>), grid, dim3(64), lds, st, a);
     switch (a.head_dim * 2 + (kv_int8 ? 1 : 0)) {
     case 64:  ATTN_CASE(false, 32) break;

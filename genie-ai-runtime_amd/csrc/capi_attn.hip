@@ -42,7 +42,7 @@ int attn_run(uint16_t* out, const uint16_t* q, const void* k, const void* v, int
     a.counters = (int*)scratch;
     a.part = (float*)(scratch + ATTN_COUNTER_BYTES);
     a.n_heads = n_heads; a.n_kv = n_kv; a.head_dim = hd; a.cache_head_dim = chd;
-    a.seq = seq; a.window = window; a.n_splits = n_splits; a.scale = scale; a.tokens = 1; a.tq = 1;
+    a.seq = seq; a.window = window; a.n_splits = n_splits; a.scale = scale; a.tokens = 1; a.tq = 1; a.wsplit = 1;
     return launch_status(attn_launch(a, kv_int8 != 0, (hipStream_t)stream), "attention");
 }
 }  // namespace
@@ -89,6 +89,7 @@ int jllm_hip_flash_attention_prefill_batched(uint16_t* out, const uint16_t* q, c
     // several query tokens per wave: each KV tile serves tq tokens x G heads
     a.tq = ATTN_MAX_COLUMNS / (n_heads / n_kv_heads);
     if (a.tq < 1) a.tq = 1;
+    a.wsplit = ATTN_PREFILL_WAVES;     // (used when tq > 1)
     return launch_status(attn_launch(a, kv_int8 != 0, (hipStream_t)stream), "attention prefill");
 }
 
