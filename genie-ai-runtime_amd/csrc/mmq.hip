@@ -718,11 +718,20 @@ int mmq_splits(int M, int N, int K) {
     const int64_t tiles = (int64_t)((M + TM - 1) / TM) * ((N + TN - 1) / TN);
     const int nb = K / QK_K;
     if (tiles >= MMQ_MULTI_MIN_TILES || nb < 4) return 1;
-    int S = (int)std::min<int64_t>((512 + tiles - 1) / tiles, 16);
-    S = std::min(S, nb / 2);
-    if (S < 2) return 1;
-    const int sps = (nb + S - 1) / S;
-    return (nb + sps - 1) / sps;
+    // ranges of whole super-blocks; pick the count that minimises (rounds of
+    // resident workgroups) x (super-blocks per range) -- 2 workgroups per CU
+    // on 256 CUs; e.g. 160 tiles with 38 super-blocks: 3 ranges (480
+    // workgroups, one round of 13) rather than 4 (640: two rounds of 10).
+    // Fewer ranges win ties (less partial traffic).
+    const int64_t slots = 512;
+    int best = 1;
+    int64_t best_cost = ((tiles + slots - 1) / slots) * nb;
+    for (int S = 2; S <= std::min(16, nb / 2); S++) {
+        const int sps = (nb + S - 1) / S, eff = (nb + sps - 1) / sps;
+        const int64_t cost = ((tiles * eff + slots - 1) / slots) * sps;
+        if (cost < best_cost) { best = eff; best_cost = cost; }
+    }
+    return best;
 }
 
 }  // namespace jllm_hip
