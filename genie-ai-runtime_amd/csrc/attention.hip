@@ -470,6 +470,57 @@ void attn_reduce_kernel(uint16_t* __restrict__ out, const float* __restrict__ pa
     }
 }
 
+// The same combination with one wave per head: lane l holds splits l, l+64,
+// ... (m, l) and then sums the acc of every split for d = 2l, 2l+1 in split
+// order; no workgroup barriers.
+__global__ __launch_bounds__(64)
+void attn_reduce_wave_kernel(uint16_t* __restrict__ out, const float* __restrict__ part, int n_heads, int hd, int S) {
+    __shared__ float sW[AT_MAXS];
+    const int h = blockIdx.x, l = threadIdx.x;
+    const float* pm = part + (int64_t)h * S;
+    const float* pl = part + (int64_t)n_heads * S + (int64_t)h * S;
+    const float* pacc = part + (int64_t)n_heads * S * 2 + (int64_t)h * S * hd;
+    float mv[AT_MAXS / 64], lv[AT_MAXS / 64];
+    float mx = -FLT_MAX;
+#pragma unroll
+    for (int i = 0; i < AT_MAXS / 64; i++) {
+        const int sp = l + 64 * i;
+        mv[i] = sp < S ? pm[sp] : -FLT_MAX;
+        lv[i] = sp < S ? pl[sp] : 0.0f;
+        mx = fmaxf(mx, mv[i]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    float L = 0.0f;
+#pragma unroll
+    for (int i = 0; i < AT_MAXS / 64; i++) {
+        const float wgt = l + 64 * i < S ? expf(mv[i] - mx) : 0.0f;
+        sW[l + 64 * i] = wgt;
+        L += lv[i] * wgt;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    if (2 * l >= hd) return;
+    float ox = 0.0f, oy = 0.0f;
+    for (int s0 = 0; s0 < S; s0 += 16) {
+        float2 v[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            v[i] = s0 + i < S ? *(const float2*)(pacc + (int64_t)(s0 + i) * hd + 2 * l) : make_float2(0.0f, 0.0f);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float wi = s0 + i < S ? sW[s0 + i] : 0.0f;
+            ox += v[i].x * wi;
+            oy += v[i].y * wi;
+        }
+    }
+    *(uint32_t*)(out + (int64_t)h * hd + 2 * l) =
+        (uint32_t)f32_to_f16_bits(ox * inv) | ((uint32_t)f32_to_f16_bits(oy * inv) << 16);
+}
+
 hipError_t attn_launch(const AttnArgs& a, bool kv_int8, hipStream_t st) {
     if (a.tokens < 1 || a.tq < 1 || (a.tokens > 1 && a.n_splits != 1) || (a.n_splits > 1 && a.tq != 1) ||
         (a.n_heads / a.n_kv) * a.tq > AT_MAXG)
@@ -496,8 +547,14 @@ hipError_t attn_launch(const AttnArgs& a, bool kv_int8, hipStream_t st) {
 #undef ATTN_CASE
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.n_splits == 1) return e;
-    hipLaunchKernelGGL(attn_reduce_kernel, dim3(a.n_heads), dim3(AT_RED_THREADS), 0, st, a.out, (const float*)a.part,
-                       a.n_heads, a.head_dim, a.n_splits);
+    // one wave per head up to 32 splits (ctx 512: 10.4 -> 9.2 us for partial +
+    // reduce), 8 waves per head beyond (128 splits: 13.0 us against 16.1)
+    if (a.n_splits <= 32)
+        hipLaunchKernelGGL(attn_reduce_wave_kernel, dim3(a.n_heads), dim3(64), 0, st, a.out, (const float*)a.part,
+                           a.n_heads, a.head_dim, a.n_splits);
+    else
+        hipLaunchKernelGGL(attn_reduce_kernel, dim3(a.n_heads), dim3(AT_RED_THREADS), 0, st, a.out,
+                           (const float*)a.part, a.n_heads, a.head_dim, a.n_splits);
     return hipGetLastError();
 }
 
