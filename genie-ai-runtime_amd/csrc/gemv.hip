@@ -371,11 +371,11 @@ __device__ __forceinline__ float block_dot(const Raw& r, int b, int q, const Q4C
 // residual rows are loaded before any weight bytes, behind a barrier, so
 // that they do not queue behind the CU's weight traffic.
 
-#ifndef JLLM_GEMV_ST_THREADS
-#define JLLM_GEMV_ST_THREADS 256
-#endif
-constexpr int ST_T = JLLM_GEMV_ST_THREADS;
-constexpr int ST_W = ST_T / 64;        // waves per workgroup
+// threads per workgroup: 256, or 512 for a launch under 12 MB (one
+// workgroup of 8 waves per CU stages the activation once per CU: QKV triple
+// 6.05 -> 5.7 us, with RMSNorm 6.85 -> 6.5 us)
+constexpr int ST_T = 256;
+constexpr int ST_T_SMALL = 512;
 
 // lane ^ 1 and lane ^ 2 through DPP quad_perm (no LDS round trip)
 __device__ __forceinline__ int dpp_x1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
@@ -618,16 +618,16 @@ __device__ __forceinline__ void wg_rows(const StreamArgs& a, int wg, int& g0, in
 }
 
 // The workgroup's rows [g0, g1) as one sequence of blocks (OUT_SWIGLU: the
-// gate rows' blocks, then the up rows'), cut into ST_W equal contiguous
+// gate rows' blocks, then the up rows'), cut into T/64 equal contiguous
 // ranges, one per wave; the wave's range as up to three pieces, one per
 // segment it touches.  Slots are indexed by the block's place in the
 // workgroup sequence.
-template <int TYPE, int L, int OUT>
+template <int TYPE, int L, int OUT, int T>
 __device__ __forceinline__ int make_pieces(const StreamArgs& a, int g0, int g1, int wv, Piece (&pc)[3]) {
     constexpr int NB = WGeom<TYPE, L>::NBLK;
     const int nb = a.nb, nrow = g1 - g0;
     const int seq = nrow * nb * (OUT == OUT_SWIGLU ? 2 : 1);
-    const int j0 = (int)((int64_t)seq * wv / ST_W), j1 = (int)((int64_t)seq * (wv + 1) / ST_W);
+    const int j0 = (int)((int64_t)seq * wv / (T / 64)), j1 = (int)((int64_t)seq * (wv + 1) / (T / 64));
     int nr = 0;
 #pragma unroll
     for (int s = 0; s < 3; s++) {
@@ -697,7 +697,7 @@ __device__ uint64_t g_gemv_rtrace[4096 * 48];
 // One wave's rows: rounds stream through two register stages and the wave's
 // own LDS buffer; the slots of its rows are added up and stored at the end.
 // Both weight types run the same two workgroup barriers (activation staging).
-template <bool MMVQ, int OUT, int TYPE, int L, int NX, int PRE>
+template <bool MMVQ, int OUT, int TYPE, int L, int NX, int PRE, int T>
 __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int g0, int g1, int lane, int wv,
                                           uint16_t* res_lds) {
     const int nb = a.nb, K = a.K;
@@ -709,7 +709,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
     tr[7] = ((uint64_t)__builtin_amdgcn_s_getreg((31 << 11) | 20) << 32) | (uint64_t)__builtin_amdgcn_s_getreg((31 << 11) | 4);
 #endif
     Piece pc[3];
-    const int nr = make_pieces<TYPE, L, OUT>(a, g0, g1, wv, pc);
+    const int nr = make_pieces<TYPE, L, OUT, T>(a, g0, g1, wv, pc);
     u32x4 R0[L], R1[L];
     {
         // activation (and residual) loads first, on every wave, then a barrier,
@@ -719,7 +719,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         u32x4 nwv[PRE == PRE_RMS ? 2 * NX : 1];     // RMSNorm weights of the lane's chunks, loaded with x
 #pragma unroll
         for (int i = 0; i < NX; i++) {
-            const int c = (int)threadIdx.x + ST_T * i;
+            const int c = (int)threadIdx.x + T * i;
             xv[i] = *(const u32x4*)(a.x + 8 * (c < nch ? c : 0));
             if (PRE == PRE_RMS) {
                 const int cc = c < nch ? c : 0;
@@ -733,7 +733,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
             }
         }
         uint16_t rv = 0;
-        const int nres = OUT == OUT_ADD ? g1 - g0 : 0;   // the workgroup's rows, nres <= ST_T
+        const int nres = OUT == OUT_ADD ? g1 - g0 : 0;   // the workgroup's rows, nres <= T
         if (OUT == OUT_ADD && (int)threadIdx.x < nres) rv = a.seg[0].res[g0 + threadIdx.x];
         __builtin_amdgcn_s_barrier();
 #ifdef JLLM_GEMV_XFIRST
@@ -745,13 +745,13 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         __builtin_amdgcn_sched_barrier(0);
         GT_MARK(1);
         if (PRE == PRE_RMS) {
-            // sum of squares of the whole activation (K <= NX * ST_T * 8 here):
+            // sum of squares of the whole activation (K <= NX * T * 8 here):
             // lanes, then waves through LDS (the first words of wave 0's round
             // buffer, not written before the staging barrier below)
             float ss = 0.0f;
 #pragma unroll
             for (int i = 0; i < NX; i++) {
-                const int c = (int)threadIdx.x + ST_T * i;
+                const int c = (int)threadIdx.x + T * i;
                 if (c < nch) ss += sumsq8(xv[i]);
             }
 #pragma unroll
@@ -763,33 +763,33 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
             float tot = 0.0f;
 #pragma unroll
-            for (int w = 0; w < ST_W; w++) tot += red[w];
+            for (int w = 0; w < (T / 64); w++) tot += red[w];
             const float rrms = 1.0f / sqrtf(tot / (float)K + a.pre.eps);
 #pragma unroll
             for (int i = 0; i < NX; i++) {
-                const int c = (int)threadIdx.x + ST_T * i;
-                if (ST_T * i + 64 * wv < nch && c < nch) xv[i] = rms8(xv[i], rrms, a.pre.nw_fp32, nwv[2 * i], nwv[2 * i + 1]);
+                const int c = (int)threadIdx.x + T * i;
+                if (T * i + 64 * wv < nch && c < nch) xv[i] = rms8(xv[i], rrms, a.pre.nw_fp32, nwv[2 * i], nwv[2 * i + 1]);
             }
         }
         // (a wave whose chunks all lie beyond K skips the staging arithmetic: uniform branch)
 #pragma unroll
         for (int i = 0; i < NX; i++) {
-            const int c = (int)threadIdx.x + ST_T * i;
-            if (ST_T * i + 64 * wv >= nch) continue;
+            const int c = (int)threadIdx.x + T * i;
+            if (T * i + 64 * wv >= nch) continue;
             if (MMVQ) xstage_q8_1(xv[i], c, K, lds);
             else      xstage_f16(xv[i], c, K, lds);
         }
         // K beyond NX chunks per lane (K > 10240): the rest after the weights
-        for (int c0 = NX * ST_T; c0 < nch; c0 += NX * ST_T) {
+        for (int c0 = NX * T; c0 < nch; c0 += NX * T) {
 #pragma unroll
             for (int i = 0; i < NX; i++) {
-                const int c = c0 + (int)threadIdx.x + ST_T * i;
+                const int c = c0 + (int)threadIdx.x + T * i;
                 xv[i] = *(const u32x4*)(a.x + 8 * (c < nch ? c : 0));
             }
 #pragma unroll
             for (int i = 0; i < NX; i++) {
-                const int c = c0 + (int)threadIdx.x + ST_T * i;
-                if (c0 + ST_T * i + 64 * wv >= nch) continue;
+                const int c = c0 + (int)threadIdx.x + T * i;
+                if (c0 + T * i + 64 * wv >= nch) continue;
                 if (MMVQ) xstage_q8_1(xv[i], c, K, lds);
                 else      xstage_f16(xv[i], c, K, lds);
             }
@@ -803,7 +803,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
     GT_MARK(2);
     const uint8_t* xlds = lds;
     uint8_t* buf = lds + a.xlds_bytes + wv * (64 * 16 * L);
-    float* slots = (float*)(lds + a.xlds_bytes + ST_W * (64 * 16 * L));    // the workgroup's block slots
+    float* slots = (float*)(lds + a.xlds_bytes + (T / 64) * (64 * 16 * L));    // the workgroup's block slots
     // Round r travels in register stage r mod 2.  Step k: compute round k
     // from the wave's LDS buffer, move round k+1 from its registers into the
     // buffer, and reuse those registers for round k+3 (round k+2 stays in
@@ -815,7 +815,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
     issue_round<L>(round_desc<TYPE, L>(a, pc, 2), R0, lane);
     auto step = [&](int k, u32x4 (&nxt)[L]) {
 #ifdef JLLM_GEMV_TRACE
-        const int64_t gw = (int64_t)blockIdx.x * ST_W + wv;
+        const int64_t gw = (int64_t)blockIdx.x * (T / 64) + wv;
         const bool rt = gw < 4096 && k < 16 && lane == 0;
         if (rt) g_gemv_rtrace[gw * 48 + k * 3] = __builtin_amdgcn_s_memrealtime();
 #endif
@@ -843,10 +843,10 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     // rows: 8 lanes per row add the row's slots (lane j the blocks b = j mod 8,
-    // in order), then a fixed butterfly; ST_T / 8 rows per pass
+    // in order), then a fixed butterfly; T / 8 rows per pass
     const int nrow = g1 - g0, j = lane & 7, rg = (int)threadIdx.x >> 3;
     if (OUT == OUT_SWIGLU) {
-        for (int t0 = 0; t0 < nrow; t0 += ST_T / 8) {
+        for (int t0 = 0; t0 < nrow; t0 += T / 8) {
             const int t = t0 + rg;
             float vg = 0.0f, vu = 0.0f;
             if (t < nrow) {
@@ -870,13 +870,13 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
             uint64_t tv = 0;
 #pragma unroll
             for (int i = 0; i < 8; i++) if (lane == i) tv = tr[i];
-            if (lane < 8) g_gemv_trace[((int64_t)blockIdx.x * ST_W + wv) * 8 + lane] = tv;
+            if (lane < 8) g_gemv_trace[((int64_t)blockIdx.x * (T / 64) + wv) * 8 + lane] = tv;
         }
 #endif
         return;
     }
     GT_MARK(5);
-    for (int t0 = 0; t0 < nrow; t0 += ST_T / 8) {
+    for (int t0 = 0; t0 < nrow; t0 += T / 8) {
         const int t = t0 + rg;
         float v = 0.0f;
         if (t < nrow) {
@@ -898,7 +898,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         uint64_t tv = 0;
 #pragma unroll
         for (int i = 0; i < 8; i++) if (lane == i) tv = tr[i];
-        if (lane < 8) g_gemv_trace[((int64_t)blockIdx.x * ST_W + wv) * 8 + lane] = tv;
+        if (lane < 8) g_gemv_trace[((int64_t)blockIdx.x * (T / 64) + wv) * 8 + lane] = tv;
     }
 #endif
 }
@@ -909,8 +909,8 @@ template <class T>
 __device__ __forceinline__ void pin_sgpr(const T& v) { asm volatile("" :: "s"(v)); }
 
 // TA: the type of the first row class (Q4_K or Q5_K); the second is Q6_K.
-template <bool MMVQ, int OUT, int L, int NX, int PRE, int TA>
-__global__ __launch_bounds__(ST_T) __attribute__((amdgpu_waves_per_eu(4)))
+template <bool MMVQ, int OUT, int L, int NX, int PRE, int TA, int T>
+__global__ __launch_bounds__(T) __attribute__((amdgpu_waves_per_eu(4)))
 void gemv_stream_kernel(StreamArgs a_in) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     StreamArgs a = a_in;
@@ -927,46 +927,49 @@ void gemv_stream_kernel(StreamArgs a_in) {
     int g0, g1;
     bool q4;
     wg_rows(a, blockIdx.x, g0, g1, q4);
-    uint16_t* res_lds = (uint16_t*)(lds + a.xlds_bytes + ST_W * (64 * 16 * L) + 4 * a.slots_per_wg);
+    uint16_t* res_lds = (uint16_t*)(lds + a.xlds_bytes + (T / 64) * (64 * 16 * L) + 4 * a.slots_per_wg);
     // (both bodies hold the same workgroup barriers; a workgroup serves one class)
     if constexpr (OUT == OUT_SWIGLU) {
-        wave_body<MMVQ, OUT, TA, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds);
+        wave_body<MMVQ, OUT, TA, L, NX, PRE, T>(a, lds, g0, g1, lane, wv, res_lds);
     } else {
-        if (q4) wave_body<MMVQ, OUT, TA, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds);
-        else    wave_body<MMVQ, OUT, TYPE_Q6_K, L, NX, PRE>(a, lds, g0, g1, lane, wv, res_lds);
+        if (q4) wave_body<MMVQ, OUT, TA, L, NX, PRE, T>(a, lds, g0, g1, lane, wv, res_lds);
+        else    wave_body<MMVQ, OUT, TYPE_Q6_K, L, NX, PRE, T>(a, lds, g0, g1, lane, wv, res_lds);
     }
 }
 
-template <bool MMVQ, int OUT, int L, int NX, int PRE, int TA>
+template <bool MMVQ, int OUT, int L, int NX, int PRE, int TA, int T>
 static hipError_t launch_s(const StreamArgs& a, int grid, size_t lds, hipStream_t st) {
-    static const hipError_t attr = hipFuncSetAttribute((const void*)gemv_stream_kernel<MMVQ, OUT, L, NX, PRE, TA>,
+    static const hipError_t attr = hipFuncSetAttribute((const void*)gemv_stream_kernel<MMVQ, OUT, L, NX, PRE, TA, T>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((gemv_stream_kernel<MMVQ, OUT, L, NX, PRE, TA>), dim3(grid), dim3(ST_T), lds, st, a);
+    hipLaunchKernelGGL((gemv_stream_kernel<MMVQ, OUT, L, NX, PRE, TA, T>), dim3(grid), dim3(T), lds, st, a);
     return hipGetLastError();
 }
 
-template <bool MMVQ, int OUT, int L, int PRE, int TA>
+template <bool MMVQ, int OUT, int L, int PRE, int TA, int T>
 static hipError_t launch_nx_t(const StreamArgs& a, int grid, size_t lds, hipStream_t st) {
     const int nch = a.K / 8;
-    if (nch <= ST_T) return launch_s<MMVQ, OUT, L, 1, PRE, TA>(a, grid, lds, st);
+    if (nch <= T) return launch_s<MMVQ, OUT, L, 1, PRE, TA, T>(a, grid, lds, st);
     if constexpr (PRE == PRE_RMS) {
-        return launch_s<MMVQ, OUT, L, 2, PRE, TA>(a, grid, lds, st);
+        return launch_s<MMVQ, OUT, L, 2, PRE, TA, T>(a, grid, lds, st);
     } else {
-        if (nch <= 2 * ST_T) return launch_s<MMVQ, OUT, L, 2, PRE, TA>(a, grid, lds, st);
-        return launch_s<MMVQ, OUT, L, 5, PRE, TA>(a, grid, lds, st);
+        if (nch <= 2 * T) return launch_s<MMVQ, OUT, L, 2, PRE, TA, T>(a, grid, lds, st);
+        return launch_s<MMVQ, OUT, L, 5, PRE, TA, T>(a, grid, lds, st);
     }
 }
 
 // Q5_K rows exist only in float mode
 template <bool MMVQ, int OUT, int L, int PRE = PRE_NONE>
-static hipError_t launch_nx(const StreamArgs& a, int grid, size_t lds, hipStream_t st, bool q5) {
+static hipError_t launch_nx(const StreamArgs& a, int grid, size_t lds, hipStream_t st, bool q5, int threads) {
     if constexpr (MMVQ) {
         if (q5) return hipErrorInvalidValue;
-        return launch_nx_t<true, OUT, L, PRE, TYPE_Q4_K>(a, grid, lds, st);
+        return threads == ST_T_SMALL ? launch_nx_t<true, OUT, L, PRE, TYPE_Q4_K, ST_T_SMALL>(a, grid, lds, st)
+                                     : launch_nx_t<true, OUT, L, PRE, TYPE_Q4_K, ST_T>(a, grid, lds, st);
     } else {
-        if (q5) return launch_nx_t<false, OUT, L, PRE, TYPE_Q5_K>(a, grid, lds, st);
-        return launch_nx_t<false, OUT, L, PRE, TYPE_Q4_K>(a, grid, lds, st);
+        if (q5) return threads == ST_T_SMALL ? launch_nx_t<false, OUT, L, PRE, TYPE_Q5_K, ST_T_SMALL>(a, grid, lds, st)
+                                             : launch_nx_t<false, OUT, L, PRE, TYPE_Q5_K, ST_T>(a, grid, lds, st);
+        return threads == ST_T_SMALL ? launch_nx_t<false, OUT, L, PRE, TYPE_Q4_K, ST_T_SMALL>(a, grid, lds, st)
+                                     : launch_nx_t<false, OUT, L, PRE, TYPE_Q4_K, ST_T>(a, grid, lds, st);
     }
 }
 
@@ -1036,7 +1039,9 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     a.row_split = (int)rows4;
     const int64_t bytes4 = rows4 * a.nb * (has5 ? Q5K_BYTES : Q4K_BYTES), bytes6 = rows6 * a.nb * Q6K_BYTES;
     a.xlds_bytes = (int)((gemv_lds_bytes(mmvq, a.K) + 15) & ~(size_t)15);
-    const size_t wbuf = ST_W * (size_t)(64 * 16 * ST_L);
+    const int64_t wbytes = bytes4 + bytes6;
+    const int threads = wbytes < ((int64_t)12 << 20) ? ST_T_SMALL : ST_T;
+    const size_t wbuf = (size_t)(threads / 64) * (size_t)(64 * 16 * ST_L);
     // JLLM_GEMV_WG_PER_CU workgroups per CU when LDS allows, split between
     // the classes by bytes; a workgroup takes a contiguous row range
     int64_t grid = 0;
@@ -1057,8 +1062,7 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
         return (size_t)a.xlds_bytes + wbuf + (size_t)4 * slot_rows * max_rows * a.nb + res;
     };
     // (the residual rows of a workgroup are staged one per lane)
-    auto fits = [&](int per_cu) { return (size_t)per_cu * lds_of() <= LDS_CU && !(out_kind == OUT_ADD && max_rows > ST_T); };
-    const int64_t wbytes = bytes4 + bytes6;
+    auto fits = [&](int per_cu) { return (size_t)per_cu * lds_of() <= LDS_CU && !(out_kind == OUT_ADD && max_rows > threads); };
     const int per_cu0 = wbytes > ((int64_t)64 << 20) ? JLLM_GEMV_WG_PER_CU_BIG
                       : (wbytes < ((int64_t)12 << 20) ? JLLM_GEMV_WG_PER_CU_SMALL : JLLM_GEMV_WG_PER_CU);
     for (int per_cu = per_cu0; per_cu >= 1 && grid == 0; per_cu--) {
@@ -1081,27 +1085,27 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     const int g = (int)grid;
     a.pre = in.pre;
     if (in.pre.kind == PRE_RMS) {      // the sum of squares needs the whole x in the first staging pass
-        if (a.K > 2 * ST_T * 8) return hipErrorInvalidValue;
-        if (mmvq && out_kind == OUT_HALF) return launch_nx<true, OUT_HALF, ST_L, PRE_RMS>(a, g, lds, st, has5);
-        if (mmvq && out_kind == OUT_F32)  return launch_nx<true, OUT_F32, ST_L, PRE_RMS>(a, g, lds, st, has5);
-        if (!mmvq && out_kind == OUT_F32) return launch_nx<false, OUT_F32, ST_L, PRE_RMS>(a, g, lds, st, has5);
-        if (!mmvq && out_kind == OUT_HALF) return launch_nx<false, OUT_HALF, ST_L, PRE_RMS>(a, g, lds, st, has5);
-        if (mmvq && sw) return launch_nx<true, OUT_SWIGLU, ST_L, PRE_RMS>(a, g, lds, st, has5);
-        if (!mmvq && sw) return launch_nx<false, OUT_SWIGLU, ST_L, PRE_RMS>(a, g, lds, st, has5);
+        if (a.K > 2 * threads * 8) return hipErrorInvalidValue;
+        if (mmvq && out_kind == OUT_HALF) return launch_nx<true, OUT_HALF, ST_L, PRE_RMS>(a, g, lds, st, has5, threads);
+        if (mmvq && out_kind == OUT_F32)  return launch_nx<true, OUT_F32, ST_L, PRE_RMS>(a, g, lds, st, has5, threads);
+        if (!mmvq && out_kind == OUT_F32) return launch_nx<false, OUT_F32, ST_L, PRE_RMS>(a, g, lds, st, has5, threads);
+        if (!mmvq && out_kind == OUT_HALF) return launch_nx<false, OUT_HALF, ST_L, PRE_RMS>(a, g, lds, st, has5, threads);
+        if (mmvq && sw) return launch_nx<true, OUT_SWIGLU, ST_L, PRE_RMS>(a, g, lds, st, has5, threads);
+        if (!mmvq && sw) return launch_nx<false, OUT_SWIGLU, ST_L, PRE_RMS>(a, g, lds, st, has5, threads);
         return hipErrorInvalidValue;
     }
     if (sw) {
-        if (mmvq) return launch_nx<true, OUT_SWIGLU, ST_L>(a, g, lds, st, has5);
-        return launch_nx<false, OUT_SWIGLU, ST_L>(a, g, lds, st, has5);
+        if (mmvq) return launch_nx<true, OUT_SWIGLU, ST_L>(a, g, lds, st, has5, threads);
+        return launch_nx<false, OUT_SWIGLU, ST_L>(a, g, lds, st, has5, threads);
     }
     if (mmvq) {
-        if (out_kind == OUT_HALF) return launch_nx<true, OUT_HALF, ST_L>(a, g, lds, st, has5);
-        if (out_kind == OUT_F32)  return launch_nx<true, OUT_F32, ST_L>(a, g, lds, st, has5);
-        return launch_nx<true, OUT_ADD, ST_L>(a, g, lds, st, has5);
+        if (out_kind == OUT_HALF) return launch_nx<true, OUT_HALF, ST_L>(a, g, lds, st, has5, threads);
+        if (out_kind == OUT_F32)  return launch_nx<true, OUT_F32, ST_L>(a, g, lds, st, has5, threads);
+        return launch_nx<true, OUT_ADD, ST_L>(a, g, lds, st, has5, threads);
     }
-    if (out_kind == OUT_HALF) return launch_nx<false, OUT_HALF, ST_L>(a, g, lds, st, has5);
-    if (out_kind == OUT_F32)  return launch_nx<false, OUT_F32, ST_L>(a, g, lds, st, has5);
-    return launch_nx<false, OUT_ADD, ST_L>(a, g, lds, st, has5);
+    if (out_kind == OUT_HALF) return launch_nx<false, OUT_HALF, ST_L>(a, g, lds, st, has5, threads);
+    if (out_kind == OUT_F32)  return launch_nx<false, OUT_F32, ST_L>(a, g, lds, st, has5, threads);
+    return launch_nx<false, OUT_ADD, ST_L>(a, g, lds, st, has5, threads);
 }
 
 #ifdef JLLM_GEMV_TRACE
