@@ -1040,7 +1040,12 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     const int64_t bytes4 = rows4 * a.nb * (has5 ? Q5K_BYTES : Q4K_BYTES), bytes6 = rows6 * a.nb * Q6K_BYTES;
     a.xlds_bytes = (int)((gemv_lds_bytes(mmvq, a.K) + 15) & ~(size_t)15);
     const int64_t wbytes = bytes4 + bytes6;
-    const int threads = wbytes < ((int64_t)12 << 20) ? ST_T_SMALL : ST_T;
+    // 512 threads (the same waves per CU in half the workgroups) where it
+    // measured faster: under 12 MB, plain products of 12-64 MB (gate/up pair
+    // 9.3-9.6 -> 9.0-9.2 us; not the residual form -- down 8.4 -> 8.8 -- nor
+    // the RMSNorm / SwiGLU fusions) and above 64 MB (lm_head 62 -> 61 us)
+    const bool mid_plain = in.pre.kind != PRE_RMS && !sw && out_kind != OUT_ADD;
+    const int threads = (wbytes < ((int64_t)12 << 20) || wbytes > ((int64_t)64 << 20) || mid_plain) ? ST_T_SMALL : ST_T;
     const size_t wbuf = (size_t)(threads / 64) * (size_t)(64 * 16 * ST_L);
     // JLLM_GEMV_WG_PER_CU workgroups per CU when LDS allows, split between
     // the classes by bytes; a workgroup takes a contiguous row range
@@ -1063,8 +1068,9 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     };
     // (the residual rows of a workgroup are staged one per lane)
     auto fits = [&](int per_cu) { return (size_t)per_cu * lds_of() <= LDS_CU && !(out_kind == OUT_ADD && max_rows > threads); };
-    const int per_cu0 = wbytes > ((int64_t)64 << 20) ? JLLM_GEMV_WG_PER_CU_BIG
+    int per_cu0 = wbytes > ((int64_t)64 << 20) ? JLLM_GEMV_WG_PER_CU_BIG
                       : (wbytes < ((int64_t)12 << 20) ? JLLM_GEMV_WG_PER_CU_SMALL : JLLM_GEMV_WG_PER_CU);
+    if (threads == ST_T_SMALL && wbytes >= ((int64_t)12 << 20)) per_cu0 /= 2;     // same waves per CU
     for (int per_cu = per_cu0; per_cu >= 1 && grid == 0; per_cu--) {
         split((int64_t)device_cus() * per_cu);
         if (fits(per_cu)) grid = (int64_t)device_cus() * per_cu;
