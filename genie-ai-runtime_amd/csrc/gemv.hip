@@ -736,9 +736,6 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         const int nres = OUT == OUT_ADD ? g1 - g0 : 0;   // the workgroup's rows, nres <= T
         if (OUT == OUT_ADD && (int)threadIdx.x < nres) rv = a.seg[0].res[g0 + threadIdx.x];
         __builtin_amdgcn_s_barrier();
-#ifdef JLLM_GEMV_XFIRST
-        __builtin_amdgcn_s_waitcnt(0x0F70);     // vmcnt(0): this wave's activation loads are in
-#endif
         __builtin_amdgcn_sched_barrier(0);
         issue_round<L>(round_desc<TYPE, L>(a, pc, 0), R0, lane);
         issue_round<L>(round_desc<TYPE, L>(a, pc, 1), R1, lane);
