@@ -15,6 +15,10 @@ struct AttnArgs {
     float* part;              // partials: m [H*S] | l [H*S] | acc [H*S*hd]
     int* counters;            // [n_kv] split-completion counters, zero between calls
     int n_heads, n_kv, head_dim, cache_head_dim, seq, window, n_splits;
+    // decode only (tokens == 1): when not null, the key count is read on the
+    // device as *pos_dev + 1 and `seq` is ignored (a captured graph replays
+    // for every position; the split count stays the host's n_splits)
+    const int* pos_dev = nullptr;
     float scale;
     // query tokens (grid z): token t attends to keys [0, seq + t) and reads
     // q / writes out at t * n_heads * head_dim.  tokens > 1 needs n_splits 1.

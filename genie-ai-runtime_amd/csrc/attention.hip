@@ -132,18 +132,19 @@ void attn_partial_kernel(AttnArgs a) {
     const size_t wave_lds = attn_wave_lds_bytes(a.n_heads, a.n_kv, a.head_dim, a.tq);
     uint8_t* smem = smem_wg + (size_t)wv * wave_lds;
     const int kvh = blockIdx.x, split = blockIdx.y, tok0 = MT ? blockIdx.z * a.tq : blockIdx.z;
+    const int aseq = (!MT && a.pos_dev) ? __builtin_amdgcn_readfirstlane(*a.pos_dev) + 1 : a.seq;
     const int G = a.n_heads / a.n_kv;
     const int ntok = MT ? min(a.tq, a.tokens - tok0) : 1;       // tokens of this wave
     const int GC = ntok * G;                                    // live columns
     const int l = (int)threadIdx.x & 63, li = l & 31, lg = l >> 5;
     // column li: its token, causal bound and window start
     const int ctok = MT ? tok0 + (li < GC ? li / G : 0) : tok0;
-    const int seq_c = a.seq + ctok;
+    const int seq_c = aseq + ctok;
     const int lo_c = a.window > 0 ? max(0, seq_c - a.window) : 0;
     // the wave's key range covers every column's
-    const int seq = a.seq + tok0 + ntok - 1;
+    const int seq = aseq + tok0 + ntok - 1;
     const int kv_dim = a.n_kv * a.cache_head_dim, hoff = kvh * a.cache_head_dim;
-    const int lo_pos = a.window > 0 ? max(0, a.seq + tok0 - a.window) : 0;
+    const int lo_pos = a.window > 0 ? max(0, aseq + tok0 - a.window) : 0;
     const int span = seq - lo_pos;
     const int S = a.n_splits;
     const int per = (span + S - 1) / S;

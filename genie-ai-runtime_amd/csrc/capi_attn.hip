@@ -30,8 +30,8 @@ int attn_check(const void* out, const void* q, const void* k, const void* v, int
 
 int attn_run(uint16_t* out, const uint16_t* q, const void* k, const void* v, int n_heads, int n_kv, int hd, int chd,
              int seq, float scale, int kv_int8, const float* ks, const float* vs, int window, int n_splits,
-             void* stream) {
-    int st = attn_check(out, q, k, v, n_heads, n_kv, hd, chd, seq, kv_int8, window);
+             void* stream, const int32_t* pos_dev = nullptr) {
+    int st = attn_check(out, q, k, v, n_heads, n_kv, hd, chd, pos_dev ? 1 : seq, kv_int8, window);
     if (st) return st;
     if (n_splits < 1) n_splits = 1;
     if (n_splits > ATTN_MAX_SPLITS) n_splits = ATTN_MAX_SPLITS;
@@ -43,6 +43,7 @@ int attn_run(uint16_t* out, const uint16_t* q, const void* k, const void* v, int
     a.part = (float*)(scratch + ATTN_COUNTER_BYTES);
     a.n_heads = n_heads; a.n_kv = n_kv; a.head_dim = hd; a.cache_head_dim = chd;
     a.seq = seq; a.window = window; a.n_splits = n_splits; a.scale = scale; a.tokens = 1; a.tq = 1; a.wsplit = 1;
+    a.pos_dev = pos_dev;
     return launch_status(attn_launch(a, kv_int8 != 0, (hipStream_t)stream), "attention");
 }
 }  // namespace
@@ -71,6 +72,15 @@ int jllm_hip_flash_attention_decode_splits(uint16_t* out, const uint16_t* q, con
                                            const float* v_scales, int window, int n_splits, void* stream) {
     return attn_run(out, q, k, v, n_heads, n_kv_heads, head_dim, cache_head_dim, seq_len, scale, kv_int8,
                     k_scales, v_scales, window, n_splits, stream);
+}
+
+int jllm_hip_flash_attention_decode_dyn(uint16_t* out, const uint16_t* q, const void* k, const void* v,
+                                        int n_heads, int n_kv_heads, int head_dim, int cache_head_dim,
+                                        const int32_t* d_pos, float scale, int kv_int8, const float* k_scales,
+                                        const float* v_scales, int window, int n_splits, void* stream) {
+    if (!d_pos) return JLLM_ERR_INVALID;
+    return attn_run(out, q, k, v, n_heads, n_kv_heads, head_dim, cache_head_dim, 0, scale, kv_int8, k_scales,
+                    v_scales, window, n_splits, stream, d_pos);
 }
 
 int jllm_hip_flash_attention_prefill_batched(uint16_t* out, const uint16_t* q, const void* k, const void* v,

@@ -56,4 +56,8 @@ int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uin
 int gemm_batched_res(const char* tag, uint16_t* y, const void* W, int type, const uint16_t* x, const uint16_t* up,
                      uint16_t* act_tmp, const uint16_t* res, int M, int N, int K, void* stream);
 
+// The decoder's supported shapes (jllm_hip_decoder_create, jllm_hip_gguf_config):
+// false, with the reason on stderr, for a configuration a later step would reject.
+bool decoder_config_ok(const jllm_hip_decoder_config& c);
+
 }  // namespace jllm_hip

@@ -8,6 +8,12 @@
 
 using namespace jllm_hip;
 
+// The engine's registry lookup (defined in its src/engine/model.cpp when the
+// engine is linked in; a null address otherwise).
+namespace jllm {
+const void* resolve_mapped_weight_device_ptr(const void* host_ptr) __attribute__((weak));
+}
+
 namespace {
 struct MappedRegion { const char* host; const char* dev; int64_t bytes; };
 std::mutex g_reg_mu;
@@ -56,9 +62,13 @@ void jllm_hip_clear_mapped_weight_region(const void* host_base) {
 
 const void* jllm_hip_resolve_mapped_weight_device_ptr(const void* host_ptr) {
     const char* p = (const char*)host_ptr;
-    std::lock_guard<std::mutex> lk(g_reg_mu);
-    for (const auto& r : g_regions)
-        if (p >= r.host && p < r.host + r.bytes) return r.dev + (p - r.host);
+    {
+        std::lock_guard<std::mutex> lk(g_reg_mu);
+        for (const auto& r : g_regions)
+            if (p >= r.host && p < r.host + r.bytes) return r.dev + (p - r.host);
+    }
+    // then the engine's own registry (src/engine/model.cpp:39-66) when it is linked in
+    if (&jllm::resolve_mapped_weight_device_ptr) return jllm::resolve_mapped_weight_device_ptr(host_ptr);
     return nullptr;
 }
 

@@ -83,7 +83,8 @@ int jllm_hip_qk_norm_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v, 
         return JLLM_ERR_INVALID;
     }
     if (N == 0) return JLLM_OK;
-    if (!q || !k || !v || !k_dst || !v_dst || (q_norm && !k_norm)) return JLLM_ERR_INVALID;
+    // the engine norms q and k only when the layer has both weights (decode.cu:1443)
+    if (!q || !k || !v || !k_dst || !v_dst || (q_norm == nullptr) != (k_norm == nullptr)) return JLLM_ERR_INVALID;
     QKPostArgs a;
     a.q = q; a.k = k; a.v = v; a.q_norm = q_norm; a.k_norm = k_norm;
     a.k_dst = k_dst; a.v_dst = v_dst; a.k_scales = k_scales; a.v_scales = v_scales; a.kv_stride = kv_stride;
@@ -92,6 +93,69 @@ int jllm_hip_qk_norm_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v, 
     a.norm_fp32 = norm_fp32 != 0; a.neox = neox != 0; a.kv_int8 = kv_int8 != 0;
     rope_frequencies(a.fr, head_dim, theta_base);
     return launch_status(qk_post_launch(a, (hipStream_t)stream), "qk_post");
+}
+
+int jllm_hip_rope_inplace_dyn(uint16_t* q, uint16_t* k, int n_heads, int n_kv_heads, int head_dim,
+                              const int32_t* d_pos, float theta_base, int neox, void* stream) {
+    if (n_heads < 0 || n_kv_heads < 0 || !d_pos) return JLLM_ERR_INVALID;
+    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > 2 * ROPE_MAX_HALF) {
+        fprintf(stderr, "[rope] head_dim=%d: need an even head_dim <= %d\n", head_dim, 2 * ROPE_MAX_HALF);
+        return JLLM_ERR_INVALID;
+    }
+    if (!k) n_kv_heads = 0;
+    if (n_heads + n_kv_heads == 0) return JLLM_OK;
+    if (n_heads && !q) return JLLM_ERR_INVALID;
+    RopeFreq fr;
+    rope_frequencies(fr, head_dim, theta_base);
+    return launch_status(rope_launch(q, k, n_heads, n_kv_heads, head_dim, 0, 1, n_heads * head_dim,
+                                     n_kv_heads * head_dim, fr, neox != 0, (hipStream_t)stream, d_pos), "rope");
+}
+
+namespace {
+// RoPE of q and k plus an fp16 copy of k and v into the cache (no norms):
+// the reference's rope_inplace_store_kv_fp16 family on the fused front
+int rope_store_fp16(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* k_dst, uint16_t* v_dst,
+                    int64_t cache_row_stride, int n_heads, int n_kv_heads, int head_dim, int cache_head_dim,
+                    int start_pos, const int32_t* d_pos, int N, int64_t q_in_stride, int64_t kv_in_stride,
+                    float theta_base, int neox, void* stream) {
+    if (n_heads <= 0 || n_kv_heads <= 0 || N < 0 || start_pos < 0 || cache_head_dim < head_dim ||
+        cache_row_stride < (int64_t)n_kv_heads * cache_head_dim || q_in_stride < (int64_t)n_heads * head_dim ||
+        kv_in_stride < (int64_t)n_kv_heads * head_dim)
+        return JLLM_ERR_INVALID;
+    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > 2 * ROPE_MAX_HALF) {
+        fprintf(stderr, "[rope] head_dim=%d: need an even head_dim <= %d\n", head_dim, 2 * ROPE_MAX_HALF);
+        return JLLM_ERR_INVALID;
+    }
+    if (N == 0) return JLLM_OK;
+    if (!q || !k || !v || !k_dst || !v_dst) return JLLM_ERR_INVALID;
+    QKPostArgs a;
+    a.q = q; a.k = k; a.v = v; a.q_norm = nullptr; a.k_norm = nullptr;
+    a.k_dst = k_dst; a.v_dst = v_dst; a.k_scales = nullptr; a.v_scales = nullptr; a.kv_stride = cache_row_stride;
+    a.n_heads = n_heads; a.n_kv = n_kv_heads; a.head_dim = head_dim; a.cache_head_dim = cache_head_dim;
+    a.start_pos = start_pos; a.N = N; a.eps = 0.0f;
+    a.norm_fp32 = 0; a.neox = neox != 0; a.kv_int8 = 0;
+    a.q_in_stride = q_in_stride; a.kv_in_stride = kv_in_stride; a.pos_dev = d_pos;
+    rope_frequencies(a.fr, head_dim, theta_base);
+    return launch_status(qk_post_launch(a, (hipStream_t)stream), "rope_store_kv");
+}
+}  // namespace
+
+int jllm_hip_rope_inplace_store_kv_fp16_dyn(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* k_cache_layer_base,
+                                            uint16_t* v_cache_layer_base, int n_heads, int n_kv_heads, int head_dim,
+                                            int cache_head_dim, const int32_t* d_pos, float theta_base, int neox,
+                                            void* stream) {
+    if (!d_pos) return JLLM_ERR_INVALID;
+    return rope_store_fp16(q, k, v, k_cache_layer_base, v_cache_layer_base, (int64_t)n_kv_heads * cache_head_dim,
+                           n_heads, n_kv_heads, head_dim, cache_head_dim, 0, d_pos, 1, (int64_t)n_heads * head_dim,
+                           (int64_t)n_kv_heads * head_dim, theta_base, neox, stream);
+}
+
+int jllm_hip_rope_inplace_store_kv_fp16_batched(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* k_cache_base,
+                                                uint16_t* v_cache_base, int kv_slot, int n_heads, int n_kv_heads,
+                                                int head_dim, int start_pos, int N, int q_stride, int kv_stride,
+                                                float theta_base, int neox, void* stream) {
+    return rope_store_fp16(q, k, v, k_cache_base, v_cache_base, kv_slot, n_heads, n_kv_heads, head_dim, head_dim,
+                           start_pos, nullptr, N, q_stride, kv_stride, theta_base, neox, stream);
 }
 
 int jllm_hip_dequant_embedding_rows(uint16_t* dst, const void* W, int ggml_type, const int32_t* tokens, int N,

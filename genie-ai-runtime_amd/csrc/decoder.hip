@@ -143,16 +143,41 @@ int head(jllm_hip_decoder* d, const uint16_t* xrow, int32_t* out, void* st) {
 
 }  // namespace
 
+namespace jllm_hip {
+bool decoder_config_ok(const jllm_hip_decoder_config& c) {
+    const char* why = nullptr;
+    if (c.n_layers <= 0 || c.hidden_dim <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 ||
+        c.intermediate_dim <= 0 || c.vocab_size <= 0 || c.max_seq <= 0)
+        why = "every dimension must be positive";
+    else if (c.hidden_dim % 256 || (c.n_heads * c.head_dim) % 256 || c.intermediate_dim % 256)
+        why = "hidden_dim, n_heads * head_dim and intermediate_dim must be multiples of 256 (K-quant rows)";
+    else if (c.hidden_dim > 4096)
+        why = "hidden_dim must be <= 4096 (the decode GEMVs normalise the whole activation in each workgroup)";
+    else if (c.intermediate_dim > 28672 || c.n_heads * c.head_dim > 28672)
+        why = "intermediate_dim and n_heads * head_dim must be <= 28672 (GEMV activation staging)";
+    else if (c.head_dim % 32 || c.head_dim > 128)
+        why = "head_dim must be a multiple of 32 and <= 128 (attention tiles)";
+    else if (c.n_heads % c.n_kv_heads || c.n_heads / c.n_kv_heads > 16)
+        why = "n_heads must be a multiple of n_kv_heads with at most 16 query heads per KV head";
+    if (why) {
+        fprintf(stderr, "[decoder] unsupported configuration (layers %d, hidden %d, heads %d/%d, head_dim %d, "
+                        "ffn %d, vocab %d, max_seq %d): %s\n", c.n_layers, c.hidden_dim, c.n_heads, c.n_kv_heads,
+                c.head_dim, c.intermediate_dim, c.vocab_size, c.max_seq, why);
+        return false;
+    }
+    return true;
+}
+}  // namespace jllm_hip
+
 extern "C" {
+
 
 jllm_hip_decoder* jllm_hip_decoder_create(const jllm_hip_decoder_config* cfg, const jllm_hip_model_weights* mw,
                                           const jllm_hip_layer_weights* layers, int max_batch) {
     if (!cfg || !mw || !layers) return nullptr;
     const jllm_hip_decoder_config& c = *cfg;
-    if (c.n_layers <= 0 || c.hidden_dim <= 0 || c.hidden_dim % 256 != 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 ||
-        c.head_dim <= 0 || (c.n_heads * c.head_dim) % 256 != 0 || c.intermediate_dim % 256 != 0 ||
-        c.intermediate_dim <= 0 || c.vocab_size <= 0 || c.max_seq <= 0 || max_batch <= 0) {
-        fprintf(stderr, "[decoder] invalid configuration\n");
+    if (!jllm_hip::decoder_config_ok(c) || max_batch <= 0) {
+        if (max_batch <= 0) fprintf(stderr, "[decoder] max_batch=%d must be positive\n", max_batch);
         return nullptr;
     }
     if (!valid_type(mw->embd_type) || !valid_type(mw->output_type) || !mw->tok_embd || !mw->output ||

@@ -867,7 +867,8 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
             uint64_t tv = 0;
 #pragma unroll
             for (int i = 0; i < 8; i++) if (lane == i) tv = tr[i];
-            if (lane < 8) g_gemv_trace[((int64_t)blockIdx.x * (T / 64) + wv) * 8 + lane] = tv;
+            const int64_t gwt = (int64_t)blockIdx.x * (T / 64) + wv;
+            if (lane < 8 && gwt < 8192) g_gemv_trace[gwt * 8 + lane] = tv;
         }
 #endif
         return;
@@ -895,7 +896,8 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         uint64_t tv = 0;
 #pragma unroll
         for (int i = 0; i < 8; i++) if (lane == i) tv = tr[i];
-        if (lane < 8) g_gemv_trace[((int64_t)blockIdx.x * (T / 64) + wv) * 8 + lane] = tv;
+        const int64_t gwt = (int64_t)blockIdx.x * (T / 64) + wv;
+        if (lane < 8 && gwt < 8192) g_gemv_trace[gwt * 8 + lane] = tv;
     }
 #endif
 }
@@ -1113,6 +1115,8 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
 
 #ifdef JLLM_GEMV_TRACE
 extern "C" int jllm_hip_gemv_trace_read(uint64_t* host, int n) {
+    if (n < 0) return -1;
+    if (n > 8192 * 8) n = 8192 * 8;
     return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_gemv_trace), (size_t)n * 8, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
 }
 extern "C" int jllm_hip_gemv_rtrace_read(uint64_t* host) {

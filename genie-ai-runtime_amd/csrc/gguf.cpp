@@ -27,6 +27,7 @@
 #include <string>
 #include <vector>
 #include "../../include/jllm_hip.h"
+#include "capi_common.h"
 
 namespace {
 
@@ -340,6 +341,7 @@ int jllm_hip_gguf_config(const jllm_hip_gguf* g, jllm_hip_decoder_config* cfg) {
         fprintf(stderr, "[gguf] metadata lacks the model shape\n");
         return JLLM_ERR_INVALID;
     }
+    if (!jllm_hip::decoder_config_ok(c)) return JLLM_ERR_UNSUPPORTED;
     *cfg = c;
     return JLLM_OK;
 }
@@ -352,33 +354,63 @@ jllm_hip_gguf_model* jllm_hip_gguf_model_load(const jllm_hip_gguf* g, const jllm
     // one device allocation for every tensor the decoder uses (256-byte aligned)
     struct Use { const Tensor* t; const void** dst; int* type; };
     std::vector<Use> uses;
-    auto want = [&](const std::string& name, const void** dst, int* type) {
+    bool shape_ok = true;
+    // a used tensor must have the shape the kernels will index with: a K-quant
+    // matrix [K, M] (dims[0] fastest) of type 12-14, a norm vector [n] of F32
+    // (type 0) when fp32 is 1, else F16 (type 1); anything else would make
+    // the kernels read past the tensor's slot in the arena
+    auto check = [&](const Tensor& t, int64_t d0, int64_t d1, int fp32) {
+        bool good;
+        if (d1 > 0) good = t.n_dims == 2 && t.dims[0] == d0 && t.dims[1] == d1 && t.type >= 12 && t.type <= 14;
+        else good = t.n_dims == 1 && t.dims[0] == d0 && t.type == (fp32 ? 0u : 1u);
+        if (!good) {
+            fprintf(stderr, "[gguf] tensor '%s': type %u, %u dims [%lld, %lld]; the configuration needs ",
+                    t.name.c_str(), t.type, t.n_dims, (long long)t.dims[0], (long long)(t.n_dims > 1 ? t.dims[1] : 0));
+            if (d1 > 0) fprintf(stderr, "a Q4_K/Q5_K/Q6_K matrix [%lld, %lld]\n", (long long)d0, (long long)d1);
+            else fprintf(stderr, "an %s vector [%lld]\n", fp32 ? "F32" : "F16", (long long)d0);
+            shape_ok = false;
+        }
+    };
+    auto want = [&](const std::string& name, const void** dst, int* type, int64_t d0, int64_t d1, int fp32) {
         const int64_t i = jllm_hip_gguf_find_tensor(g, name.c_str());
-        if (i >= 0) uses.push_back({&g->tensors[(size_t)i], dst, type});
+        if (i >= 0) {
+            check(g->tensors[(size_t)i], d0, d1, fp32);
+            uses.push_back({&g->tensors[(size_t)i], dst, type});
+        }
         return i >= 0;
     };
-    bool ok = want("token_embd.weight", &m->mw.tok_embd, &m->mw.embd_type);
-    ok &= want("output_norm.weight", &m->mw.output_norm, nullptr);
+    const int64_t H = cfg->hidden_dim, QD = (int64_t)cfg->n_heads * cfg->head_dim,
+                  KVD = (int64_t)cfg->n_kv_heads * cfg->head_dim, I = cfg->intermediate_dim, V = cfg->vocab_size;
+    bool ok = want("token_embd.weight", &m->mw.tok_embd, &m->mw.embd_type, H, V, 0);
+    ok &= want("output_norm.weight", &m->mw.output_norm, nullptr, H, 0, cfg->output_norm_fp32);
     // tied embeddings: without output.weight the output projection re-uses
     // token_embd (model.cpp:791-806)
-    const bool tied = !want("output.weight", &m->mw.output, &m->mw.output_type);
+    const bool tied = !want("output.weight", &m->mw.output, &m->mw.output_type, H, V, 0);
     for (int l = 0; l < cfg->n_layers; l++) {
         jllm_hip_layer_weights& w = m->lw[(size_t)l];
         const std::string p = "blk." + std::to_string(l) + ".";
-        ok &= want(p + "attn_q.weight", &w.wq, &w.type_wq);
-        ok &= want(p + "attn_k.weight", &w.wk, &w.type_wk);
-        ok &= want(p + "attn_v.weight", &w.wv, &w.type_wv);
-        ok &= want(p + "attn_output.weight", &w.wo, &w.type_wo);
-        ok &= want(p + "ffn_gate.weight", &w.w_gate, &w.type_w_gate);
-        ok &= want(p + "ffn_up.weight", &w.w_up, &w.type_w_up);
-        ok &= want(p + "ffn_down.weight", &w.w_down, &w.type_w_down);
-        ok &= want(p + "attn_norm.weight", &w.rms_attn, nullptr);
-        ok &= want(p + "ffn_norm.weight", &w.rms_ffn, nullptr);
-        want(p + "attn_q_norm.weight", &w.q_norm, nullptr);
-        want(p + "attn_k_norm.weight", &w.k_norm, nullptr);
+        ok &= want(p + "attn_q.weight", &w.wq, &w.type_wq, H, QD, 0);
+        ok &= want(p + "attn_k.weight", &w.wk, &w.type_wk, H, KVD, 0);
+        ok &= want(p + "attn_v.weight", &w.wv, &w.type_wv, H, KVD, 0);
+        ok &= want(p + "attn_output.weight", &w.wo, &w.type_wo, QD, H, 0);
+        ok &= want(p + "ffn_gate.weight", &w.w_gate, &w.type_w_gate, H, I, 0);
+        ok &= want(p + "ffn_up.weight", &w.w_up, &w.type_w_up, H, I, 0);
+        ok &= want(p + "ffn_down.weight", &w.w_down, &w.type_w_down, I, H, 0);
+        ok &= want(p + "attn_norm.weight", &w.rms_attn, nullptr, H, 0, cfg->norm_fp32);
+        ok &= want(p + "ffn_norm.weight", &w.rms_ffn, nullptr, H, 0, cfg->norm_fp32);
+        const bool qn = want(p + "attn_q_norm.weight", &w.q_norm, nullptr, cfg->head_dim, 0, cfg->qk_norm_fp32);
+        const bool kn = want(p + "attn_k_norm.weight", &w.k_norm, nullptr, cfg->head_dim, 0, cfg->qk_norm_fp32);
+        if (qn != kn) {
+            fprintf(stderr, "[gguf] layer %d has only one of attn_q_norm / attn_k_norm\n", l);
+            shape_ok = false;
+        }
     }
     if (!ok) {
         fprintf(stderr, "[gguf] the file lacks tensors of the Llama/Qwen3 decoder\n");
+        delete m;
+        return nullptr;
+    }
+    if (!shape_ok) {
         delete m;
         return nullptr;
     }

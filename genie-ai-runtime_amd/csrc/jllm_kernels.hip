@@ -35,14 +35,6 @@ inline uint16_t* H(half* p) { return reinterpret_cast<uint16_t*>(p); }
 
 namespace jllm {
 
-const void* resolve_mapped_weight_device_ptr(const void* host_ptr) {
-    return jllm_hip_resolve_mapped_weight_device_ptr(host_ptr);
-}
-void register_mapped_weight_region(const void* host_base, const void* device_base, int64_t bytes) {
-    (void)jllm_hip_register_mapped_weight_region(host_base, device_base, bytes);
-}
-void clear_mapped_weight_region(const void* host_base) { jllm_hip_clear_mapped_weight_region(host_base); }
-
 void gemv_q4(half* y, const void* W_q4, const half*, const half* x, int M, int K, int, hipStream_t stream) {
     gemv_quant(y, W_q4, 12, x, M, K, stream);
 }
@@ -103,6 +95,39 @@ void flash_attention_decode(half* output, const half* q, const void* k_cache, co
            "flash_attention_decode", output, (size_t)n_heads * head_dim * 2, stream);
 }
 
+void flash_attention_decode_dyn(half* output, const half* q, const void* k_cache, const void* v_cache, int n_heads,
+                                int n_kv_heads, int head_dim, int cache_head_dim, const int* d_pos, float scale,
+                                bool kv_int8, const float* kv_scales, int window, int n_splits, hipStream_t stream) {
+    const size_t bytes = (size_t)(n_heads > 0 ? n_heads : 0) * (head_dim > 0 ? head_dim : 0) * 2;
+    if (kv_int8) {
+        fprintf(stderr, "[jllm] flash_attention_decode_dyn: an INT8 cache needs separate K and V scales (use the "
+                        "overload taking k_scales and v_scales); output zero-filled\n");
+        zero_fill(output, bytes, stream);
+        return;
+    }
+    (void)kv_scales;
+    report(jllm_hip_flash_attention_decode_dyn(H(output), H(q), k_cache, v_cache, n_heads, n_kv_heads, head_dim,
+                                               cache_head_dim, d_pos, scale, 0, nullptr, nullptr, window, n_splits,
+                                               stream),
+           "flash_attention_decode_dyn", output, bytes, stream);
+}
+
+void flash_attention_decode_dyn(half* output, const half* q, const void* k_cache, const void* v_cache, int n_heads,
+                                int n_kv_heads, int head_dim, int cache_head_dim, const int* d_pos, float scale,
+                                bool kv_int8, const float* k_scales, const float* v_scales, int window, int n_splits,
+                                hipStream_t stream) {
+    report(jllm_hip_flash_attention_decode_dyn(H(output), H(q), k_cache, v_cache, n_heads, n_kv_heads, head_dim,
+                                               cache_head_dim, d_pos, scale, kv_int8 ? 1 : 0, k_scales, v_scales,
+                                               window, n_splits, stream),
+           "flash_attention_decode_dyn", output, (size_t)(n_heads > 0 ? n_heads : 0) * (head_dim > 0 ? head_dim : 0) * 2,
+           stream);
+}
+
+// in-place on fp32 logits: left unchanged on failure
+void softmax_inplace(float* x, int n, hipStream_t stream) {
+    report(jllm_hip_softmax_inplace(x, n, stream), "softmax_inplace", nullptr, 0, stream);
+}
+
 int decode_attn_splits(int seq_len) { return jllm_hip_decode_attn_splits(seq_len); }
 
 float* get_splitk_partials(int n_heads, int n_splits, int head_dim) {
@@ -160,6 +185,55 @@ void rope_inplace_store_kv_fp16(half* q, half* k, const half* v, half* k_cache_d
                                           nullptr, nullptr, (int64_t)n_kv_heads * head_dim, n_heads, n_kv_heads,
                                           head_dim, head_dim, position, 1, theta_base, neox ? 1 : 0, 0, stream),
            "rope_inplace_store_kv_fp16", nullptr, 0, stream);
+}
+
+void rope_inplace_store_kv_fp16_batched(half* q, half* k, const half* v, half* k_cache_base, half* v_cache_base,
+                                        int kv_slot, int n_heads, int n_kv_heads, int head_dim, int start_pos, int N,
+                                        int q_stride, int kv_stride, float theta_base, bool neox, hipStream_t stream) {
+    report(jllm_hip_rope_inplace_store_kv_fp16_batched(H(q), H(k), H(v), H(k_cache_base), H(v_cache_base), kv_slot,
+                                                       n_heads, n_kv_heads, head_dim, start_pos, N, q_stride,
+                                                       kv_stride, theta_base, neox ? 1 : 0, stream),
+           "rope_inplace_store_kv_fp16_batched", nullptr, 0, stream);
+}
+
+void rope_inplace_store_kv_fp16_dyn(half* q, half* k, const half* v, half* k_cache_layer_base,
+                                    half* v_cache_layer_base, int n_heads, int n_kv_heads, int head_dim,
+                                    int cache_head_dim, const int* d_pos, float theta_base, bool neox,
+                                    hipStream_t stream) {
+    report(jllm_hip_rope_inplace_store_kv_fp16_dyn(H(q), H(k), H(v), H(k_cache_layer_base), H(v_cache_layer_base),
+                                                   n_heads, n_kv_heads, head_dim, cache_head_dim, d_pos, theta_base,
+                                                   neox ? 1 : 0, stream),
+           "rope_inplace_store_kv_fp16_dyn", nullptr, 0, stream);
+}
+
+void rope_inplace_dyn(half* q, half* k, int n_heads, int n_kv_heads, int head_dim, const int* d_pos,
+                      float theta_base, bool neox, hipStream_t stream) {
+    report(jllm_hip_rope_inplace_dyn(H(q), H(k), n_heads, n_kv_heads, head_dim, d_pos, theta_base, neox ? 1 : 0,
+                                     stream),
+           "rope_inplace_dyn", nullptr, 0, stream);
+}
+
+void fused_geglu(half* output, const half* gate, const half* up, int rows, int intermediate_dim, hipStream_t stream) {
+    report(jllm_hip_fused_geglu(H(output), H(gate), H(up), rows, intermediate_dim, stream), "fused_geglu", output,
+           (size_t)(rows > 0 ? rows : 0) * (intermediate_dim > 0 ? intermediate_dim : 0) * 2, stream);
+}
+
+void vec_scale(half* x, int n, float s, hipStream_t stream) {
+    report(jllm_hip_vec_scale(H(x), n, s, stream), "vec_scale", nullptr, 0, stream);
+}
+
+void logit_softcap(float* x, int n, float cap, hipStream_t stream) {
+    report(jllm_hip_logit_softcap(x, n, cap, stream), "logit_softcap", nullptr, 0, stream);
+}
+
+void gemv_dense(half* out, const void* W, int wtype, const half* x, int M, int K, hipStream_t stream) {
+    report(jllm_hip_gemv_dense(H(out), W, wtype, H(x), M, K, stream), "gemv_dense", out,
+           (size_t)(M > 0 ? M : 0) * 2, stream);
+}
+
+void gemm_dense_batched(half* out, const void* W, int wtype, const half* x, int M, int N, int K, hipStream_t stream) {
+    report(jllm_hip_gemm_dense_batched(H(out), W, wtype, H(x), M, N, K, stream), "gemm_dense_batched", out,
+           (size_t)(M > 0 ? M : 0) * (N > 0 ? N : 0) * 2, stream);
 }
 
 void flash_attention_prefill_batched(half* output, const half* q, const void* k_cache, const void* v_cache,

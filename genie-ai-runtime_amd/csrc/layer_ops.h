@@ -22,9 +22,12 @@ hipError_t swiglu_launch(uint16_t* out, const uint16_t* gate, const uint16_t* up
 hipError_t vec_add_launch(uint16_t* out, const uint16_t* a, const uint16_t* b, int64_t n, hipStream_t st);
 
 // q [N][q_stride], k [N][k_stride] rotated in place; token t at position
-// start_pos + t.  k may be null (n_kv = 0).
+// start_pos + t, or *pos_dev + t when pos_dev is not null (read on the
+// device, so a captured graph stays valid for every position).  k may be
+// null (n_kv = 0).
 hipError_t rope_launch(uint16_t* q, uint16_t* k, int n_heads, int n_kv, int head_dim, int start_pos, int N,
-                       int q_stride, int k_stride, const RopeFreq& fr, bool neox, hipStream_t st);
+                       int q_stride, int k_stride, const RopeFreq& fr, bool neox, hipStream_t st,
+                       const int* pos_dev = nullptr);
 
 // Post-projection step of attention for N tokens: optional q/k RMSNorm
 // (weights q_norm/k_norm, fp32 or fp16), RoPE of q and k (both in place),
@@ -35,8 +38,8 @@ struct QKPostArgs {
     uint16_t* q;              // [N][n_heads * hd]
     uint16_t* k;              // [N][n_kv * hd]
     const uint16_t* v;        // [N][n_kv * hd]
-    const void* q_norm;       // [hd] or null (then k_norm is ignored too)
-    const void* k_norm;
+    const void* q_norm;       // [hd] or null (no q RMSNorm)
+    const void* k_norm;       // [hd] or null (no k RMSNorm)
     void* k_dst;              // row t at t * kv_stride elements, head h at h * cache_head_dim
     void* v_dst;
     float* k_scales;          // [t][n_kv] (int8 only; may be null)
@@ -46,6 +49,11 @@ struct QKPostArgs {
     float eps;
     int norm_fp32, neox, kv_int8;
     RopeFreq fr;
+    // input row strides (elements) of q and of k / v; 0 = packed rows
+    int64_t q_in_stride = 0, kv_in_stride = 0;
+    // when not null the first position is *pos_dev (read on the device) and
+    // k_dst / v_dst / k_scales / v_scales address position 0 of the layer
+    const int* pos_dev = nullptr;
 };
 hipError_t qk_post_launch(const QKPostArgs& a, hipStream_t st);
 

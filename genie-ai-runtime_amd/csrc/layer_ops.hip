@@ -209,7 +209,7 @@ __device__ __forceinline__ void rotate(float v0, float v1, float c, float s, flo
 // one thread per (token, head, pair)
 __global__ __launch_bounds__(256) void rope_kernel(uint16_t* q, uint16_t* k, int n_heads, int n_kv, int hd,
                                                    int start_pos, int N, int q_stride, int k_stride, RopeFreq fr,
-                                                   int neox) {
+                                                   int neox, const int* pos_dev) {
     const int h2 = hd / 2;
     const int64_t per_tok = (int64_t)(n_heads + n_kv) * h2;
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -219,7 +219,8 @@ __global__ __launch_bounds__(256) void rope_kernel(uint16_t* q, uint16_t* k, int
     const int head = r / h2, i = r % h2;
     uint16_t* p = head < n_heads ? q + (int64_t)t * q_stride + (int64_t)head * hd
                                  : k + (int64_t)t * k_stride + (int64_t)(head - n_heads) * hd;
-    const float ang = (float)(start_pos + t) * fr.f[i];
+    const int p0 = pos_dev ? *pos_dev : start_pos;
+    const float ang = (float)(p0 + t) * fr.f[i];
     float s, c;
     sincosf(ang, &s, &c);
     const int i0 = neox ? i : 2 * i, i1 = neox ? i + h2 : 2 * i + 1;
@@ -230,11 +231,12 @@ __global__ __launch_bounds__(256) void rope_kernel(uint16_t* q, uint16_t* k, int
 }
 
 hipError_t rope_launch(uint16_t* q, uint16_t* k, int n_heads, int n_kv, int head_dim, int start_pos, int N,
-                       int q_stride, int k_stride, const RopeFreq& fr, bool neox, hipStream_t st) {
+                       int q_stride, int k_stride, const RopeFreq& fr, bool neox, hipStream_t st,
+                       const int* pos_dev) {
     const int64_t total = (int64_t)(n_heads + n_kv) * (head_dim / 2) * N;
     if (total <= 0) return hipSuccess;
     hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, q, k, n_heads, n_kv,
-                       head_dim, start_pos, N, q_stride, k_stride, fr, neox ? 1 : 0);
+                       head_dim, start_pos, N, q_stride, k_stride, fr, neox ? 1 : 0, pos_dev);
     return hipGetLastError();
 }
 
@@ -256,26 +258,30 @@ __global__ __launch_bounds__(256) void qk_post_kernel(QKPostArgs a) {
     const int t = gw / slots, slot = gw % slots;
     const int kind = slot < a.n_heads ? 0 : (slot < a.n_heads + a.n_kv ? 1 : 2);   // q, k, v
     const int head = kind == 0 ? slot : (kind == 1 ? slot - a.n_heads : slot - a.n_heads - a.n_kv);
-    const uint16_t* src = kind == 0 ? a.q + ((int64_t)t * a.n_heads + head) * hd
-                                    : (kind == 1 ? a.k : a.v) + ((int64_t)t * a.n_kv + head) * hd;
-    const int pos = a.start_pos + t;
+    const int64_t qs = a.q_in_stride ? a.q_in_stride : (int64_t)a.n_heads * hd;
+    const int64_t ks = a.kv_in_stride ? a.kv_in_stride : (int64_t)a.n_kv * hd;
+    const uint16_t* src = kind == 0 ? a.q + t * qs + (int64_t)head * hd
+                                    : (kind == 1 ? a.k : a.v) + t * ks + (int64_t)head * hd;
+    const int p0 = a.pos_dev ? __builtin_amdgcn_readfirstlane(*a.pos_dev) : a.start_pos;
+    const int64_t r0 = a.pos_dev ? p0 : 0;            // cache row of token 0 relative to k_dst / v_dst
+    const int pos = p0 + t;
     float s = 0.0f, c = 1.0f;
     if (kind < 2) sincosf((float)pos * a.fr.f[l < hd / 2 ? l : 0], &s, &c);
     float v0, v1;
     int i0, i1;
-    front_pair(src, hd, a.neox != 0, kind < 2 ? (kind == 0 ? a.q_norm : (a.q_norm ? a.k_norm : nullptr)) : nullptr,
+    front_pair(src, hd, a.neox != 0, kind < 2 ? (kind == 0 ? a.q_norm : a.k_norm) : nullptr,
                a.norm_fp32 != 0, a.eps, kind < 2, c, s, l, v0, v1, i0, i1);
     if (kind < 2 && l < hd / 2) {
-        uint16_t* dq = kind == 0 ? a.q + ((int64_t)t * a.n_heads + head) * hd : a.k + ((int64_t)t * a.n_kv + head) * hd;
+        uint16_t* dq = kind == 0 ? a.q + t * qs + (int64_t)head * hd : a.k + t * ks + (int64_t)head * hd;
         dq[i0] = f32_to_f16_bits(v0);
         dq[i1] = f32_to_f16_bits(v1);
     }
     if (kind == 0) return;
-    const int64_t row = (int64_t)t * a.kv_stride + (int64_t)head * a.cache_head_dim;
+    const int64_t row = (r0 + t) * a.kv_stride + (int64_t)head * a.cache_head_dim;
     void* cache = kind == 1 ? a.k_dst : a.v_dst;
     float* sc = kind == 1 ? a.k_scales : a.v_scales;
     front_store_kv(a.kv_int8 ? (void*)((int8_t*)cache + row) : (void*)((uint16_t*)cache + row),
-                   sc ? sc + (int64_t)t * a.n_kv + head : nullptr, a.kv_int8 != 0, hd, v0, v1, i0, i1, l);
+                   sc ? sc + (r0 + t) * a.n_kv + head : nullptr, a.kv_int8 != 0, hd, v0, v1, i0, i1, l);
 }
 
 hipError_t qk_post_launch(const QKPostArgs& a, hipStream_t st) {

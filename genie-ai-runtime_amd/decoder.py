@@ -235,9 +235,11 @@ class Decoder:
 
 # ---- GGUF ------------------------------------------------------------------------
 
-def write_gguf(path, shape, model_np, arch="qwen3", max_seq=40960):
+def write_gguf(path, shape, model_np, arch="qwen3", max_seq=40960, hook=None):
     """Store a synth_np model as a GGUF v3 file with llama.cpp's tensor names
-    (the names the reference loader maps, model.cpp:675-810)."""
+    (the names the reference loader maps, model.cpp:675-810).  hook(name,
+    ggml_type, dims, array) -> (ggml_type, dims, array), when given, may
+    change a tensor before it is written (tests write malformed models)."""
     lib = jllm.lib()
     w = lib.jllm_hip_gguf_writer_create()
     if not w:
@@ -263,6 +265,8 @@ def write_gguf(path, shape, model_np, arch="qwen3", max_seq=40960):
         keep = []
 
         def tensor(name, t, dims, arr):
+            if hook:
+                t, dims, arr = hook(name, t, dims, arr)
             a = np.ascontiguousarray(arr)
             keep.append(a)
             d = (ctypes.c_int64 * len(dims))(*dims)

@@ -43,6 +43,7 @@ SIGNATURES = {
     "jllm_hip_mmq_subdots": (I, [P, P, I, P, I, I, I, P]),
     "jllm_hip_flash_attention_decode": (I, [P, P, P, P, I, I, I, I, I, F, I, P, P, I, P]),
     "jllm_hip_flash_attention_decode_splits": (I, [P, P, P, P, I, I, I, I, I, F, I, P, P, I, I, P]),
+    "jllm_hip_flash_attention_decode_dyn": (I, [P, P, P, P, I, I, I, I, P, F, I, P, P, I, I, P]),
     "jllm_hip_decode_attn_splits": (I, [I]),
     "jllm_hip_get_splitk_partials": (P, [I, I, I]),
     "jllm_hip_fp16_to_int8": (I, [P, P, P, I, I, P]),
@@ -52,12 +53,22 @@ SIGNATURES = {
     "jllm_hip_vec_add": (I, [P, P, P, I64, P]),
     "jllm_hip_rope_inplace": (I, [P, P, I, I, I, I, F, I, P]),
     "jllm_hip_rope_inplace_batched": (I, [P, P, I, I, I, I, I, I, I, F, I, P]),
+    "jllm_hip_rope_inplace_dyn": (I, [P, P, I, I, I, P, F, I, P]),
+    "jllm_hip_rope_inplace_store_kv_fp16_dyn": (I, [P, P, P, P, P, I, I, I, I, P, F, I, P]),
+    "jllm_hip_rope_inplace_store_kv_fp16_batched": (I, [P, P, P, P, P, I, I, I, I, I, I, I, I, F, I, P]),
     "jllm_hip_rope_precompute_table": (I, [I, I, F]),
     "jllm_hip_rope_clear_tables": (None, []),
     "jllm_hip_qk_norm_rope_store_kv": (I, [P, P, P, P, P, I, F, P, P, P, P, I64, I, I, I, I, I, I, F, I, I, P]),
     "jllm_hip_dequant_embedding_row": (I, [P, P, I, I, I, P]),
     "jllm_hip_dequant_embedding_rows": (I, [P, P, I, P, I, I, I, P]),
     "jllm_hip_argmax_f32": (I, [P, P, I, P]),
+    # outside the Llama/Qwen decode path (Gemma family, logits)
+    "jllm_hip_fused_geglu": (I, [P, P, P, I, I, P]),
+    "jllm_hip_vec_scale": (I, [P, I64, F, P]),
+    "jllm_hip_logit_softcap": (I, [P, I64, F, P]),
+    "jllm_hip_softmax_inplace": (I, [P, I, P]),
+    "jllm_hip_gemv_dense": (I, [P, P, I, P, I, I, P]),
+    "jllm_hip_gemm_dense_batched": (I, [P, P, I, P, I, I, I, P]),
     # GGUF reader / loader / writer
     "jllm_hip_gguf_open": (P, [ctypes.c_char_p]),
     "jllm_hip_gguf_close": (None, [P]),

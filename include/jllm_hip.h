@@ -38,7 +38,11 @@ const char* jllm_hip_status_string(int status);
 
 /* Mapped-weight registry.  Replaces register_mapped_weight_region,
  * clear_mapped_weight_region, resolve_mapped_weight_device_ptr
- * (jllm_kernels.h:40-43, defined in src/engine/model.cpp:39-66). */
+ * (jllm_kernels.h:40-43, defined in src/engine/model.cpp:39-66) for callers
+ * without the engine.  Resolution (here and for every weight argument)
+ * looks in this registry first, then in the engine's own registry when the
+ * engine's jllm::resolve_mapped_weight_device_ptr is linked into the process
+ * (a weak reference: the library does not define the jllm:: registry). */
 int         jllm_hip_register_mapped_weight_region(const void* host_base, const void* device_base, int64_t bytes);
 void        jllm_hip_clear_mapped_weight_region(const void* host_base);
 const void* jllm_hip_resolve_mapped_weight_device_ptr(const void* host_ptr);
@@ -199,6 +203,21 @@ int jllm_hip_flash_attention_decode_splits(uint16_t* out, const uint16_t* q, con
                                            int seq_len, float scale, int kv_int8, const float* k_scales,
                                            const float* v_scales, int window, int n_splits, void* stream);
 
+/* Decode attention whose key count is read on the device: seq = *d_pos + 1
+ * at kernel execution time, so one captured HIP graph serves every decode
+ * position; n_splits (1..256) is fixed by the caller, as in the reference
+ * (size the partials buffer with jllm_hip_get_splitk_partials(n_heads,
+ * n_splits, head_dim) before capture).  Splits that receive no keys
+ * contribute nothing.  INT8 caches take their K and V scales separately
+ * (the reference's single kv_scales argument passed one buffer as both,
+ * attention.cu:1021-1024; that path is unreachable there because graph mode
+ * is off for INT8 KV).  Replaces flash_attention_decode_dyn,
+ * jllm_kernels.h:380 (attention.cu:1007-1034). */
+int jllm_hip_flash_attention_decode_dyn(uint16_t* out, const uint16_t* q, const void* k, const void* v,
+                                        int n_heads, int n_kv_heads, int head_dim, int cache_head_dim,
+                                        const int32_t* d_pos, float scale, int kv_int8, const float* k_scales,
+                                        const float* v_scales, int window, int n_splits, void* stream);
+
 /* Split-count policy and partials buffer.  Replace decode_attn_splits and
  * get_splitk_partials, jllm_kernels.h:402-403 (attention.cu:975-1005).  The
  * MI355X policy is ceil(seq/32) splits capped at 128 (one wave per KV head
@@ -259,11 +278,37 @@ int  jllm_hip_rope_inplace(uint16_t* q, uint16_t* k, int n_heads, int n_kv_heads
 int  jllm_hip_rope_inplace_batched(uint16_t* q, uint16_t* k, int n_heads, int n_kv_heads, int head_dim,
                                    int start_pos, int N, int q_stride, int k_stride, float theta_base, int neox,
                                    void* stream);
+/* RoPE of one token whose position is read on the device (*d_pos at kernel
+ * execution time); k may be NULL with n_kv_heads 0 (rotate q only).
+ * Replaces rope_inplace_dyn, jllm_kernels.h:306 (rope.cu:719-735). */
+int  jllm_hip_rope_inplace_dyn(uint16_t* q, uint16_t* k, int n_heads, int n_kv_heads, int head_dim,
+                               const int32_t* d_pos, float theta_base, int neox, void* stream);
+/* RoPE of q and k plus fp16 copies of the rotated k and of v into the cache
+ * (no q/k norm, no int8).
+ *   _dyn: one token at position *d_pos (device); k and v go to
+ *     k/v_cache_layer_base + pos * n_kv_heads * cache_head_dim, head h at
+ *     h * cache_head_dim.  Replaces rope_inplace_store_kv_fp16_dyn,
+ *     jllm_kernels.h:287 (rope.cu:737-763, kernel :581-640).
+ *   _batched: N tokens at positions start_pos + t; q/k/v rows at t * q_stride
+ *     / t * kv_stride halves; the cache row of token t at t * kv_slot halves
+ *     from k/v_cache_base, head h at h * head_dim.  Replaces
+ *     rope_inplace_store_kv_fp16_batched, jllm_kernels.h:278 (rope.cu:551-574,
+ *     kernel :498-529). */
+int  jllm_hip_rope_inplace_store_kv_fp16_dyn(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* k_cache_layer_base,
+                                             uint16_t* v_cache_layer_base, int n_heads, int n_kv_heads, int head_dim,
+                                             int cache_head_dim, const int32_t* d_pos, float theta_base, int neox,
+                                             void* stream);
+int  jllm_hip_rope_inplace_store_kv_fp16_batched(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* k_cache_base,
+                                                 uint16_t* v_cache_base, int kv_slot, int n_heads, int n_kv_heads,
+                                                 int head_dim, int start_pos, int N, int q_stride, int kv_stride,
+                                                 float theta_base, int neox, void* stream);
 int  jllm_hip_rope_precompute_table(int max_seq, int head_dim, float theta_base);
 void jllm_hip_rope_clear_tables(void);
 
 /* The attention front of N tokens in one launch: q_norm/k_norm RMSNorm over
- * each head (skipped when q_norm is NULL), RoPE of q and k (both in place),
+ * each head (both given, or both NULL to skip the norms, as the engine
+ * applies them only when a layer has both; one without the other is
+ * JLLM_ERR_INVALID), RoPE of q and k (both in place),
  * then k and v written to the cache rows of positions start_pos + t: int8
  * with a per-(position, kv head) scale absmax/127 (kv_int8 != 0) or fp16.
  * q [N][n_heads*hd], k and v [N][n_kv_heads*hd].  k_dst/v_dst address the
@@ -305,6 +350,31 @@ int jllm_hip_dequant_embedding_rows(uint16_t* dst, const void* W, int ggml_type,
  * small library-owned device array of per-chunk candidates: calls on one
  * device must be serialised (one stream). */
 int jllm_hip_argmax_f32(int32_t* out, const float* logits, int n, void* stream);
+
+/* ---- kernels outside the Llama/Qwen decode path (Gemma family, logits) ---- */
+
+/* out = half(gelu_tanh(gate) * up) over rows x intermediate_dim,
+ * gelu_tanh(g) = 0.5 g (1 + tanh(0.7978845608 (g + 0.044715 g^3))).
+ * Replaces fused_geglu, jllm_kernels.h:203 (convert.cu:121-151). */
+int jllm_hip_fused_geglu(uint16_t* out, const uint16_t* gate, const uint16_t* up, int rows, int intermediate_dim,
+                         void* stream);
+/* x *= s in place: element pairs (0,1), (2,3), ... are multiplied in fp16 by
+ * half(s); a trailing odd element in fp32 by s, then rounded.  Replaces
+ * vec_scale, jllm_kernels.h:207 (convert.cu:155-170). */
+int jllm_hip_vec_scale(uint16_t* x, int64_t n, float s, void* stream);
+/* x = cap * tanh(x / cap) in place on fp32 logits (cap > 0).  Replaces
+ * logit_softcap, jllm_kernels.h:210 (convert.cu:173-181). */
+int jllm_hip_logit_softcap(float* x, int64_t n, float cap, void* stream);
+/* x = exp(x - max) / sum in place on fp32 logits (one workgroup).  Replaces
+ * softmax_inplace, jllm_kernels.h:407 (softmax.cu:15-81). */
+int jllm_hip_softmax_inplace(float* x, int n, void* stream);
+/* Dense projections, W row-major [M][K] of F32 (wtype 0), F16 (1) or BF16
+ * (30): out[t][m] = half(sum_k W[m][k] x[t][k]), fp32 accumulation; x fp16
+ * [N][K].  Other types: JLLM_ERR_UNSUPPORTED.  Replace gemv_dense and
+ * gemm_dense_batched, jllm_kernels.h:214-226 (gemv_q4.cu:2815-2885). */
+int jllm_hip_gemv_dense(uint16_t* out, const void* W, int wtype, const uint16_t* x, int M, int K, void* stream);
+int jllm_hip_gemm_dense_batched(uint16_t* out, const void* W, int wtype, const uint16_t* x, int M, int N, int K,
+                                void* stream);
 
 /* ---- decoder loop (the engine-side caller of the kernels above) ---- */
 

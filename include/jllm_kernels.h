@@ -17,7 +17,12 @@
 
 namespace jllm {
 
-// mapped-weight registry (jllm_kernels.h:40-43 of the reference)
+// mapped-weight registry (jllm_kernels.h:40-43 of the reference).  Declared
+// here because the engine includes them from this header, but NOT defined by
+// libjllm_hip.so: their definitions live in the engine's src/engine/model.cpp
+// (:39-66), which stays compiled.  The library consults the engine's registry
+// through a weak reference to resolve_mapped_weight_device_ptr when the
+// engine is linked in, and its own C registry (jllm_hip.h) otherwise.
 const void* resolve_mapped_weight_device_ptr(const void* host_ptr);
 void register_mapped_weight_region(const void* host_base, const void* device_base, int64_t bytes);
 void clear_mapped_weight_region(const void* host_base);
@@ -55,6 +60,24 @@ void flash_attention_decode(half* output, const half* q, const void* k_cache, co
 int decode_attn_splits(int seq_len);
 float* get_splitk_partials(int n_heads, int n_splits, int head_dim);
 
+// graph-capturable decode attention, seq = *d_pos + 1 on the device
+// (reference :380).  The reference signature carries one kv_scales pointer,
+// which its split-K path passes as both K and V scales (attention.cu:1021-1024,
+// unreachable there since graph mode is off for INT8 KV): here an FP16 cache
+// is supported through it and an INT8 cache is refused (stderr, output
+// zero-filled); INT8 callers use the overload with separate scales.
+void flash_attention_decode_dyn(half* output, const half* q, const void* k_cache, const void* v_cache, int n_heads,
+                                int n_kv_heads, int head_dim, int cache_head_dim, const int* d_pos, float scale,
+                                bool kv_int8, const float* kv_scales, int window, int n_splits, hipStream_t stream);
+// no reference counterpart: the same with separate K and V scales (INT8 KV)
+void flash_attention_decode_dyn(half* output, const half* q, const void* k_cache, const void* v_cache, int n_heads,
+                                int n_kv_heads, int head_dim, int cache_head_dim, const int* d_pos, float scale,
+                                bool kv_int8, const float* k_scales, const float* v_scales, int window, int n_splits,
+                                hipStream_t stream);
+
+// logits softmax (reference :407)
+void softmax_inplace(float* x, int n, hipStream_t stream);
+
 // KV quantiser (reference :413)
 void fp16_to_int8(int8_t* dst, float* scale_out, const half* src, int rows, int cols, hipStream_t stream);
 
@@ -78,5 +101,23 @@ void rope_inplace_store_kv_fp16(half* q, half* k, const half* v, half* k_cache_d
                                 hipStream_t stream);
 void rope_inplace_batched(half* q, half* k, int n_heads, int n_kv_heads, int head_dim, int start_pos, int N,
                           int q_stride, int k_stride, float theta_base, bool neox, hipStream_t stream);
+void rope_inplace_store_kv_fp16_batched(half* q, half* k, const half* v, half* k_cache_base, half* v_cache_base,
+                                        int kv_slot, int n_heads, int n_kv_heads, int head_dim, int start_pos, int N,
+                                        int q_stride, int kv_stride, float theta_base, bool neox, hipStream_t stream);
+
+// graph-capturable RoPE, position read from *d_pos on the device (reference :287, :306)
+void rope_inplace_store_kv_fp16_dyn(half* q, half* k, const half* v, half* k_cache_layer_base,
+                                    half* v_cache_layer_base, int n_heads, int n_kv_heads, int head_dim,
+                                    int cache_head_dim, const int* d_pos, float theta_base, bool neox,
+                                    hipStream_t stream);
+void rope_inplace_dyn(half* q, half* k, int n_heads, int n_kv_heads, int head_dim, const int* d_pos,
+                      float theta_base, bool neox, hipStream_t stream);
+
+// Gemma-family kernels (reference :203-226)
+void fused_geglu(half* output, const half* gate, const half* up, int rows, int intermediate_dim, hipStream_t stream);
+void vec_scale(half* x, int n, float s, hipStream_t stream);
+void logit_softcap(float* x, int n, float cap, hipStream_t stream);
+void gemv_dense(half* out, const void* W, int wtype, const half* x, int M, int K, hipStream_t stream);
+void gemm_dense_batched(half* out, const void* W, int wtype, const half* x, int M, int N, int K, hipStream_t stream);
 
 }  // namespace jllm

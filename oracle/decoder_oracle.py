@@ -38,7 +38,7 @@ def mmvq_f16(W, t, x, M, K):
 
 
 def float_f16(W, t, x, M, K):
-    return _f16(oracle.gemv_quant_cpu(W, t, x, M, K))
+    return _f16(oracle.gemv_quant_cpu(W, t, x, M, K, threads=None))
 
 
 def pair(W0, t0, W1, t1, x, M, K):
@@ -52,7 +52,7 @@ def triple_mmvq(t0, t1, t2):
 
 def gemv_add(W, t, x, res, M, K):
     """gemv_quant_add: half(half(W.x) + residual), float dequant."""
-    proj = _f32(_f16(oracle.gemv_quant_cpu(W, t, x, M, K)))
+    proj = _f32(_f16(oracle.gemv_quant_cpu(W, t, x, M, K, threads=None)))
     return _f16(proj + _f32(res))
 
 
@@ -91,7 +91,7 @@ class OracleDecoder:
             self.logits = oracle.mmvq(self.m["output"], t, oracle.quantize_q8_1(normed, s.hidden_dim), s.vocab_size,
                                       s.hidden_dim)
         else:
-            self.logits = oracle.gemv_quant_cpu(self.m["output"], t, normed, s.vocab_size, s.hidden_dim)
+            self.logits = oracle.gemv_quant_cpu(self.m["output"], t, normed, s.vocab_size, s.hidden_dim, threads=None)
         return oracle.argmax(self.logits)
 
     def _attn_front(self, l, L, q, k, v, start, N):

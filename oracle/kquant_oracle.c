@@ -38,6 +38,13 @@
 
 #define QK_K 256
 
+/* Thread count of the row/token-parallel loops below (orc_mmvq, orc_mmq_*,
+ * the prefill attention).  Each output element is computed by one thread in
+ * the same operation order as the serial loop, so results do not depend on
+ * it; it only makes the full-size decoder oracle finish in minutes. */
+int orc_threads = 1;
+void orc_set_threads(int n) { orc_threads = n > 0 ? n : 1; }
+
 /* GGUF block layouts, gemv_q4.cu:141-164 */
 #pragma pack(push, 1)
 typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[12]; uint8_t qs[128]; } orc_block_q4k;   /* 144 B */
@@ -377,6 +384,7 @@ float orc_mmvq_q6k_row(const void* Wrow, const void* xq, int K) {
 
 void orc_mmvq(float* y, const void* W, int type, const void* xq, int M, int K) {
     const int nb = K / QK_K;
+    #pragma omp parallel for num_threads(orc_threads) schedule(static)
     for (int r = 0; r < M; r++) {
         if (type == 12) y[r] = orc_mmvq_q4k_row((const orc_block_q4k*)W + (int64_t)r * nb, xq, K);
         else            y[r] = orc_mmvq_q6k_row((const orc_block_q6k*)W + (int64_t)r * nb, xq, K);
@@ -423,6 +431,7 @@ void orc_mmq_subdots(int32_t* out, const void* W, int type, const void* q8v, int
 void orc_mmq_q4k(float* y, const void* W, const void* q8v, int M, int N, int K, int Npad) {
     const orc_block_q8_1_mmq* q8 = (const orc_block_q8_1_mmq*)q8v;
     const int nb = K / QK_K;
+    #pragma omp parallel for collapse(2) num_threads(orc_threads) schedule(static)
     for (int t = 0; t < N; t++)
         for (int r = 0; r < M; r++) {
             float sum = 0.0f;
@@ -459,6 +468,7 @@ void orc_mmq_q4k(float* y, const void* W, const void* q8v, int M, int N, int K, 
 void orc_mmq_q6k(float* y, const void* W, const void* q8v, int M, int N, int K, int Npad) {
     const orc_block_q8_1_mmq* q8 = (const orc_block_q8_1_mmq*)q8v;
     const int nb = K / QK_K;
+    #pragma omp parallel for collapse(2) num_threads(orc_threads) schedule(static)
     for (int t = 0; t < N; t++)
         for (int r = 0; r < M; r++) {
             float sum = 0.0f;

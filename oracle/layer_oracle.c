@@ -22,6 +22,15 @@
  *   orc_embed_row  : the dequant oracle pinned in kquant_oracle.c.
  *   orc_argmax     : numpy argmax over the finite values (first index).
  *   orc_attn_prefill: float64 numpy causal softmax attention.
+ *   orc_geglu      : |gelu_tanh(g) - g*Phi(g)| <= 5e-4 against the exact
+ *                    erf GELU (float64), odd part gelu(g) - gelu(-g) = g,
+ *                    u = 0 -> 0.
+ *   orc_vec_scale  : numpy float16 products (one rounding of the exact
+ *                    product) for pairs, float32 for a trailing element.
+ *   orc_logit_softcap: float64 cap * tanh(x / cap); |x| << cap -> x.
+ *   orc_softmax    : float64 softmax; shift invariance; sums to 1.
+ *   orc_dense      : float64 numpy dot of the widened weights (bf16 via
+ *                    torch's bfloat16 conversion).
  */
 #include <math.h>
 #include <stdint.h>
@@ -37,6 +46,7 @@ void orc_dequant_q5k(float* out, const void* W, int64_t n_blocks);
 void orc_attn_decode_int8(uint16_t* out, const uint16_t* q, const int8_t* kc, const int8_t* vc,
                           int n_heads, int n_kv, int hd, int chd, int seq, float scale,
                           const float* ks, const float* vs, int window, int n_splits);
+extern int orc_threads;
 
 
 /* fused_rmsnorm_residual_kernel, fused_norm.cu:33-101: v = x + residual
@@ -170,7 +180,66 @@ void orc_attn_prefill_int8(uint16_t* out, const uint16_t* q, const int8_t* kc, c
                            int n_kv, int hd, int chd, int N, int start_pos, float scale, const float* ks,
                            const float* vs, int window) {
     const int64_t qd = (int64_t)n_heads * hd;
+    #pragma omp parallel for num_threads(orc_threads) schedule(dynamic)
     for (int t = 0; t < N; t++)
         orc_attn_decode_int8(out + t * qd, q + t * qd, kc, vc, n_heads, n_kv, hd, chd, start_pos + t + 1, scale, ks,
                              vs, window, 1);
+}
+
+/* ---- kernels outside the Llama/Qwen decode path (Gemma family, logits) ---- */
+
+/* geglu_kernel, convert.cu:121-151: out = half(gelu_tanh(g) * u),
+ * gelu_tanh(g) = 0.5*g*(1 + tanhf(0.7978845608028654*(g + 0.044715*g*g*g))). */
+void orc_geglu(uint16_t* out, const uint16_t* gate, const uint16_t* up, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        const float g = orc_f16_to_f32(gate[i]), u = orc_f16_to_f32(up[i]);
+        const float gl = 0.5f * g * (1.0f + tanhf(0.7978845608028654f * (g + 0.044715f * g * g * g)));
+        out[i] = orc_f32_to_f16(gl * u);
+    }
+}
+
+/* vec_scale_kernel, convert.cu:155-170: pairs (2i, 2i+1) with 2i+1 < n are
+ * multiplied in fp16 by half(s) (__hmul2: the exact product rounded once);
+ * a trailing odd element in fp32 by s. */
+void orc_vec_scale(uint16_t* x, int64_t n, float s) {
+    const float sh = orc_f16_to_f32(orc_f32_to_f16(s));
+    for (int64_t i = 0; i < n; i++) {
+        const float f = (i < (n & ~(int64_t)1)) ? sh : s;
+        x[i] = orc_f32_to_f16(orc_f16_to_f32(x[i]) * f);
+    }
+}
+
+/* logit_softcap_kernel, convert.cu:173-181: x = cap * tanhf(x / cap). */
+void orc_logit_softcap(float* x, int64_t n, float cap) {
+    for (int64_t i = 0; i < n; i++) x[i] = cap * tanhf(x[i] / cap);
+}
+
+/* softmax_kernel, softmax.cu:15-81: max, e = expf(x - max) with its sum,
+ * then x = e * (1/sum) (sums here in index order). */
+void orc_softmax(float* x, int n) {
+    float m = -FLT_MAX;
+    for (int i = 0; i < n; i++) m = fmaxf(m, x[i]);
+    float s = 0.0f;
+    for (int i = 0; i < n; i++) { x[i] = expf(x[i] - m); s += x[i]; }
+    const float inv = 1.0f / s;
+    for (int i = 0; i < n; i++) x[i] *= inv;
+}
+
+/* gemv_dense_kernel / gemm_dense_batched_kernel, gemv_q4.cu:2815-2885:
+ * out[t][m] = half(sum_k w(m, k) * x[t][k]), w from F32 (wtype 0), F16 (1)
+ * or BF16 (30, the high half of an fp32), fp32 sum in k order. */
+void orc_dense(uint16_t* out, const void* W, int wtype, const uint16_t* x, int M, int N, int K) {
+    for (int t = 0; t < N; t++)
+        for (int m = 0; m < M; m++) {
+            float acc = 0.0f;
+            for (int k = 0; k < K; k++) {
+                const int64_t i = (int64_t)m * K + k;
+                float w;
+                if (wtype == 0) w = ((const float*)W)[i];
+                else if (wtype == 1) w = orc_f16_to_f32(((const uint16_t*)W)[i]);
+                else { const uint32_t b = (uint32_t)((const uint16_t*)W)[i] << 16; memcpy(&w, &b, 4); }
+                acc += w * orc_f16_to_f32(x[(int64_t)t * K + k]);
+            }
+            out[(int64_t)t * M + m] = orc_f32_to_f16(acc);
+        }
 }

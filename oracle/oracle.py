@@ -28,6 +28,7 @@ def lib():
         _lib = ctypes.CDLL(LIB_PATH)
         P, I, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
         sig = {
+            "orc_set_threads": (None, [I]),
             "orc_f16_to_f32": (F, [ctypes.c_uint16]),
             "orc_f32_to_f16": (ctypes.c_uint16, [F]),
             "orc_dequant_q4k": (None, [P, P, ctypes.c_int64]),
@@ -52,11 +53,28 @@ def lib():
             "orc_embed_row": (None, [P, P, I, I, I]),
             "orc_argmax": (I, [P, I]),
             "orc_attn_prefill_int8": (None, [P, P, P, P, I, I, I, I, I, I, F, P, P, I]),
+            "orc_geglu": (None, [P, P, P, ctypes.c_int64]),
+            "orc_vec_scale": (None, [P, ctypes.c_int64, F]),
+            "orc_logit_softcap": (None, [P, ctypes.c_int64, F]),
+            "orc_softmax": (None, [P, I]),
+            "orc_dense": (None, [P, P, I, P, I, I, I]),
         }
         for n, (r, a) in sig.items():
             f = getattr(_lib, n)
             f.restype, f.argtypes = r, a
     return _lib
+
+
+_threads = 1
+
+
+def set_threads(n):
+    """Thread count of the oracle's row/token-parallel loops (MMVQ, MMQ,
+    prefill attention, and gemv_quant_cpu when called with threads=None).
+    Results are independent of it."""
+    global _threads
+    _threads = max(1, int(n))
+    lib().orc_set_threads(_threads)
 
 
 def _p(a):
@@ -86,6 +104,8 @@ def dequant(W, ggml_type, rows, K):
 
 def gemv_quant_cpu(W, ggml_type, x, M, K, threads=1):
     W, x = _c(W, np.uint8), _c(x, np.uint16)
+    if threads is None:
+        threads = _threads
     y = np.empty(M, dtype=np.float32)
     if threads == 1:
         st = lib().orc_gemv_quant_cpu(_p(y), _p(W), ggml_type, _p(x), M, K)
@@ -223,4 +243,40 @@ def attn_prefill_int8(q, k, v, n_heads, n_kv, hd, chd, N, start_pos, scale, ks, 
     out = np.empty(N * n_heads * hd, dtype=np.uint16)
     lib().orc_attn_prefill_int8(_p(out), _p(q), _p(k), _p(v), n_heads, n_kv, hd, chd, N, start_pos, float(scale),
                                 _p(ks), _p(vs), window)
+    return out
+
+
+# ---- kernels outside the Llama/Qwen decode path (layer_oracle.c) ----
+
+def geglu(g, u):
+    g, u = _c(g, np.uint16).ravel(), _c(u, np.uint16).ravel()
+    out = np.empty(g.size, dtype=np.uint16)
+    lib().orc_geglu(_p(out), _p(g), _p(u), g.size)
+    return out
+
+
+def vec_scale(x, s):
+    x = np.array(x, dtype=np.uint16, copy=True).ravel()
+    lib().orc_vec_scale(_p(x), x.size, float(s))
+    return x
+
+
+def logit_softcap(x, cap):
+    x = np.array(x, dtype=np.float32, copy=True).ravel()
+    lib().orc_logit_softcap(_p(x), x.size, float(cap))
+    return x
+
+
+def softmax(x):
+    x = np.array(x, dtype=np.float32, copy=True).ravel()
+    lib().orc_softmax(_p(x), x.size)
+    return x
+
+
+def dense(W, wtype, x, M, N, K):
+    """W raw bytes/values [M][K] (float32 for wtype 0, uint16 bits for 1 / 30)."""
+    W = _c(W, np.float32 if wtype == 0 else np.uint16)
+    x = _c(x, np.uint16)
+    out = np.empty(N * M, dtype=np.uint16)
+    lib().orc_dense(_p(out), _p(W), wtype, _p(x), M, N, K)
     return out

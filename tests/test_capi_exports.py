@@ -35,14 +35,78 @@ def test_every_c_declaration_exported():
         assert n in jllm.SIGNATURES, n
 
 
-def test_every_cpp_declaration_exported():
+# the engine's mapped-weight registry: declared in jllm_kernels.h, defined by
+# the engine's src/engine/model.cpp:39-66 (which stays compiled), never by the library
+REGISTRY = {"register_mapped_weight_region", "clear_mapped_weight_region", "resolve_mapped_weight_device_ptr"}
+
+
+def _cpp_declared():
     hdr = open(os.path.join(ROOT, "include", "jllm_kernels.h")).read()
     body = hdr[hdr.index("namespace jllm {"):]
-    names = set(re.findall(r"^\s*(?:const\s+)?[\w\*]+\*?\s+\**(\w+)\s*\(", body, re.M))
+    return set(re.findall(r"^\s*(?:const\s+)?[\w\*]+\*?\s+\**(\w+)\s*\(", body, re.M))
+
+
+def test_every_cpp_declaration_exported():
+    names = _cpp_declared()
     assert {"gemv_quant", "gemm_quant_batched", "flash_attention_decode", "fp16_to_int8"} <= names
+    assert REGISTRY <= names
     exp = _exports()
-    missing = [n for n in sorted(names) if f"jllm::{n}(" not in exp]
+    missing = [n for n in sorted(names - REGISTRY) if f"jllm::{n}(" not in exp]
     assert not missing, missing
+    defined_registry = [n for n in REGISTRY if f"jllm::{n}(" in exp]
+    assert not defined_registry, defined_registry
+
+
+# Every function of the reference's include/jllm_kernels.h (namespace jllm):
+# the engine's kernel translation units (gemv_q4.cu, mmq_q4k_llama.cu,
+# mmq_q6k_llama.cu, attention.cu, rope.cu, fused_norm.cu, convert.cu,
+# softmax.cu, dense_tc.cu) can all be dropped only if the library defines
+# each of them except the registry, which model.cpp defines.
+REFERENCE_HEADER_FUNCTIONS = {
+    "resolve_mapped_weight_device_ptr", "register_mapped_weight_region", "clear_mapped_weight_region",
+    "gemv_q4", "gemv_quant", "gemv_quant_add", "gemv_quant_pair", "gemv_quant_triple", "gemm_quant_batched",
+    "gemv_quant_f32", "dequant_embedding_row", "fused_rmsnorm_residual", "fused_swiglu", "fused_geglu",
+    "vec_scale", "logit_softcap", "gemv_dense", "gemm_dense_batched", "rope_precompute_table",
+    "rope_clear_tables", "rope_inplace", "rope_inplace_store_kv_fp16", "rope_inplace_batched",
+    "rope_inplace_store_kv_fp16_batched", "rope_inplace_store_kv_fp16_dyn", "rope_inplace_dyn",
+    "flash_attention_decode", "flash_attention_prefill_batched", "flash_attention_decode_dyn",
+    "decode_attn_splits", "get_splitk_partials", "softmax_inplace", "fp16_to_int8",
+}
+
+
+def test_reference_header_fully_declared():
+    assert REFERENCE_HEADER_FUNCTIONS <= _cpp_declared()
+
+
+def test_engine_links_against_library_alone(tmp_path):
+    """A C++ translation unit calling every function the engine calls through
+    jllm_kernels.h links against libjllm_hip.so plus a stand-in of
+    model.cpp's registry and nothing else (-Wl,--no-undefined); no jllm::
+    symbol is defined both by the library and by the stand-in; and the
+    library's weak reference finds the engine's registry at run time."""
+    cxx = os.path.join(ROOT, "tests", "cxx")
+    exe = str(tmp_path / "engine_link")
+    libdir = os.path.dirname(jllm.LIB_PATH)
+    cmd = ["/opt/rocm/bin/hipcc", "-std=c++17", "-O1", "-I" + os.path.join(ROOT, "include"),
+           os.path.join(cxx, "engine_link.cpp"), os.path.join(cxx, "model_registry_stub.cpp"),
+           "-L" + libdir, "-ljllm_hip", "-Wl,-rpath," + libdir, "-Wl,--no-undefined", "-o", exe]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-4000:]
+    stub_obj = str(tmp_path / "stub.o")
+    r = subprocess.run(["/opt/rocm/bin/hipcc", "-std=c++17", "-c", "-I" + os.path.join(ROOT, "include"),
+                        os.path.join(cxx, "model_registry_stub.cpp"), "-o", stub_obj], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-4000:]
+    stub = subprocess.run(["nm", "-C", "--defined-only", stub_obj], capture_output=True, text=True, check=True).stdout
+    stub_defs = set(re.findall(r" T (jllm::\w+)\(", stub))
+    lib_defs = set(re.findall(r" T (jllm::\w+)\(", _exports()))
+    assert stub_defs == {"jllm::" + n for n in REGISTRY}
+    assert not (stub_defs & lib_defs)
+    called = subprocess.run(["nm", "-DC", exe], capture_output=True, text=True, check=True).stdout
+    undefined = set(re.findall(r" U (jllm::\w+)\(", called))
+    internal = {"quantize_q8_1", "gemm_q4k_mmq_llama", "gemm_q6k_mmq_llama"}   # gemv_q4.cu:468, :2462, :2470
+    assert undefined == {"jllm::" + n for n in (REFERENCE_HEADER_FUNCTIONS - REGISTRY) | internal}
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and "engine link ok" in r.stdout, r.stdout + r.stderr
 
 
 def test_status_strings():

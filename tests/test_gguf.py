@@ -163,3 +163,94 @@ def test_decoder_from_gguf_matches_in_memory_model(dev, tiny_file):
     assert a.cpu().tolist() == b.cpu().tolist()
     ref.close()
     gg.close()
+
+
+def _load_fails(path, capfd, needle):
+    """The loader refuses the file before any device allocation (the message
+    names the offending tensor)."""
+    lib = jllm.lib()
+    cfg, g = decoder.gguf_config(path)
+    try:
+        m = lib.jllm_hip_gguf_model_load(g, ctypes.addressof(cfg))
+        assert not m
+    finally:
+        lib.jllm_hip_gguf_close(g)
+    err = capfd.readouterr().err
+    assert needle in err, err
+
+
+def test_model_load_rejects_wrong_shaped_matrix(tmp_path, capfd):
+    """attn_k stored as [1024, 64] instead of [512, 128]: the same byte count,
+    but the GEMV would read rows of the wrong length."""
+    model = decoder.synth_np(TINY, 34)
+
+    def hook(name, t, dims, arr):
+        return (t, [1024, 64], arr) if name == "blk.1.attn_k.weight" else (t, dims, arr)
+    path = tmp_path / "bad_k.gguf"
+    decoder.write_gguf(path, TINY, model, hook=hook)
+    _load_fails(path, capfd, "blk.1.attn_k.weight")
+
+
+def test_model_load_rejects_mixed_norm_types(tmp_path, capfd):
+    """blk.0 norms are F32 (so the config says fp32), blk.1's attn_norm is F16:
+    the decoder would read it as fp32."""
+    model = decoder.synth_np(TINY, 35)
+
+    def hook(name, t, dims, arr):
+        if name == "blk.1.attn_norm.weight":
+            return 1, dims, np.asarray(arr, np.float32).astype(np.float16).view(np.uint16)
+        return t, dims, arr
+    path = tmp_path / "bad_norm.gguf"
+    decoder.write_gguf(path, TINY, model, hook=hook)
+    _load_fails(path, capfd, "blk.1.attn_norm.weight")
+
+
+def test_model_load_rejects_unsupported_matrix_type(tmp_path, capfd):
+    model = decoder.synth_np(TINY, 36)
+
+    def hook(name, t, dims, arr):
+        if name == "blk.0.ffn_up.weight":      # the same bytes declared as F16 [4096, 9*...] -> not a K-quant
+            n = np.asarray(arr).nbytes // 2
+            return 1, [n], arr
+        return t, dims, arr
+    path = tmp_path / "bad_type.gguf"
+    decoder.write_gguf(path, TINY, model, hook=hook)
+    _load_fails(path, capfd, "blk.0.ffn_up.weight")
+
+
+@pytest.mark.parametrize("field,value,needle", [("hidden_dim", 5120, "hidden_dim must be <= 4096"),
+                                                ("head_dim", 80, "head_dim must be a multiple of 32"),
+                                                ("n_kv_heads", 3, "n_heads must be a multiple"),
+                                                ("intermediate_dim", 1000, "multiples of 256")])
+def test_decoder_create_rejects_unsupported_shapes(capfd, field, value, needle):
+    """Refused at creation (before any allocation), with the reason."""
+    cfg = decoder.Config(2, 2560, 32, 8, 128, 9728, 1000, 64, 1e-6, 1e6, 1, 1, 1, 1, 1)
+    setattr(cfg, field, value)
+    arr = (decoder.LayerW * 2)()
+    mw = decoder.ModelW()
+    h = jllm.lib().jllm_hip_decoder_create(ctypes.addressof(cfg), ctypes.addressof(mw), ctypes.addressof(arr), 16)
+    assert not h
+    err = capfd.readouterr().err
+    assert needle in err, err
+
+
+def test_gguf_config_rejects_unsupported_shapes(tmp_path, capfd):
+    shape = decoder.Shape(n_layers=1, hidden_dim=512, n_heads=8, n_kv_heads=2, head_dim=64, intermediate_dim=1024,
+                          vocab_size=1000)
+    model = decoder.synth_np(shape, 37)
+    path = tmp_path / "hd64.gguf"
+    decoder.write_gguf(path, shape, model)
+
+    lib = jllm.lib()
+    g = lib.jllm_hip_gguf_open(str(path).encode())
+    cfg = decoder.Config()
+    assert lib.jllm_hip_gguf_config(g, ctypes.addressof(cfg)) == 0     # head_dim 64 is supported
+    lib.jllm_hip_gguf_close(g)
+    bad = decoder.Shape(n_layers=1, hidden_dim=512, n_heads=8, n_kv_heads=3, head_dim=64, intermediate_dim=1024,
+                        vocab_size=1000)
+    path = tmp_path / "kv3.gguf"
+    decoder.write_gguf(path, bad, decoder.synth_np(bad, 38))
+    g = lib.jllm_hip_gguf_open(str(path).encode())
+    assert lib.jllm_hip_gguf_config(g, ctypes.addressof(cfg)) == -2
+    lib.jllm_hip_gguf_close(g)
+    assert "n_heads must be a multiple" in capfd.readouterr().err

@@ -225,3 +225,84 @@ def test_decoder_oracle_prefill_chunking_and_steps():
     rel = np.abs(c.logits - a.logits).max() / np.abs(a.logits).max()
     assert rel < 2e-2, rel
     assert np.abs(a.logits).max() > 0.5                   # the random model is not degenerate
+
+
+# ---- kernels outside the Llama/Qwen decode path ------------------------------
+
+def test_geglu_against_exact_gelu():
+    from scipy.special import erf
+    g = synth.rng(21)
+    gate = f16b(np.concatenate([np.linspace(-8, 8, 4001), g.standard_normal(3000) * 3]))
+    one = f16b(np.ones(gate.size))
+    got = f64(oracle.geglu(gate, one))
+    x = f64(gate)
+    exact = x * 0.5 * (1.0 + erf(x / np.sqrt(2.0)))
+    # the tanh form is within ~4.7e-4 of the erf GELU (plus one fp16 rounding)
+    assert np.all(np.abs(got - exact) <= 5e-4 + np.abs(exact) * 2 ** -10)
+    # odd part: gelu(x) - gelu(-x) = x  (one fp16 rounding each)
+    neg = f64(oracle.geglu(f16b(-x), one))
+    assert np.all(np.abs((got - neg) - x) <= 2 * 2 ** -10 * np.maximum(np.abs(got), np.abs(neg)) + 1e-6)
+    # up = 0 -> 0; up scales the result
+    assert np.all(f64(oracle.geglu(gate, f16b(np.zeros(gate.size)))) == 0)
+
+
+def test_vec_scale_is_fp16_product():
+    g = synth.rng(22)
+    for n in (1, 2, 7, 1000, 1001):
+        x = synth.x_f16(g, n)
+        for s in (1.5, 0.1, 3.3333, 1.0 / 3.0):
+            got = oracle.vec_scale(x, s).view(np.float16)
+            xf = x.view(np.float16)
+            m = n & ~1
+            want = np.empty(n, np.float16)
+            want[:m] = (xf[:m].astype(np.float32) * np.float32(np.float16(s))).astype(np.float16)
+            want[m:] = (xf[m:].astype(np.float32) * np.float32(s)).astype(np.float16)
+            assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    # s = 2 doubles exactly
+    x = synth.x_f16(g, 64)
+    assert np.array_equal(oracle.vec_scale(x, 2.0).view(np.float16), x.view(np.float16) * np.float16(2))
+
+
+def test_logit_softcap_vs_float64():
+    g = synth.rng(23)
+    x = (g.standard_normal(10000) * 40).astype(np.float32)
+    got = oracle.logit_softcap(x, 30.0)
+    want = 30.0 * np.tanh(x.astype(np.float64) / 30.0)
+    assert np.all(np.abs(got - want) <= 4 * np.spacing(np.abs(want).astype(np.float32)) + 1e-7)
+    small = np.float32([1e-3, -2e-3])
+    assert np.allclose(oracle.logit_softcap(small, 30.0), small, rtol=1e-6)
+
+
+def test_softmax_vs_float64():
+    g = synth.rng(24)
+    x = (g.standard_normal(151936) * 5).astype(np.float32)
+    got = oracle.softmax(x).astype(np.float64)
+    e = np.exp(x.astype(np.float64) - x.max())
+    want = e / e.sum()
+    assert np.abs(got.sum() - 1.0) < 1e-4
+    assert np.all(np.abs(got - want) <= 1e-4 * want + 1e-12)
+    assert np.allclose(oracle.softmax(x + np.float32(3.0)), got, rtol=1e-4, atol=1e-12)
+
+
+@pytest.mark.parametrize("wtype", [0, 1, 30])
+def test_dense_vs_float64(wtype):
+    import torch
+    g = synth.rng(25 + wtype)
+    M, N, K = 37, 3, 520
+    wf = (g.standard_normal((M, K)) * 0.05).astype(np.float32)
+    if wtype == 0:
+        W, wv = wf, wf.astype(np.float64)
+    elif wtype == 1:
+        W = f16b(wf)
+        wv = f64(W).reshape(M, K)
+    else:
+        tb = torch.from_numpy(wf).to(torch.bfloat16)
+        W = tb.view(torch.int16).numpy().view(np.uint16)
+        wv = tb.to(torch.float64).numpy()
+    x = synth.x_f16(g, (N, K))
+    got = f64(oracle.dense(W, wtype, x, M, N, K)).reshape(N, M)
+    want = f64(x).reshape(N, K) @ wv.T
+    sabs = np.abs(f64(x).reshape(N, K)) @ np.abs(wv).T
+    assert np.all(np.abs(got - want) <= 2 ** -11 * np.abs(want) + 1e-6 * sabs + 1e-7)
+    # a transposed operand or a dropped term would miss by O(|want|)
+    assert np.abs(want).max() > 0.1
