@@ -20,6 +20,7 @@
 namespace jllm_hip {
 
 typedef uint32_t u32x4x __attribute__((ext_vector_type(4)));
+typedef float f32x4x __attribute__((ext_vector_type(4)));
 
 // gelu_tanh(g) * u, gelu_tanh(g) = 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3)))
 __device__ __forceinline__ float geglu_val(float g, float u) {
@@ -104,9 +105,9 @@ __device__ __forceinline__ float dense_w(const void* W, int64_t i) {
 template <int WT>
 __device__ __forceinline__ void dense_w8(const void* W, int64_t i, float (&w)[8]) {
     if (WT == 0) {
-        const u32x4x a = *(const u32x4x*)((const float*)W + i), b = *(const u32x4x*)((const float*)W + i + 4);
-#pragma unroll
-        for (int e = 0; e < 4; e++) { w[e] = __builtin_bit_cast(float, a[e]); w[4 + e] = __builtin_bit_cast(float, b[e]); }
+        const f32x4x a = *(const f32x4x*)((const float*)W + i), b = *(const f32x4x*)((const float*)W + i + 4);
+        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+        w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
     } else {
         const u32x4x a = *(const u32x4x*)((const uint16_t*)W + i);
 #pragma unroll

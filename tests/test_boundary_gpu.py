@@ -14,7 +14,8 @@
 Bars as in the other GPU tests: bit-exact where the arithmetic is the same
 expression (vec_scale, the position variants against their fixed forms);
 one fp16 ulp where a libm function or a reduction order differs (GeGLU,
-dense projections); 4 fp32 ulps for the soft-cap; 1e-5 relative for softmax.
+dense projections); 4 fp32 ulps for the soft-cap; for softmax 2e-4 relative to the oracle's
+serial fp32 sum and 2e-5 to float64.
 """
 import ctypes
 import os
@@ -238,7 +239,11 @@ def test_softmax(dev, n):
     xd = to_dev(x)
     jllm.call("jllm_hip_softmax_inplace", xd, n)
     got, want = from_dev(xd), oracle.softmax(x)
-    assert np.all(np.abs(got - want) <= 1e-5 * want + 1e-12)
+    # the oracle sums the n exponentials serially in fp32 (error ~1e-4 at the
+    # vocabulary size), the kernel in a tree: both against float64 too
+    e = np.exp(x.astype(np.float64) - x.max())
+    assert np.all(np.abs(got - want) <= 2e-4 * want + 1e-12)
+    assert np.all(np.abs(got - e / e.sum()) <= 2e-5 * e / e.sum() + 1e-12)
 
 
 @pytest.mark.parametrize("wtype,M,N,K", [(0, 2560, 1, 256), (30, 256 * 35, 1, 2560), (1, 333, 5, 2560),
