@@ -28,19 +28,26 @@ int attn_check(const void* out, const void* q, const void* k, const void* v, int
     return JLLM_OK;
 }
 
+// part: the caller's partials buffer (allocation-free entry), else the
+// library's grown-on-demand one
 int attn_run(uint16_t* out, const uint16_t* q, const void* k, const void* v, int n_heads, int n_kv, int hd, int chd,
              int seq, float scale, int kv_int8, const float* ks, const float* vs, int window, int n_splits,
-             void* stream, const int32_t* pos_dev = nullptr) {
+             void* stream, const int32_t* pos_dev = nullptr, float* part = nullptr) {
     int st = attn_check(out, q, k, v, n_heads, n_kv, hd, chd, pos_dev ? 1 : seq, kv_int8, window);
     if (st) return st;
     if (n_splits < 1) n_splits = 1;
     if (n_splits > ATTN_MAX_SPLITS) n_splits = ATTN_MAX_SPLITS;
-    uint8_t* scratch = (uint8_t*)g_part.get(attn_scratch_bytes(n_heads, n_splits, hd));
-    if (!scratch) return JLLM_ERR_NOMEM;
+    int* counters = nullptr;
+    if (!part) {
+        uint8_t* sc = (uint8_t*)g_part.get(attn_scratch_bytes(n_heads, n_splits, hd));
+        if (!sc) return JLLM_ERR_NOMEM;
+        counters = (int*)sc;
+        part = (float*)(sc + ATTN_COUNTER_BYTES);
+    }
     AttnArgs a;
     a.out = out; a.q = q; a.k = k; a.v = v; a.ks = ks; a.vs = vs;
-    a.counters = (int*)scratch;
-    a.part = (float*)(scratch + ATTN_COUNTER_BYTES);
+    a.counters = counters;
+    a.part = part;
     a.n_heads = n_heads; a.n_kv = n_kv; a.head_dim = hd; a.cache_head_dim = chd;
     a.seq = seq; a.window = window; a.n_splits = n_splits; a.scale = scale; a.tokens = 1; a.tq = 1; a.wsplit = 1;
     a.pos_dev = pos_dev;

@@ -9,7 +9,7 @@
 using namespace jllm_hip;
 
 namespace {
-DeviceScratch g_q8;     // quantised activations (fp16 codes + scale words), grown on demand, never freed
+DeviceScratch g_q8;     // quantised activations (int8 and fp16 codes + scale words), grown on demand, never freed
 DeviceScratch g_ws;     // split-K fp32 partials [splits][N][M], grown on demand, never freed
 
 int npad_of(int N) { return ((N + MMQ_TILE_N - 1) / MMQ_TILE_N) * MMQ_TILE_N; }
@@ -32,7 +32,7 @@ int check_gemm(const char* tag, const void* y, int type, const uint16_t* x, int 
 
 // The product of an already quantised activation (q8 = codes + scale words
 // of the right kind, or null for Q5_K) into y.
-int mmq_after_quant(const char* tag, void* y, const void* Wd, int type, const uint16_t* x, const uint16_t* codes,
+int mmq_after_quant(const char* tag, void* y, const void* Wd, int type, const uint16_t* x, const void* codes,
                     const uint32_t* scl, int M, int N, int K, int out_kind, hipStream_t st,
                     const uint16_t* res = nullptr) {
     // split-K when the tile grid alone does not cover the chip: partials to
@@ -61,19 +61,29 @@ const void* device_weight(const char* tag, const void* W) {
     return Wd;
 }
 
-// q8 scratch: codes, then the scale words of up to two quantiser kinds
-int q8_scratch(const char* tag, int N, int K, uint16_t*& codes, uint32_t* (&scl)[2]) {
+// q8 scratch for the two quantiser kinds, kind 0 = DS4 (Q4_K kernel: int8
+// codes), kind 1 = D4 (Q6_K kernel: fp16 codes): the codes, then the scale
+// words of each kind
+int q8_scratch(const char* tag, int N, int K, void* (&codes)[2], uint32_t* (&scl)[2]) {
     const int Npad = npad_of(N);
-    const size_t cb = mmq_codes_bytes(K, Npad), sb = mmq_scales_bytes(K, Npad);
-    uint8_t* q8 = (uint8_t*)g_q8.get(cb + 2 * sb);
+    const size_t c8 = mmq_codes8_bytes(K, Npad), c16 = mmq_codes_bytes(K, Npad), sb = mmq_scales_bytes(K, Npad);
+    uint8_t* q8 = (uint8_t*)g_q8.get(c8 + c16 + 2 * sb);
     if (!q8) {
         fprintf(stderr, "[%s] q8 scratch allocation failed\n", tag);
         return JLLM_ERR_NOMEM;
     }
-    codes = (uint16_t*)q8;
-    scl[0] = (uint32_t*)(q8 + cb);
-    scl[1] = (uint32_t*)(q8 + cb + sb);
+    codes[0] = q8;
+    codes[1] = q8 + c8;
+    scl[0] = (uint32_t*)(q8 + c8 + c16);
+    scl[1] = (uint32_t*)(q8 + c8 + c16 + sb);
     return JLLM_OK;
+}
+
+// the activation quantised for weight type `type` (12: kind 0, 14: kind 1)
+hipError_t quantize_for(int type, const uint16_t* x, void* const (&codes)[2], uint32_t* const (&scl)[2], int N, int K,
+                        hipStream_t st, const uint16_t* up = nullptr) {
+    const int k = type == 12 ? 0 : 1;
+    return quantize_mmq_f16_launch(x, codes[k], scl[k], N, K, npad_of(N), k == 0, st, up, k == 0);
 }
 
 int run_mmq(const char* tag, void* y, const void* W, int type, const uint16_t* x, int M, int N, int K,
@@ -82,14 +92,15 @@ int run_mmq(const char* tag, void* y, const void* W, int type, const uint16_t* x
     if (!Wd) return JLLM_ERR_POINTER;
     if (!aligned16(Wd)) return JLLM_ERR_INVALID;
     hipStream_t st = (hipStream_t)stream;
-    uint16_t* codes = nullptr;
+    void* codes[2] = {nullptr, nullptr};
     uint32_t* scl[2] = {nullptr, nullptr};
+    const int k = type == 12 ? 0 : 1;
     if (type != 13) {
         int r = q8_scratch(tag, N, K, codes, scl); if (r) return r;
-        const hipError_t e = quantize_mmq_f16_launch(x, codes, scl[0], N, K, npad_of(N), type == 12, st);
+        const hipError_t e = quantize_for(type, x, codes, scl, N, K, st);
         if (e != hipSuccess) return launch_status(e, tag);
     }
-    return mmq_after_quant(tag, y, Wd, type, x, codes, scl[0], M, N, K, out_kind, st);
+    return mmq_after_quant(tag, y, Wd, type, x, codes[k], scl[k], M, N, K, out_kind, st);
 }
 }  // namespace
 
@@ -115,14 +126,15 @@ int gemm_batched_res(const char* tag, uint16_t* y, const void* W, int type, cons
     const void* Wd = device_weight(tag, W);
     if (!Wd) return JLLM_ERR_POINTER;
     if (!aligned16(Wd)) return JLLM_ERR_INVALID;
-    uint16_t* codes = nullptr;
+    void* codes[2] = {nullptr, nullptr};
     uint32_t* scl[2] = {nullptr, nullptr};
+    const int k = type == 12 ? 0 : 1;
     if (type != 13) {
         st = q8_scratch(tag, N, K, codes, scl); if (st) return st;
-        const hipError_t e = quantize_mmq_f16_launch(x, codes, scl[0], N, K, npad_of(N), type == 12, hs, up);
+        const hipError_t e = quantize_for(type, x, codes, scl, N, K, hs, up);
         if (e != hipSuccess) return launch_status(e, tag);
     }
-    return mmq_after_quant(tag, y, Wd, type, x, codes, scl[0], M, N, K, 0, hs, res);
+    return mmq_after_quant(tag, y, Wd, type, x, codes[k], scl[k], M, N, K, 0, hs, res);
 }
 
 int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uint16_t* x, int N, int K, void* stream) {
@@ -137,7 +149,7 @@ int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uin
         return JLLM_OK;
     }
     hipStream_t hs = (hipStream_t)stream;
-    uint16_t* codes = nullptr;
+    void* codes[2] = {nullptr, nullptr};
     uint32_t* scl[2] = {nullptr, nullptr};
     bool need[2] = {false, false};                   // DS4 (Q4_K), D4 (Q6_K)
     for (int i = 0; i < n; i++) {
@@ -149,7 +161,7 @@ int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uin
         int st = q8_scratch(tag, N, K, codes, scl); if (st) return st;
         for (int k = 0; k < 2; k++) {
             if (!need[k]) continue;
-            const hipError_t e = quantize_mmq_f16_launch(x, codes, scl[k], N, K, npad_of(N), k == 0, hs);
+            const hipError_t e = quantize_for(k == 0 ? 12 : 14, x, codes, scl, N, K, hs);
             if (e != hipSuccess) return launch_status(e, tag);
         }
     }
@@ -172,15 +184,16 @@ int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uin
             rtiles += (outs[i].M + 127) / 128;
         }
         if (all4 && nm >= 2 && rtiles * (npad_of(N) / MMQ_TILE_N) >= MMQ_MULTI_MIN_TILES)
-            return launch_status(mmq_q4k_multi_launch(Wm, ym, Mm, nm, codes, scl[0], N, K, npad_of(N), hs), tag);
+            return launch_status(mmq_q4k_multi_launch(Wm, ym, Mm, nm, (const uint8_t*)codes[0], scl[0], N, K,
+                                                      npad_of(N), hs), tag);
     }
     for (int i = 0; i < n; i++) {
         if (outs[i].M == 0) continue;
         const void* Wd = device_weight(tag, outs[i].W);
         if (!Wd) return JLLM_ERR_POINTER;
         if (!aligned16(Wd)) return JLLM_ERR_INVALID;
-        const uint32_t* sc = outs[i].type == 12 ? scl[0] : scl[1];
-        int st = mmq_after_quant(tag, outs[i].y, Wd, outs[i].type, x, codes, sc, outs[i].M, N, K, 0, hs);
+        const int k = outs[i].type == 12 ? 0 : 1;
+        int st = mmq_after_quant(tag, outs[i].y, Wd, outs[i].type, x, codes[k], scl[k], outs[i].M, N, K, 0, hs);
         if (st) return st;
     }
     return JLLM_OK;
@@ -224,6 +237,16 @@ int jllm_hip_quantize_mmq_f16(const uint16_t* x, uint16_t* codes, uint32_t* scal
         return JLLM_ERR_INVALID;
     if (Npad == 0) return JLLM_OK;
     return launch_status(quantize_mmq_f16_launch(x, codes, scales, N, K, Npad, ds4 != 0, (hipStream_t)stream), "GEMM");
+}
+
+int jllm_hip_quantize_mmq_i8(const uint16_t* x, int8_t* codes, uint32_t* scales, int N, int K, int Npad, int ds4,
+                             void* stream) {
+    if (!x || !codes || !scales || N < 0 || K <= 0 || K % 256 != 0 || Npad < N || Npad % MMQ_TILE_N != 0 ||
+        !aligned16(x) || !aligned16(codes))
+        return JLLM_ERR_INVALID;
+    if (Npad == 0) return JLLM_OK;
+    return launch_status(quantize_mmq_f16_launch(x, codes, scales, N, K, Npad, ds4 != 0, (hipStream_t)stream,
+                                                 nullptr, true), "GEMM");
 }
 
 int jllm_hip_mmq_subdots(int32_t* out, const void* W, int type, const uint16_t* x, int M, int N, int K,

@@ -14,19 +14,23 @@ constexpr int MMQ_REF_NPAD = 64;  // Npad granularity of the reference-layout qu
 // float d per 32)
 hipError_t quantize_mmq_launch(const uint16_t* x, void* q8, int N, int K, int Npad, bool ds4, hipStream_t st);
 
-// the same values in the kernels' layout: codes fp16 [K/256][Npad][256],
-// scale words [K/32][Npad] (DS4: half d | half sum << 16; D4: float d)
-// (up != null: the values are half(silu(x) * up), the SwiGLU of gate x and up)
-hipError_t quantize_mmq_f16_launch(const uint16_t* x, uint16_t* codes, uint32_t* scl, int N, int K, int Npad,
-                                   bool ds4, hipStream_t st, const uint16_t* up = nullptr);
-inline size_t mmq_codes_bytes(int K, int Npad) { return (size_t)K * Npad * 2; }
+// the same values in the kernels' layout: codes [K/256][Npad][256] as fp16
+// values (i8 = false; the Q6_K kernel) or int8 bytes (i8 = true; the Q4_K
+// kernel), scale words [K/32][Npad] (DS4: half d | half sum << 16; D4:
+// float d) (up != null: the values are half(silu(x) * up), the SwiGLU of
+// gate x and up)
+hipError_t quantize_mmq_f16_launch(const uint16_t* x, void* codes, uint32_t* scl, int N, int K, int Npad,
+                                   bool ds4, hipStream_t st, const uint16_t* up = nullptr, bool i8 = false);
+inline size_t mmq_codes_bytes(int K, int Npad) { return (size_t)K * Npad * 2; }     // fp16 layout
+inline size_t mmq_codes8_bytes(int K, int Npad) { return (size_t)K * Npad; }        // int8 layout
 inline size_t mmq_scales_bytes(int K, int Npad) { return (size_t)(K / 32) * Npad * 4; }
 
 // out_kind: 0 = fp16 y[N x M], 1 = fp32 y[N x M], 2 = raw int32 sub-block
 // dots [N][M][K/G] (G = 32 for Q4_K, 16 for Q6_K).  splits > 1 (fp32 only):
 // K is cut into `splits` ranges of whole super-blocks and range s writes
 // its partial sums to y + s*N*M (reduce with splitk_reduce_launch).
-hipError_t mmq_launch(void* y, const uint8_t* W, int type, const uint16_t* codes, const uint32_t* scl, int M, int N,
+// codes: int8 layout for Q4_K, fp16 layout for Q6_K
+hipError_t mmq_launch(void* y, const uint8_t* W, int type, const void* codes, const uint32_t* scl, int M, int N,
                       int K, int Npad, int out_kind, int splits, hipStream_t st);
 
 // Weight matrices of one multi-matrix launch (row tiles of segment s:
@@ -44,7 +48,7 @@ constexpr int MMQ_MULTI_MIN_TILES = 384;
 
 // Q4_K only, fp16 y, no split: the nseg (<= 3) products W[s] . x -> y[s]
 // of one quantised activation, one launch over all their row tiles.
-hipError_t mmq_q4k_multi_launch(const uint8_t* const* W, void* const* y, const int* M, int nseg, const uint16_t* codes,
+hipError_t mmq_q4k_multi_launch(const uint8_t* const* W, void* const* y, const int* M, int nseg, const uint8_t* codes,
                                 const uint32_t* scl, int N, int K, int Npad, hipStream_t st);
 
 // Split count for an N x M x K GEMM: enough workgroups to cover the chip

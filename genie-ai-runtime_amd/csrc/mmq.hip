@@ -102,10 +102,12 @@ hipError_t quantize_mmq_launch(const uint16_t* x, void* q8, int N, int K, int Np
 // stay within the lane -- so d and the sum are the same floats.
 // SW: the values are half(silu(gate) * up) of two fp16 inputs (x = gate,
 // x2 = up), formed here exactly as the SwiGLU kernel rounds them.
-template <bool SW>
+// I8: the codes as int8 bytes [K/256][Npad][256] (the Q4_K kernel's layout)
+// instead of fp16 values.
+template <bool SW, bool I8>
 __global__ __launch_bounds__(256) void quantize_mmq_f16_kernel(const uint16_t* __restrict__ x,
                                                                const uint16_t* __restrict__ x2,
-                                                               uint16_t* __restrict__ codes,
+                                                               void* __restrict__ codes,
                                                                uint32_t* __restrict__ scl, int N, int K, int Npad,
                                                                int ds4) {
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;     // (col, kb32, sub), sub fastest
@@ -146,25 +148,41 @@ __global__ __launch_bounds__(256) void quantize_mmq_f16_kernel(const uint16_t* _
     const float sum = s1[0] + s1[1];
     const float d = amax / 127.0f;
     const float dinv = d > 0.0f ? 1.0f / d : 0.0f;
-    uint32_t o[4];
+    const int64_t at = ((int64_t)(kb32 >> 3) * Npad + col) * 256 + (kb32 & 7) * 32 + 8 * sub;
+    if (I8) {
+        uint32_t o[2] = {0u, 0u};
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const int q0 = (int)__builtin_rintf(v[2 * e] * dinv), q1 = (int)__builtin_rintf(v[2 * e + 1] * dinv);
-        o[e] = (uint32_t)f32_to_f16_bits((float)q0) | ((uint32_t)f32_to_f16_bits((float)q1) << 16);
+        for (int e = 0; e < 8; e++) {
+            const int q = (int)__builtin_rintf(v[e] * dinv);
+            o[e >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (e & 3));
+        }
+        *(u32x2m*)((uint8_t*)codes + at) = u32x2m{o[0], o[1]};
+    } else {
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int q0 = (int)__builtin_rintf(v[2 * e] * dinv), q1 = (int)__builtin_rintf(v[2 * e + 1] * dinv);
+            o[e] = (uint32_t)f32_to_f16_bits((float)q0) | ((uint32_t)f32_to_f16_bits((float)q1) << 16);
+        }
+        *(u32x4m*)((uint16_t*)codes + at) = u32x4m{o[0], o[1], o[2], o[3]};
     }
-    *(u32x4m*)(codes + ((int64_t)(kb32 >> 3) * Npad + col) * 256 + (kb32 & 7) * 32 + 8 * sub) =
-        u32x4m{o[0], o[1], o[2], o[3]};
     if (sub == 0)
         scl[(int64_t)kb32 * Npad + col] =
             ds4 ? ((uint32_t)f32_to_f16_bits(d) | ((uint32_t)f32_to_f16_bits(sum) << 16)) : __builtin_bit_cast(uint32_t, d);
 }
 
-hipError_t quantize_mmq_f16_launch(const uint16_t* x, uint16_t* codes, uint32_t* scl, int N, int K, int Npad,
-                                   bool ds4, hipStream_t st, const uint16_t* up) {
+hipError_t quantize_mmq_f16_launch(const uint16_t* x, void* codes, uint32_t* scl, int N, int K, int Npad,
+                                   bool ds4, hipStream_t st, const uint16_t* up, bool i8) {
     const int64_t nthr = (int64_t)Npad * (K / 32) * 4;
     const dim3 g((unsigned)((nthr + 255) / 256));
-    if (up) hipLaunchKernelGGL(quantize_mmq_f16_kernel<true>, g, dim3(256), 0, st, x, up, codes, scl, N, K, Npad, ds4 ? 1 : 0);
-    else    hipLaunchKernelGGL(quantize_mmq_f16_kernel<false>, g, dim3(256), 0, st, x, x, codes, scl, N, K, Npad, ds4 ? 1 : 0);
+    const int d4 = ds4 ? 1 : 0;
+    if (i8) {
+        if (up) hipLaunchKernelGGL((quantize_mmq_f16_kernel<true, true>), g, dim3(256), 0, st, x, up, codes, scl, N, K, Npad, d4);
+        else    hipLaunchKernelGGL((quantize_mmq_f16_kernel<false, true>), g, dim3(256), 0, st, x, x, codes, scl, N, K, Npad, d4);
+    } else {
+        if (up) hipLaunchKernelGGL((quantize_mmq_f16_kernel<true, false>), g, dim3(256), 0, st, x, up, codes, scl, N, K, Npad, d4);
+        else    hipLaunchKernelGGL((quantize_mmq_f16_kernel<false, false>), g, dim3(256), 0, st, x, x, codes, scl, N, K, Npad, d4);
+    }
     return hipGetLastError();
 }
 
@@ -212,19 +230,46 @@ __device__ __forceinline__ f32x16m mfma16(h8m a, h8m b, f32x16m c) {
 // a second two-slot ring indexed by the super-block's parity.
 
 // ---------------------------------------------------------------------------
-// Q4_K
+// Q4_K on the int8 matrix cores.
+//
+// Per 32-wide sub-block j the dots C_j = sum q4 * q8 (q4 in 0..15, q8 in
+// -127..127) are one v_mfma_i32_32x32x32_i8 per 32 x 32 (rows x tokens)
+// tile -- exact int32, K = 32 is exactly one sub-block.  The epilogue the
+// format forces, sum += half(d*sc_j) * d8_j * C_j, takes the scale product
+// S = half(d*sc_j) * d8_j (two fp16 values, exact in fp32) from a
+// v_mfma_f32_32x32x8_f16 outer product, so each output element costs the
+// VALU one cvt and one fma per sub-block; the min term sum_j half(-dmin*m_j)
+// * sumx_j of a half super-block is one more K = 8 f16 MFMA accumulating
+// straight into the fp32 result.  (A register-only microbenchmark of this
+// step, genie-ai-runtime_amd/microbench/mmq_ceiling.hip, bounds it at ~20 %
+// of the int8 peak: the fp32 epilogue, not the matrix cores, is the limit.)
+//
+// Workgroup tile 128 rows x 64 tokens, 4 waves of 32 rows x 64 tokens (two
+// 32 x 32 tiles sharing the weight operand).  The K loop runs over half
+// super-blocks ("stages" of 128 weights).  A wave's weight bytes are its
+// own: each lane loads its 2 x 16 code bytes of the next stage (and, once
+// per super-block, its row's 16-byte header) straight into registers one
+// stage ahead.  The activation codes and scale words, shared by the four
+// waves, go from global memory straight to LDS (buffer_load ... lds) in a
+// ring of three stages, two stages ahead; the 16-byte pieces of a token are
+// XOR-swizzled so the B-operand reads of a wave hit distinct banks.
+constexpr int ST_B = TN * 128;              // activation codes of a stage: 64 tokens x 128 B
+constexpr int ST_S = 4 * TN * 4;            // scale words: 4 sub-blocks x 64 tokens
+constexpr int ST_BYTES = ST_B + ST_S;
+constexpr int NRING = 3;
 
-// Up to three weight matrices (same K, same activation) in one launch: the
-// row tiles of segment s are [rt0[s], rt0[s+1]) of the grid's row-tile index.
+typedef __attribute__((address_space(3))) void lds_void;
+
+// piece P (16 B) of token t's 128 code bytes sits at position P ^ swz_b(t),
+// so that any 8 (and any 16) consecutive lanes of an operand read hit
+// distinct 16-byte bank groups
+__host__ __device__ __forceinline__ int swz_b(int tok) { return (tok ^ (tok >> 3)) & 7; }
+
 template <int OUT>   // 0: fp16 y [N][M], 1: fp32 y [N][M], 2: int32 dots [N][M][K/32]
-__global__ __launch_bounds__(MMQ_THREADS, 2)
-void mmq_q4k_kernel(MmqSegs sg, const uint16_t* __restrict__ codes,
+__global__ __launch_bounds__(MMQ_THREADS, 3)
+void mmq_q4k_kernel(MmqSegs sg, const uint8_t* __restrict__ codes,
                     const uint32_t* __restrict__ scl, int N, int K, int Npad, int sps) {
-    __shared__ __attribute__((aligned(16))) uint8_t sA[2][TM * A4_STRIDE];
-    __shared__ __attribute__((aligned(16))) uint8_t sB[2][TN * B_STRIDE];
-    __shared__ __attribute__((aligned(16))) _Float16 sDA[2][8 * TM];     // half(d*sc) per [j][row]
-    __shared__ __attribute__((aligned(16))) _Float16 sMA[2][8 * TM];     // half(-dmin*m) per [j][row]
-    __shared__ __attribute__((aligned(16))) uint32_t sS8[2][8 * TN];     // half d8 | half sum x << 16, per [j][token]
+    __shared__ __attribute__((aligned(16))) uint8_t smem[NRING * ST_BYTES];
 
     const int nb = K / QK_K, nst = 2 * nb;
     // split-K: this workgroup's stages [k0, k1) (whole super-blocks)
@@ -238,186 +283,179 @@ void mmq_q4k_kernel(MmqSegs sg, const uint16_t* __restrict__ codes,
     const int M = sg.M[sgi];
     const int row0 = (rt - sg.rt0[sgi]) * TM, col0 = (tile % n_tt) * TN;
     const int t = threadIdx.x, w = t >> 6, l = t & 63, li = l & 31, g = l >> 5;
-    const int arow = 32 * w + li;                    // A-operand row of this lane (wave w owns rows 32w..32w+31)
-    const uint32_t gmask = g ? 0u : 0xFFFFu;         // keeps the low fp16 of a word in lanes g = 0 only
+    const int arow = 32 * w + li;                      // this lane's A-operand row
 
-    // buffer descriptors: per-thread byte offsets are fixed, the stage moves
-    // the scalar offset (no 64-bit address arithmetic in the loop)
     const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0,
                                                                          (int)((int64_t)M * nb * Q4K_BYTES), 0x00020000);
     const __amdgpu_buffer_rsrc_t rC = __builtin_amdgcn_make_buffer_rsrc((void*)codes, (short)0,
-                                                                         (int)((int64_t)K * Npad * 2), 0x00020000);
+                                                                         (int)((int64_t)K * Npad), 0x00020000);
     const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc((void*)scl, (short)0,
                                                                          (int)((int64_t)(K / 32) * Npad * 4), 0x00020000);
-    int voA[2], voB[4], voS[2];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {                    // 128 rows x 64 code bytes; rows past M re-read the last row
-        const int idx = i * MMQ_THREADS + t, row = idx >> 2, piece = idx & 3;
-        voA[i] = min(row0 + row, M - 1) * nb * Q4K_BYTES + 16 + 16 * piece;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {                    // 64 tokens x 128 fp16 codes
-        const int idx = i * MMQ_THREADS + t, tok = idx >> 4, piece = idx & 15;
-        voB[i] = (col0 + tok) * 512 + 16 * piece;
-    }
+    // this lane's row (rows past M re-read the last row): code bytes 16g..
+    // of each 32-byte pair, and the 16-byte block header
+    const int voRow = min(row0 + arow, M - 1) * nb * Q4K_BYTES;
+    // DMA slots: slot q (16 B) of the codes region is written by lane q % 64 of
+    // wave q / 64 (two instructions per wave); the scale words go as 4-byte
+    // slots, 64 per wave
+    int voB[2];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-        const int e = i * MMQ_THREADS + t, j = e / TN, tok = e % TN;
-        voS[i] = (j * Npad + col0 + tok) * 4;
+        const int q = (2 * w + i) * 64 + l;
+        const int tok = q >> 3, pos = q & 7;
+        voB[i] = (col0 + tok) * 256 + 16 * (pos ^ swz_b(tok));
     }
-    const int voH = min(row0 + (t & (TM - 1)), M - 1) * nb * Q4K_BYTES;
+    const int voS = ((w * 64 + l) / TN * Npad + col0 + (w * 64 + l) % TN) * 4;   // word (jl, tok) of the stage
 
-    struct Stage { u32x4m a[2], b[4]; };
-    Stage R0, R1;                                    // staging registers of even / odd stages
-    u32x4m rh = u32x4m{};
-    uint32_t rs[2] = {0u, 0u};
-    auto fetch = [&](Stage& R, int k) {
+    auto issue_b = [&](int k) {                        // 3 DMA instructions per wave
+        uint8_t* st = smem + (k % NRING) * ST_BYTES;
         const int b = k >> 1, s = k & 1;
 #pragma unroll
-        for (int i = 0; i < 2; i++) R.a[i] = __builtin_amdgcn_raw_buffer_load_b128(rW, voA[i], b * Q4K_BYTES + 64 * s, 0);
-#pragma unroll
-        for (int i = 0; i < 4; i++) R.b[i] = __builtin_amdgcn_raw_buffer_load_b128(rC, voB[i], b * Npad * 512 + 256 * s, 0);
-        if (s == 0) {
-            rh = __builtin_amdgcn_raw_buffer_load_b128(rW, voH, b * Q4K_BYTES, 0);
-#pragma unroll
-            for (int i = 0; i < 2; i++) rs[i] = __builtin_amdgcn_raw_buffer_load_b32(rS, voS[i], b * 8 * Npad * 4, 0);
-        }
+        for (int i = 0; i < 2; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rC, (lds_void*)(st + (2 * w + i) * 1024), 16, voB[i],
+                                                     b * Npad * 256 + 128 * s, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rS, (lds_void*)(st + ST_B + w * 256), 4, voS,
+                                                 (b * 8 + 4 * s) * Npad * 4, 0, 0);
     };
-    auto commit = [&](const Stage& R, int k) {
-        const int s = k & 1, slot = (k >> 1) & 1;
+    // this lane's weight code bytes of stage k: pair 0 and pair 1 (16 B each)
+    auto load_a = [&](int k, u32x4m (&a)[2]) {
+        const int b = k >> 1, s = k & 1;
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int idx = i * MMQ_THREADS + t, row = idx >> 2, piece = idx & 3;
-            uint8_t* d = &sA[s][row * A4_STRIDE + 16 * piece];
-            *(u32x2m*)d = u32x2m{R.a[i].x, R.a[i].y};
-            *(u32x2m*)(d + 8) = u32x2m{R.a[i].z, R.a[i].w};
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int idx = i * MMQ_THREADS + t, tok = idx >> 4, piece = idx & 15;
-            *(u32x4m*)&sB[s][tok * B_STRIDE + 16 * piece] = R.b[i];
-        }
-        if (s == 0) {
-            if (t < TM) {   // per-row sub-block scales, rounded to half as the reference does
-                const float d = f16_bits_to_f32(rh.x & 0xFFFFu), dmin = f16_bits_to_f32(rh.x >> 16);
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    uint32_t sc, m;
-                    q4k_scale_min(rh.y, rh.z, rh.w, j, sc, m);
-                    sDA[slot][j * TM + t] = (_Float16)(d * (float)sc);
-                    sMA[slot][j * TM + t] = (_Float16)(-dmin * (float)m);
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < 2; i++) sS8[slot][i * MMQ_THREADS + t] = rs[i];
-        }
+        for (int pp = 0; pp < 2; pp++)
+            a[pp] = __builtin_amdgcn_raw_buffer_load_b128(rW, voRow + 16 + 16 * g, b * Q4K_BYTES + 64 * s + 32 * pp, 0);
     };
 
     f32x16m acc[2];
     acc[0] = f32x16m{};
     acc[1] = f32x16m{};
+    int b_c[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++) b_c[tt] = g ^ swz_b(32 * tt + li);   // B-read position = 2 * jl ^ b_c
 
-    auto compute = [&](int k) {
-        const int b = k >> 1, s = k & 1, slot = b & 1;
-        const uint8_t* A = sA[s];
-        const uint8_t* B = sB[s];
-        // four sub-blocks per stage; for each, both token tiles' MFMAs are
-        // issued together (two independent accumulation chains), and the B
-        // operands of the next sub-block are read from LDS before this one's
-        // fmas run
-        h8m Bn[2][2];
-        auto load_b = [&](int jl) {
-#pragma unroll
-            for (int tt = 0; tt < 2; tt++) {
-                const int btok = 32 * tt + li;
-                Bn[tt][0] = *(const h8m*)(B + btok * B_STRIDE + 64 * jl + 16 * g);
-                Bn[tt][1] = *(const h8m*)(B + btok * B_STRIDE + 64 * jl + 32 + 16 * g);
-            }
-        };
-        load_b(0);
-#pragma unroll 1
-        for (int pl = 0; pl < 2; pl++) {
-            // lane (row arow, g): code bytes 32pl + 8g .. +8 and 32pl + 16 + 8g .. +8 -- the
-            // K positions this lane feeds to the two K=16 MFMAs of sub-blocks 2p (low
-            // nibbles) and 2p+1 (high nibbles), p = 2s + pl
-            const u32x2m a0 = *(const u32x2m*)(A + arow * A4_STRIDE + 32 * pl + 8 * g);
-            const u32x2m a1 = *(const u32x2m*)(A + arow * A4_STRIDE + 32 * pl + 16 + 8 * g);
-#pragma unroll
-            for (int jj = 0; jj < 2; jj++) {
-                const int jl = 2 * pl + jj;              // sub-block within the stage
-                const int j = 4 * s + jl;                // sub-block within the super-block
-                const h8m A0 = jj ? nib_hi_h8(a0) : nib_lo_h8(a0);
-                const h8m A1 = jj ? nib_hi_h8(a1) : nib_lo_h8(a1);
-                h8m Bc[2][2];
-#pragma unroll
-                for (int tt = 0; tt < 2; tt++) { Bc[tt][0] = Bn[tt][0]; Bc[tt][1] = Bn[tt][1]; }
-                f32x16m C[2];
-#pragma unroll
-                for (int tt = 0; tt < 2; tt++) C[tt] = mfma16(A0, Bc[tt][0], f32x16m{});
-#pragma unroll
-                for (int tt = 0; tt < 2; tt++) C[tt] = mfma16(A1, Bc[tt][1], C[tt]);   // exact int32 dots of sub-block j
-                if (jl < 3) load_b(jl + 1);
-                if (OUT == 2) {
-#pragma unroll
-                    for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-                        for (int v = 0; v < 16; v++) {
-                            const int r = row0 + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3);
-                            const int tok = col0 + 32 * tt + li;
-                            if (r < M && tok < N)
-                                ((int*)y)[((int64_t)tok * M + r) * (K / 32) + b * 8 + j] = (int)C[tt][v];
-                        }
-                } else {
-                    // scale outer products: K slot 0 only (lanes g = 1 hold zeros); every
-                    // lane loads, the g = 1 lanes then drop the value (no branch)
-                    const uint32_t da_bits = (uint32_t)__builtin_bit_cast(uint16_t, sDA[slot][j * TM + arow]) & gmask;
-                    const h8m As = __builtin_bit_cast(h8m, u32x4m{da_bits, 0u, 0u, 0u});
-                    f32x16m S[2];
-#pragma unroll
-                    for (int tt = 0; tt < 2; tt++) {
-                        const uint32_t d8_bits = sS8[slot][j * TN + 32 * tt + li] & gmask;
-                        S[tt] = mfma16(As, __builtin_bit_cast(h8m, u32x4m{d8_bits, 0u, 0u, 0u}), f32x16m{});
-                    }
-#pragma unroll
-                    for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-                        for (int v = 0; v < 16; v++) acc[tt][v] = __builtin_fmaf(C[tt][v], S[tt][v], acc[tt][v]);
-                }
-            }
+    // Scale operands of the current super-block: lane (row, g) holds
+    // half(d*sc_j) and half(-dmin*m_j) of its row for the sub-blocks j = 4g ..
+    // 4g+3 in the K slots of a K = 8 f16 MFMA operand.  The scale product of
+    // sub-block j is the MFMA of that operand with d8_j of each token in slot
+    // j (zeros elsewhere); the min term of a stage is one MFMA with the
+    // stage's four sum x_j in their slots.
+    h4m As = h4m{}, Am = h4m{};
+    auto scales = [&](const u32x4m hdr) {
+        const float d = f16_bits_to_f32(hdr.x & 0xFFFFu), dmin = f16_bits_to_f32(hdr.x >> 16);
+        // the 6-bit (sc, m) of sub-blocks 4g .. 4g+3, one per byte (get_scale_min_k4 layout)
+        uint32_t SC, MM;
+        if (g == 0) {
+            SC = hdr.y & 0x3F3F3F3Fu;
+            MM = hdr.z & 0x3F3F3F3Fu;
+        } else {
+            SC = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+            MM = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
         }
-        if (OUT != 2 && s == 1) {
-            // min term of the whole super-block: K = 8 sub-blocks on one MFMA per tile
-            h4m Am;
 #pragma unroll
-            for (int e = 0; e < 4; e++) Am[e] = sMA[slot][(4 * g + e) * TM + arow];
+        for (int q = 0; q < 4; q++) {
+            As[q] = (_Float16)(d * (float)((SC >> (8 * q)) & 0xFFu));     // half(d*sc), as the reference rounds it
+            Am[q] = (_Float16)(-dmin * (float)((MM >> (8 * q)) & 0xFFu));
+        }
+    };
+
+    auto compute = [&](int k, const u32x4m (&a)[2]) {
+        const uint8_t* st = smem + (k % NRING) * ST_BYTES;
+        const int b = k >> 1, s = k & 1;
+        const uint32_t* sS = (const uint32_t*)(st + ST_B);
+        const bool mine = g == s;                      // this lane group's K slots belong to the stage
+        uint32_t sw[2][4];
+        i32x4 Bv[2];
+        auto read_b = [&](int jl) {
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++)
+                Bv[tt] = *(const i32x4*)(st + (32 * tt + li) * 128 + 16 * ((2 * jl) ^ b_c[tt]));
+        };
+        read_b(0);
+#pragma unroll
+        for (int jl = 0; jl < 4; jl++) {
+            const int j = 4 * s + jl;
+            const u32x4m araw = a[jl >> 1];            // low nibbles: sub-block 2p, high: 2p+1
+            const i32x4 Ai = __builtin_bit_cast(i32x4, (jl & 1) ? ((araw >> 4u) & 0x0F0F0F0Fu) : (araw & 0x0F0F0F0Fu));
+            i32x16 C[2];
+            f32x16m S[2];
 #pragma unroll
             for (int tt = 0; tt < 2; tt++) {
-                const int btok = 32 * tt + li;
-                h4m Bm;
+                if (OUT != 2) {
+                    sw[tt][jl] = sS[jl * TN + 32 * tt + li];               // half d8 | half sum x << 16
+                    // d8 in K slot jl of this lane group's four (the stage's), zeros elsewhere
+                    const uint32_t dv = (jl & 1) ? (sw[tt][jl] << 16) : (sw[tt][jl] & 0xFFFFu);
+                    u32x2m bs = u32x2m{0u, 0u};
+                    if (jl < 2) bs.x = mine ? dv : 0u;
+                    else        bs.y = mine ? dv : 0u;
+                    S[tt] = __builtin_amdgcn_mfma_f32_32x32x8f16(As, __builtin_bit_cast(h4m, bs), f32x16m{}, 0, 0, 0);
+                }
+                C[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Ai, Bv[tt], i32x16{}, 0, 0, 0);
+            }
+            if (jl < 3) read_b(jl + 1);
+            if (OUT == 2) {
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    Bm[e] = __builtin_bit_cast(_Float16, (uint16_t)(sS8[slot][(4 * g + e) * TN + btok] >> 16));
-                acc[tt] = __builtin_amdgcn_mfma_f32_32x32x8f16(Am, Bm, acc[tt], 0, 0, 0);
+                for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) {
+                        const int r = row0 + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3);
+                        const int col = col0 + 32 * tt + li;
+                        if (r < M && col < N) ((int*)y)[((int64_t)col * M + r) * (K / 32) + b * 8 + j] = C[tt][v];
+                    }
+            } else {
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) acc[tt][v] = __builtin_fmaf(S[tt][v], (float)C[tt][v], acc[tt][v]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (OUT != 2) {
+            // min term of the stage's four sub-blocks: sum_j half(-dmin*m_j) * sum x_j
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++) {
+                u32x2m bm;
+                bm.x = mine ? ((sw[tt][0] >> 16) | (sw[tt][1] & 0xFFFF0000u)) : 0u;
+                bm.y = mine ? ((sw[tt][2] >> 16) | (sw[tt][3] & 0xFFFF0000u)) : 0u;
+                acc[tt] = __builtin_amdgcn_mfma_f32_32x32x8f16(Am, __builtin_bit_cast(h4m, bm), acc[tt], 0, 0, 0);
             }
         }
     };
 
-    // stages come in pairs (s = 0, 1); each stage's loads are issued two stages
-    // before it is written to LDS
-    fetch(R0, k0);
-    fetch(R1, k0 + 1);
-    commit(R0, k0);
-    __syncthreads();
+    // Stage pipeline (k0 is even, k1 - k0 is even): per iteration, the next
+    // stage's weight bytes (+ header) into registers, then stage k+2's
+    // activation DMA, then stage k from registers and LDS.  The loads of a
+    // wave complete in issue order, so waiting until only the newest 3 (the
+    // DMA of stage k+2) are outstanding means stage k+1's weights and DMA have
+    // landed; a plain s_barrier (no memory fence: a fence would wait for the
+    // stage k+2 DMA too) then makes every wave's copy visible, and it also
+    // orders every wave's reads of the buffer that the next DMA overwrites.
+    // Past the last stage the loads repeat the last stage (in bounds, into a
+    // ring slot nobody reads), so every iteration has the same load count
+    // and the waits are unconditional.
+    u32x4m a0[2], a1[2];
+    u32x4m hdr = __builtin_amdgcn_raw_buffer_load_b128(rW, voRow, (k0 >> 1) * Q4K_BYTES, 0);
+    load_a(k0, a0);
+    issue_b(k0);
+    issue_b(k0 + 1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);                // everything of stage k0 (and k0+1's DMA)
+    __builtin_amdgcn_s_barrier();
 #pragma unroll 1
     for (int k = k0; k < k1; k += 2) {
-        if (k + 2 < k1) fetch(R0, k + 2);
-        compute(k);
-        commit(R1, k + 1);
-        __syncthreads();
-        if (k + 3 < k1) fetch(R1, k + 3);
-        compute(k + 1);
-        if (k + 2 < k1) commit(R0, k + 2);
-        __syncthreads();
+        const int kl = k1 - 1;                         // last stage
+        // even stage k: first half of super-block k/2
+        if (OUT != 2) scales(hdr);
+        load_a(k + 1, a1);
+        __builtin_amdgcn_sched_barrier(0);             // keep the DMA the newest loads
+        issue_b(min(k + 2, kl));
+        compute(k, a0);
+        __builtin_amdgcn_s_waitcnt(0x0F73);            // vmcnt(3): all but stage k+2's DMA
+        __builtin_amdgcn_s_barrier();
+        // odd stage k+1
+        hdr = __builtin_amdgcn_raw_buffer_load_b128(rW, voRow, (min(k + 2, kl) >> 1) * Q4K_BYTES, 0);
+        load_a(min(k + 2, kl), a0);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_b(min(k + 3, kl));
+        compute(k + 1, a1);
+        __builtin_amdgcn_s_waitcnt(0x0F73);
+        __builtin_amdgcn_s_barrier();
     }
     if (OUT == 2) return;
 #pragma unroll
@@ -627,7 +665,7 @@ void mmq_q6k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const u
     }
 }
 
-hipError_t mmq_launch(void* y, const uint8_t* W, int type, const uint16_t* codes, const uint32_t* scl, int M, int N,
+hipError_t mmq_launch(void* y, const uint8_t* W, int type, const void* codes, const uint32_t* scl, int M, int N,
                       int K, int Npad, int out_kind, int splits, hipStream_t st) {
     const int tiles = ((M + TM - 1) / TM) * (Npad / TN);
     const int nb = K / QK_K;
@@ -639,13 +677,15 @@ hipError_t mmq_launch(void* y, const uint8_t* W, int type, const uint16_t* codes
         for (int i = 0; i < 3; i++) { sg.W[i] = W; sg.y[i] = y; sg.M[i] = i == 0 ? M : 0; }
         sg.rt0[0] = 0;
         for (int i = 1; i < 4; i++) sg.rt0[i] = (M + TM - 1) / TM;
-        if (out_kind == 0) hipLaunchKernelGGL(mmq_q4k_kernel<0>, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, sps);
-        else if (out_kind == 1) hipLaunchKernelGGL(mmq_q4k_kernel<1>, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, sps);
-        else hipLaunchKernelGGL(mmq_q4k_kernel<2>, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, sps);
+        const uint8_t* c8 = (const uint8_t*)codes;
+        if (out_kind == 0) hipLaunchKernelGGL(mmq_q4k_kernel<0>, grid, dim3(MMQ_THREADS), 0, st, sg, c8, scl, N, K, Npad, sps);
+        else if (out_kind == 1) hipLaunchKernelGGL(mmq_q4k_kernel<1>, grid, dim3(MMQ_THREADS), 0, st, sg, c8, scl, N, K, Npad, sps);
+        else hipLaunchKernelGGL(mmq_q4k_kernel<2>, grid, dim3(MMQ_THREADS), 0, st, sg, c8, scl, N, K, Npad, sps);
     } else {
-        if (out_kind == 0) hipLaunchKernelGGL(mmq_q6k_kernel<0>, grid, dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad, sps);
-        else if (out_kind == 1) hipLaunchKernelGGL(mmq_q6k_kernel<1>, grid, dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad, sps);
-        else hipLaunchKernelGGL(mmq_q6k_kernel<2>, grid, dim3(MMQ_THREADS), 0, st, y, W, codes, scl, M, N, K, Npad, sps);
+        const uint16_t* c16 = (const uint16_t*)codes;
+        if (out_kind == 0) hipLaunchKernelGGL(mmq_q6k_kernel<0>, grid, dim3(MMQ_THREADS), 0, st, y, W, c16, scl, M, N, K, Npad, sps);
+        else if (out_kind == 1) hipLaunchKernelGGL(mmq_q6k_kernel<1>, grid, dim3(MMQ_THREADS), 0, st, y, W, c16, scl, M, N, K, Npad, sps);
+        else hipLaunchKernelGGL(mmq_q6k_kernel<2>, grid, dim3(MMQ_THREADS), 0, st, y, W, c16, scl, M, N, K, Npad, sps);
     }
     return hipGetLastError();
 }
@@ -699,7 +739,7 @@ hipError_t splitk_reduce_launch(void* y, const float* ws, int64_t n, int splits,
     return hipGetLastError();
 }
 
-hipError_t mmq_q4k_multi_launch(const uint8_t* const* W, void* const* y, const int* M, int nseg, const uint16_t* codes,
+hipError_t mmq_q4k_multi_launch(const uint8_t* const* W, void* const* y, const int* M, int nseg, const uint8_t* codes,
                                 const uint32_t* scl, int N, int K, int Npad, hipStream_t st) {
     if (nseg < 1 || nseg > 3) return hipErrorInvalidValue;
     MmqSegs sg;

@@ -33,6 +33,7 @@ SIGNATURES = {
     "jllm_hip_gemv_quant_triple_rmsnorm": (I, [P, P, I, I, P, P, I, I, P, P, I, I, P, P, I, F, I, P]),
     "jllm_hip_gemv_quant_pair_rmsnorm": (I, [P, P, I, I, P, P, I, I, P, P, I, F, I, P]),
     "jllm_hip_quantize_mmq_f16": (I, [P, P, P, I, I, I, I, P]),
+    "jllm_hip_quantize_mmq_i8": (I, [P, P, P, I, I, I, I, P]),
     "jllm_hip_gemv_quant_pair_swiglu": (I, [P, P, I, P, I, I, P, I, P]),
     "jllm_hip_gemv_quant_pair_rmsnorm_swiglu": (I, [P, P, I, P, I, I, P, P, I, F, I, P]),
     "jllm_hip_gemv_quant_f32_rmsnorm": (I, [P, P, I, P, P, I, F, I, I, P]),

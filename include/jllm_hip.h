@@ -172,6 +172,12 @@ int jllm_hip_quantize_mmq_q8_1(const uint16_t* x, void* q8, int N, int K, int Np
 int jllm_hip_quantize_mmq_f16(const uint16_t* x, uint16_t* codes, uint32_t* scales, int N, int K, int Npad, int ds4,
                               void* stream);
 
+/* The same quantiser writing int8 codes [K/256][Npad][256] (the Q4_K MMQ
+ * kernel's layout; same codes and scale words).  No reference counterpart;
+ * exposed so the layout can be checked against the reference quantiser. */
+int jllm_hip_quantize_mmq_i8(const uint16_t* x, int8_t* codes, uint32_t* scales, int N, int K, int Npad, int ds4,
+                             void* stream);
+
 /* Test hook: the exact sub-block dots the production MMQ kernels form,
  * out [N][M][K/G] int32 (G = 32 for Q4_K sub-blocks, 16 for Q6_K groups),
  * for activations x [N x K] quantised by the production quantiser.  No

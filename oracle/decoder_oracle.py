@@ -150,3 +150,35 @@ class OracleDecoder:
         for i in range(1, n_gen):
             out.append(self.step(out[-1], len(prompt) + i - 1))
         return out
+
+
+class perturbed_matmuls:
+    """Context manager: every matmul output of the oracle (MMQ, MMVQ, float
+    GEMV) is multiplied by (1 + rel * N(0, 1)) -- the size of the fp32
+    summation-order differences between two correct implementations.  Used to
+    measure how far the decoder's logits move under such differences (the
+    int8 KV and q8 activation codes flip on ulp-level changes, and layers
+    amplify the flips), which sets the parity bar of long generations."""
+
+    NAMES = ("mmq", "mmvq", "gemv_quant_cpu")
+
+    def __init__(self, seed, rel=1e-6):
+        self.rng = np.random.default_rng(seed)
+        self.rel = rel
+        self.saved = {}
+
+    def __enter__(self):
+        for name in self.NAMES:
+            fn = getattr(oracle, name)
+            self.saved[name] = fn
+
+            def wrapped(*a, _fn=fn, **kw):
+                y = _fn(*a, **kw)
+                return (y * (1.0 + self.rel * self.rng.standard_normal(y.shape))).astype(np.float32)
+            setattr(oracle, name, wrapped)
+        return self
+
+    def __exit__(self, *exc):
+        for name, fn in self.saved.items():
+            setattr(oracle, name, fn)
+        return False

@@ -2,13 +2,19 @@
 Q5_K_M-style models run through the C ABI against the CPU restatement of the reference
 engine's layer order (oracle/decoder_oracle.py).
 
-Bars: the greedy tokens of a free-running generation are identical to the
-oracle's; with the oracle's tokens fed back (teacher forcing) every step's
-fp32 logits are within 1e-2 * max|logits| of the oracle's -- the fp16
-activations of ~15 rounded stages per layer may differ by an ulp here and
-there, as each kernel's own parity test allows; the chunked prefill and
-the one-call generate() are bit-identical to the plain prefill / steps.
+Bars: with the oracle's tokens fed back (teacher forcing) every step's fp32
+logits are within max(1e-2, 2 x envelope) * max|logits| of the oracle's,
+where the envelope is how far the oracle's own logits move when 1e-6
+relative noise (fp32 summation-order size) is put on its matmul outputs --
+the int8 KV and q8 activation codes flip on ulp-level differences and the
+layers amplify the flips, ~0 for short prompts, ~2 % for a 300-token one;
+the greedy tokens of a free-running generation are identical to the
+oracle's up to the first position whose top-2 margin is under that bar;
+the chunked prefill and the one-call generate() are bit-identical to the
+plain prefill / steps.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -35,31 +41,67 @@ def _rel(got, want):
     return float(np.abs(got - want).max() / np.abs(want).max())
 
 
+def _envelope(shape, model, prompt, tokens, max_seq):
+    """Largest logit deviation / max|logits| of the oracle itself under
+    1e-6 relative noise on its matmul outputs, teacher-forced with `tokens`
+    (the generation is chaotic: see decoder_oracle.perturbed_matmuls)."""
+    base, pert = decoder_oracle.OracleDecoder(shape, model, max_seq), decoder_oracle.OracleDecoder(shape, model, max_seq)
+    base.prefill(list(prompt))
+    with decoder_oracle.perturbed_matmuls(seed=len(prompt)):
+        pert.prefill(list(prompt))
+    env = [_rel(pert.logits, base.logits)]
+    for i in range(1, len(tokens)):
+        base.step(tokens[i - 1], len(prompt) + i - 1)
+        with decoder_oracle.perturbed_matmuls(seed=len(prompt) + i):
+            pert.step(tokens[i - 1], len(prompt) + i - 1)
+        env.append(_rel(pert.logits, base.logits))
+    return max(env)
+
+
+# (WIDE, 300 tokens): the prefill's gate/up GEMMs run as one multi-product
+# launch (>= 384 tiles) and the decode steps use multi-split attention
 @pytest.mark.parametrize("shape,n_prompt,n_gen,seed,preset", [(TINY, 20, 8, 1, "q4km"), (TINY, 1, 4, 2, "q4km"),
                                                                (WIDE, 6, 3, 3, "q4km"), (TINY, 20, 6, 4, "q5km"),
-                                                               (WIDE, 5, 3, 5, "q5km")])
+                                                               (WIDE, 5, 3, 5, "q5km"), (WIDE, 300, 4, 6, "q4km")])
 def test_decoder_vs_oracle(dev, shape, n_prompt, n_gen, seed, preset):
+    """Logit bar: max(1e-2, 2 x the oracle's own deviation under 1e-6
+    matmul noise) x max|logits| -- for short prompts the envelope is ~0 and
+    the bar is 1e-2; a 300-token prompt moves the oracle itself by ~2 %.
+    Greedy tokens: the oracle's wherever its top-2 margin exceeds the bar."""
     print_case("decoder", shape.hidden_dim, shape.n_layers, n_prompt, n_gen, preset)
+    import oracle
+    oracle.set_threads(min(16, os.cpu_count() or 1))
     model = decoder.synth_np(shape, seed, preset)
     prompt = synth.rng(seed + 100).integers(0, shape.vocab_size, n_prompt).astype(np.int32)
     max_seq = n_prompt + n_gen
     orc = decoder_oracle.OracleDecoder(shape, model, max_seq)
-    dm = decoder.to_device(model, dev)
-    gpu = decoder.Decoder(shape, dm, max_seq, max_batch=64)
-    out = torch.zeros(1, dtype=torch.int32, device=dev)
-    # teacher-forced: the oracle's token drives both
-    want_tok = [orc.prefill(list(prompt))]
-    gpu.prefill(_tok(prompt, dev), 0, out)
-    assert _rel(from_dev(gpu.logits()), orc.logits) <= TOL
+    want_tok, want_logits = [orc.prefill(list(prompt))], [orc.logits.copy()]
     for i in range(1, n_gen):
         want_tok.append(orc.step(want_tok[-1], n_prompt + i - 1))
-        gpu.step(_tok([want_tok[-2]], dev), n_prompt + i - 1, out)
-        assert _rel(from_dev(gpu.logits()), orc.logits) <= TOL, i
-    # free-running greedy generation on the device: identical tokens
-    gpu2 = decoder.Decoder(shape, dm, max_seq, max_batch=64)
+        want_logits.append(orc.logits.copy())
+    bar = max(TOL, 2.0 * _envelope(shape, model, prompt, want_tok, max_seq))
+    dm = decoder.to_device(model, dev)
+    gpu = decoder.Decoder(shape, dm, max_seq, max_batch=512)
+    out = torch.zeros(1, dtype=torch.int32, device=dev)
+    # teacher-forced: the oracle's token drives both
+    tie = n_gen
+    for i in range(n_gen):
+        if i == 0:
+            gpu.prefill(_tok(prompt, dev), 0, out)
+        else:
+            gpu.step(_tok([want_tok[i - 1]], dev), n_prompt + i - 1, out)
+        lg, w = from_dev(gpu.logits()), want_logits[i]
+        assert _rel(lg, w) <= bar, (i, _rel(lg, w), bar)
+        top2 = np.sort(w)[-2:]
+        if top2[1] - top2[0] > bar * np.abs(w).max():
+            assert int(np.argmax(lg)) == want_tok[i], i
+        else:
+            tie = min(tie, i)
+    # free-running greedy generation on the device: identical tokens up to a near-tie
+    gpu2 = decoder.Decoder(shape, dm, max_seq, max_batch=512)
     gen = torch.zeros(n_gen, dtype=torch.int32, device=dev)
     gpu2.generate(_tok(prompt, dev), n_gen, gen)
-    assert from_dev(gen).tolist() == want_tok
+    assert from_dev(gen).tolist()[:tie] == want_tok[:tie]
     gpu.close()
     gpu2.close()
 

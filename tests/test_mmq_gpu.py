@@ -62,6 +62,25 @@ def test_kernel_layout_quantizer_matches_reference_layout(dev, ds4, N, K):
     assert np.array_equal(sw, want_s)
 
 
+@pytest.mark.parametrize("N,K", [(64, 256), (70, 2560), (1, 512)])
+def test_quantize_mmq_i8_layout_bit_exact(dev, N, K):
+    """The Q4_K kernel's int8 code layout [K/256][Npad][256] holds the
+    reference quantiser's codes, and the same DS4 scale words."""
+    print_case("quantize_mmq_i8", N, K)
+    x = synth.x_f16(synth.rng(N + K + 7), (N, K))
+    x[0, 32:64] = 0
+    Npad = _npad(N)
+    codes = torch.zeros(K * Npad, dtype=torch.int8, device=dev)
+    scl = torch.zeros(K // 32 * Npad, dtype=torch.int32, device=dev)
+    jllm.call("jllm_hip_quantize_mmq_i8", to_dev(x), codes, scl, N, K, Npad, 1)
+    c = from_dev(codes).reshape(K // 256, Npad, 256)
+    sw = from_dev(scl).view(np.uint32).reshape(K // 32, Npad)
+    ref = oracle.quantize_mmq(x, N, K, Npad, True).reshape(K // 128, Npad, 144)
+    rq = ref[:, :, 16:].view(np.int8)
+    assert np.array_equal(c, rq.reshape(K // 256, 2, Npad, 128).transpose(0, 2, 1, 3).reshape(K // 256, Npad, 256))
+    assert np.array_equal(sw, ref[:, :, 0:16].copy().view(np.uint32).transpose(0, 2, 1).reshape(K // 32, Npad))
+
+
 @pytest.mark.parametrize("t", [12, 14])
 @pytest.mark.parametrize("M,N,K", [(128, 64, 256), (200, 70, 512), (33, 5, 2560), (64, 129, 768)])
 def test_mmq_int32_dots_bit_exact(dev, t, M, N, K):
