@@ -3,11 +3,44 @@
 #include "capi_common.h"
 #include "attention.h"
 #include "convert.h"
+#include <mutex>
 
 using namespace jllm_hip;
 
+// Split-K partials of the allocation-free decode entry point: a fixed
+// per-device array, held by each GPU the library runs on until the process
+// ends.  Host code never uses its name as an address (that is a host-side
+// stand-in): the device address comes from hipGetSymbolAddress, once per
+// device, and only that address is passed to kernels.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)4 << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
 namespace {
 DeviceScratch g_part;    // split-K partials + counters, grown on demand (zeroed), never freed
+
+constexpr int NOALLOC_MAX_DEV = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[NOALLOC_MAX_DEV] = {};
+
+// the device address of `scratch` on the current device (looked up on the
+// first call per device); nullptr on failure
+void* noalloc_scratch() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEV) return nullptr;
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            fprintf(stderr, "[attention] hipGetSymbolAddress(scratch) failed on device %d: %s\n", dev,
+                    hipGetErrorString(e));
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        g_noalloc_ptr[dev] = p;
+    }
+    return g_noalloc_ptr[dev];
+}
 
 int attn_check(const void* out, const void* q, const void* k, const void* v, int n_heads, int n_kv, int hd,
                int chd, int seq, int kv_int8, int window) {
@@ -88,6 +121,26 @@ int jllm_hip_flash_attention_decode_dyn(uint16_t* out, const uint16_t* q, const 
     if (!d_pos) return JLLM_ERR_INVALID;
     return attn_run(out, q, k, v, n_heads, n_kv_heads, head_dim, cache_head_dim, 0, scale, kv_int8, k_scales,
                     v_scales, window, n_splits, stream, d_pos);
+}
+
+int jllm_hip_flash_attention_decode_noalloc(uint16_t* out, const uint16_t* q, const void* k, const void* v,
+                                            int n_heads, int n_kv_heads, int head_dim, int cache_head_dim,
+                                            int seq_len, float scale, int kv_int8, const float* k_scales,
+                                            const float* v_scales, int window, void* stream) {
+    const int n_splits = attn_splits(seq_len, n_kv_heads);
+    if (n_heads > 0 && head_dim > 0 &&
+        attn_partials_floats(n_heads, n_splits, head_dim) * sizeof(float) > NOALLOC_SCRATCH_BYTES) {
+        fprintf(stderr, "[attention] decode_noalloc: %d heads x %d splits x (2 + %d) floats exceed the %zu-byte "
+                        "static partials buffer\n", n_heads, n_splits, head_dim, NOALLOC_SCRATCH_BYTES);
+        return JLLM_ERR_INVALID;
+    }
+    // argument errors first, so that no device state is touched for them
+    int st = attn_check(out, q, k, v, n_heads, n_kv_heads, head_dim, cache_head_dim, seq_len, kv_int8, window);
+    if (st) return st;
+    float* part = (float*)noalloc_scratch();
+    if (!part) return JLLM_ERR_LAUNCH;
+    return attn_run(out, q, k, v, n_heads, n_kv_heads, head_dim, cache_head_dim, seq_len, scale, kv_int8, k_scales,
+                    v_scales, window, n_splits, stream, nullptr, part);
 }
 
 int jllm_hip_flash_attention_prefill_batched(uint16_t* out, const uint16_t* q, const void* k, const void* v,

@@ -45,6 +45,7 @@ SIGNATURES = {
     "jllm_hip_flash_attention_decode": (I, [P, P, P, P, I, I, I, I, I, F, I, P, P, I, P]),
     "jllm_hip_flash_attention_decode_splits": (I, [P, P, P, P, I, I, I, I, I, F, I, P, P, I, I, P]),
     "jllm_hip_flash_attention_decode_dyn": (I, [P, P, P, P, I, I, I, I, P, F, I, P, P, I, I, P]),
+    "jllm_hip_flash_attention_decode_noalloc": (I, [P, P, P, P, I, I, I, I, I, F, I, P, P, I, P]),
     "jllm_hip_decode_attn_splits": (I, [I]),
     "jllm_hip_get_splitk_partials": (P, [I, I, I]),
     "jllm_hip_fp16_to_int8": (I, [P, P, P, I, I, P]),

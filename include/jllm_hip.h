@@ -224,6 +224,22 @@ int jllm_hip_flash_attention_decode_dyn(uint16_t* out, const uint16_t* q, const 
                                         const int32_t* d_pos, float scale, int kv_int8, const float* k_scales,
                                         const float* v_scales, int window, int n_splits, void* stream);
 
+/* Allocation-free decode attention.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The same kernels
+ * and split policy as jllm_hip_flash_attention_decode, but the split-K
+ * partials live in a fixed 4 MiB array per device (allocated with the
+ * library's code object, held until the process ends) instead of the
+ * grown-on-demand buffer; this call makes no hipMalloc / hipFree.
+ * n_heads * splits * (2 + head_dim) * 4 bytes must fit in 4 MiB (32 heads of
+ * 128 at the 128-split maximum need 2.1 MiB), else JLLM_ERR_INVALID.  Every
+ * call on a device shares that device's array: calls that overlap on one
+ * GPU (several streams) race. */
+int jllm_hip_flash_attention_decode_noalloc(uint16_t* out, const uint16_t* q, const void* k, const void* v,
+                                            int n_heads, int n_kv_heads, int head_dim, int cache_head_dim,
+                                            int seq_len, float scale, int kv_int8, const float* k_scales,
+                                            const float* v_scales, int window, void* stream);
+
 /* Split-count policy and partials buffer.  Replace decode_attn_splits and
  * get_splitk_partials, jllm_kernels.h:402-403 (attention.cu:975-1005).  The
  * MI355X policy is ceil(seq/32) splits capped at 128 (one wave per KV head
