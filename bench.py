@@ -48,7 +48,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--skip-extras", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -166,6 +166,8 @@ def main():
                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                        "bytes_per_launch": pair_bytes, "us_per_launch": round(us_launch, 3)}
 
+    stage("configs[0] single Q4_K GEMV")
+    out["gemv_q4k_9728x2560"] = bench_gemv_single(np, torch, jllm, synth, up, dev, g)
     if not args.skip_extras:
         stage("MMQ prefill GEMM")
         out["mmq"] = bench_mmq(np, torch, jllm, synth, up, dev, g)
@@ -192,6 +194,36 @@ def measured_traffic():
     return None
 
 
+def bench_gemv_single(np, torch, jllm, synth, up, dev, g):
+    """configs[0] on the GPU: one Q4_K 9728 x 2560 GEMV, fp16 x, fp32 y
+    (gemv_quant_f32, the int8 MMVQ path), 64 distinct weight copies (0.9 GB)
+    replayed from a graph so the weights stream from HBM.  Bytes per call =
+    14,008,320 (W) + 5,120 (x) + 38,912 (y)."""
+    M, K, copies = 9728, 2560, 64
+    W0 = up(synth.q4k(g, M, K))
+    Ws = [W0.clone() for _ in range(copies)]
+    x = up(synth.x_f16(g, K))
+    y = torch.empty(M, dtype=torch.float32, device=dev)
+    jllm.gemv_quant_f32(y, Ws[0], Q4, x, M, K)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        for W in Ws:
+            jllm.gemv_quant_f32(y, W, Q4, x, M, K)
+    gr.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        gr.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (5 * copies)
+    by = mat_bytes(Q4, M, K) + 2 * K + 4 * M
+    gbs = by / (us * 1e-6) / 1e9
+    del Ws
+    return {"us": round(us, 2), "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def bench_mmq(np, torch, jllm, synth, up, dev, g):
     """int8 MMQ, Q4_K 9728 x 2560 (and Q6_K 2560 x 9728) at N tokens; fp16 y
     (the reference's gemm_quant_batched).  Ops = 2*N*M*K; timed calls include the
@@ -216,18 +248,15 @@ def bench_mmq(np, torch, jllm, synth, up, dev, g):
             torch.cuda.synchronize()
             us = e0.elapsed_time(e1) * 1e3 / 10
             tops = 2.0 * N * M * K / (us * 1e-6) / 1e12
-            # algorithmic bytes: weights + the activation as q8_1 (36 B per 32) + fp16 y
-            nbytes = mat_bytes(t, M, K) + N * K * 36 // 32 + N * M * 2
-            gbs = nbytes / (us * 1e-6) / 1e9
             res[f"{'q4k' if t == 12 else 'q6k'}_M{M}_K{K}_N{N}"] = {
-                "us": round(us, 2), "TOPS": round(tops, 2), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
-                "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+                "us": round(us, 2), "TOPS": round(tops, 2), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
     return res
 
 
 def bench_attention(np, torch, jllm, synth, up, dev, g):
     """32 q heads / 8 KV heads, head_dim 128, INT8 KV with fp32 per-token
-    scales; 36 distinct layer caches per context so the KV streams from HBM.
+    scales; distinct caches totalling >= 256 MB per context (at least 36) so the KV
+    streams from HBM, not the Infinity Cache.
     Algorithmic bytes = ctx_eff * (2*8*128 + 2*8*4) + 16 KiB (q and out)."""
     H, KV, HD = 32, 8, 128
     res = {}
@@ -237,7 +266,10 @@ def bench_attention(np, torch, jllm, synth, up, dev, g):
         k0 = up(synth.kv_int8(g, ctx, KV, HD))
         v0 = up(synth.kv_int8(g, ctx, KV, HD))
         s0 = up(synth.kv_scales(g, ctx, KV))
-        caches = [(k0.clone(), v0.clone(), s0.clone(), s0.clone()) for _ in range(L)]
+        # >= 256 MB of distinct caches (the Infinity Cache holds 256 MB), at least 36
+        per_cache = ctx * (2 * KV * HD + 2 * KV * 4)
+        ncache = max(L, -(-(256 << 20) // per_cache))
+        caches = [(k0.clone(), v0.clone(), s0.clone(), s0.clone()) for _ in range(ncache)]
         jllm.call("jllm_hip_flash_attention_decode", out, q, *caches[0][:2], H, KV, HD, HD, ctx, 0.0884, 1,
                   caches[0][2], caches[0][3], window)
         gr = torch.cuda.CUDAGraph()
@@ -253,7 +285,7 @@ def bench_attention(np, torch, jllm, synth, up, dev, g):
             gr.replay()
         e1.record()
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / (5 * L)
+        us = e0.elapsed_time(e1) * 1e3 / (5 * ncache)
         eff = min(ctx, window) if window > 0 else ctx
         by = eff * (2 * KV * HD + 2 * KV * 4) + 2 * 8192
         res[f"ctx{ctx}_win{window}"] = {"us_per_call": round(us, 2), "GB/s": round(by / (us * 1e-6) / 1e9, 1),
@@ -262,19 +294,40 @@ def bench_attention(np, torch, jllm, synth, up, dev, g):
     return res
 
 
+def _golden_e2e(np):
+    """The committed oracle generation of configs[4] and the per-position
+    logit bars (tests/golden/make_e2e_golden.py, tests/test_e2e_full_gpu.py)."""
+    import importlib.util
+    gdir = os.path.join(ROOT, "tests", "golden")
+    spec = importlib.util.spec_from_file_location("make_e2e_golden", os.path.join(gdir, "make_e2e_golden.py"))
+    mk = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mk)
+    gold = np.load(os.path.join(gdir, "e2e_qwen3_4b.npz"))
+    env = np.maximum(np.load(os.path.join(gdir, "e2e_qwen3_4b_env1.npz"))["deviation"],
+                     np.load(os.path.join(gdir, "e2e_qwen3_4b_env2.npz"))["deviation"])
+    return mk, gold, env, np.maximum(1e-2 * gold["absmax"], 2.0 * env)
+
+
 def bench_e2e(np, torch, dev, n_prompt=512, n_gen=128):
     """random-init Qwen3-4B-shaped decoder in Q4_K_M layout (36 layers,
     Q6_K lm_head and every other ffn_down, fp32 norms ~ 1+N(0,0.02), RoPE base 1e6,
-    INT8 KV), a random 512-token prompt, then greedy decode to 128 tokens.  TTFT =
+    INT8 KV), the seeded 512-token prompt, then greedy decode to 128 tokens.  TTFT =
     prefill of the prompt + first-token sampling; decode tok/s over the remaining
-    127 steps.  Everything runs through the decoder's C ABI on one stream."""
+    127 steps.  Everything runs through the decoder's C ABI on one stream.  The
+    model and prompt are the ones of the committed oracle generation; after
+    the timed run an untimed teacher-forced pass must keep the logits within
+    the parity bars and the timed tokens must equal the oracle's up to the
+    first near-tie (top-2 margin within the oracle's own perturbation
+    envelope), or the bench fails.  Decode roofline: per token the weight
+    bytes (2,478,374,400 B) plus the INT8 KV read at the token's context
+    (36 layers x ctx x 2112 B) over the time per token."""
     import decoder
+    mk, gold, env, bars = _golden_e2e(np)
     shape = decoder.QWEN3_4B
-    model = decoder.synth_device(shape, 4242, dev)
+    model = decoder.to_device(decoder.synth_np(shape, int(gold["model_seed"])), dev)
     torch.cuda.synchronize()
     d = decoder.Decoder(shape, model, n_prompt + n_gen, max_batch=n_prompt)
-    prompt = torch.randint(0, shape.vocab_size, (n_prompt,), dtype=torch.int32, device=dev,
-                           generator=torch.Generator(device=dev).manual_seed(1))
+    prompt = torch.from_numpy(mk.prompt_ids(shape.vocab_size, n_prompt)).to(dev)
     toks = torch.zeros(n_gen, dtype=torch.int32, device=dev)
     d.generate(prompt, 8, toks)                                   # warm-up (code objects, allocations)
     torch.cuda.synchronize()
@@ -289,42 +342,108 @@ def bench_e2e(np, torch, dev, n_prompt=512, n_gen=128):
     ttft = ev[0].elapsed_time(ev[1])
     dec_ms = ev[1].elapsed_time(ev[2])
     gen = toks.cpu().numpy()
+    # untimed check: a teacher-forced pass (the oracle's tokens fed) measures
+    # the logit deviation at every position, which must stay within the
+    # parity bars; the timed tokens must equal the oracle's up to the first
+    # position whose top-2 margin is within the oracle's own envelope
+    gt = torch.tensor(gold["tokens"][:n_gen], dtype=torch.int32, device=dev)
+    one = torch.zeros(1, dtype=torch.int32, device=dev)
+    devs = []
+    for i in range(n_gen):
+        if i == 0:
+            d.prefill(prompt, 0, one)
+        else:
+            d.step(gt[i - 1:i], n_prompt + i - 1, one)
+        lg = d.logits().cpu().numpy()
+        devs.append(max(float(np.abs(lg[gold["sample_idx"]] - gold["sample"][i]).max()),
+                        float(np.abs(lg[gold["top_idx"][i]] - gold["top_val"][i]).max())))
+    devs = np.array(devs)
     d.close()
     del model
     torch.cuda.empty_cache()
+    over = np.nonzero(devs > bars[:n_gen])[0]
+    ties = np.nonzero(gold["margin"][:n_gen] <= env[:n_gen])[0]
+    t0 = int(ties[0]) if ties.size else n_gen
+    same = int(np.argmin(np.append(gen == gold["tokens"][:n_gen], False)))
+    if over.size or same < t0:
+        print(f"[bench] e2e parity failed: logit deviation over the bar at {over[:8].tolist()}; tokens equal "
+              f"for {same} positions, {t0} required", file=sys.stderr)
+        sys.exit(1)
+    weight_bytes = 36 * 42762240 + 18 * 20428800 + 18 * 14008320 + 319065600
+    kv_bytes = sum(36 * (n_prompt + i) * 2112 for i in range(1, n_gen))      # step i attends to n_prompt + i keys
+    dec_bytes = (n_gen - 1) * weight_bytes + kv_bytes
+    dec_gbs = dec_bytes / (dec_ms * 1e-3) / 1e9
     return {"workload": "configs[4]: Qwen3-4B-shaped Q4_K_M decoder, 36 layers, INT8 KV, prompt 512, "
                         "128 greedy tokens", "ttft_ms": round(ttft, 2),
             "prefill_tok_s": round(n_prompt / (ttft * 1e-3), 1),
             "decode_tok_s": round((n_gen - 1) / (dec_ms * 1e-3), 1),
             "decode_ms_per_token": round(dec_ms / (n_gen - 1), 3),
+            "decode_GB/s": round(dec_gbs, 1), "decode_hbm_frac": round(dec_gbs / HBM_PEAK_GBS, 4),
+            "tokens_equal_oracle": same, "first_near_tie": t0,
+            "max_logit_dev_frac": round(float((devs / gold["absmax"][:n_gen]).max()), 4),
             "distinct_tokens": int(len(set(gen.tolist()))), "first_tokens": gen[:8].tolist()}
+
+
+def _cgroup_cores():
+    """CPU cores this process may actually use: the cgroup v2 cpu.max quota
+    (quota / period, rounded down), None when unlimited or unreadable.  The
+    affinity mask (`nproc`) can list every core of the host while the
+    scheduler grants only the quota; more threads than that measure throttling."""
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, p = f.read().split()[:2]
+        return None if q == "max" else max(1, int(q) // int(p))
+    except (OSError, ValueError):
+        return None
 
 
 def cpu_baseline(np, synth, seconds):
     """The oracle's C restatement of the reference's host scalar path gemv_quant_cpu
-    (gemv_q4.cu:2519-2631) on configs[0] (Q4_K 9728 x 2560, fp16 x, fp32 y), on this
-    box's CPU: single thread (as the reference runs it), repeated for ~`seconds`."""
+    (gemv_q4.cu:2519-2631), on this box's CPU, in the metric's unit: the decode-step
+    GEMV set of configs[1] (every matrix shape of a layer and the lm_head, each timed
+    once; the step time is 36 x the layer's matrices + the lm_head), single thread
+    as the reference runs it, and with the rows split over every core the
+    process may use (the affinity mask, bounded by the cgroup CPU quota when one
+    is set; both reported).
+    Also configs[0] (Q4_K 9728 x 2560) repeated for ~`seconds`."""
     import oracle
     g = synth.rng(7)
+    nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    quota = _cgroup_cores()
+    threads = max(1, min(nproc, quota or nproc))
+    mats = {"q": (Q4, QD, HID), "k": (Q4, KVD, HID), "v": (Q4, KVD, HID), "o": (Q4, HID, QD),
+            "gate": (Q4, FFN, HID), "up": (Q4, FFN, HID), "down": (Q6, HID, FFN), "lm_head": (Q6, VOCAB, HID)}
+    per = {}
+    for name, (t, M, K) in mats.items():
+        W, x = synth.weights(g, t, M, K), synth.x_f16(g, K)
+        t0 = time.perf_counter()
+        oracle.gemv_quant_cpu(W, t, x, M, K)
+        t1 = time.perf_counter()
+        oracle.gemv_quant_cpu(W, t, x, M, K, threads=threads)
+        t2 = time.perf_counter()
+        per[name] = (mat_bytes(t, M, K) + 2 * K + 4 * M, t1 - t0, t2 - t1)
+        del W
+    layer = [n for n in mats if n != "lm_head"]
+    step_bytes = L * sum(per[n][0] for n in layer) + per["lm_head"][0]
+    step_1 = L * sum(per[n][1] for n in layer) + per["lm_head"][1]
+    step_m = L * sum(per[n][2] for n in layer) + per["lm_head"][2]
+    # configs[0]: one Q4_K 9728 x 2560 GEMV, single thread
     M, K = 9728, 2560
     W, x = synth.q4k(g, M, K), synth.x_f16(g, K)
     by = mat_bytes(Q4, M, K) + 2 * K + 4 * M
-    oracle.gemv_quant_cpu(W, Q4, x, M, K)
     calls, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < seconds:
         oracle.gemv_quant_cpu(W, Q4, x, M, K)
         calls += 1
     dt = (time.perf_counter() - t0) / calls
-    threads = min(16, os.cpu_count() or 1)
-    tm0, mcalls = time.perf_counter(), 0
-    while time.perf_counter() - tm0 < max(1.0, seconds / 4):
-        oracle.gemv_quant_cpu(W, Q4, x, M, K, threads=threads)
-        mcalls += 1
-    dtm = (time.perf_counter() - tm0) / mcalls
-    return {"value": round(by / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"configs[0] Q4_K GEMV 9728x2560 (14.05 MB/call), {calls} calls, {dt * 1e3:.1f} ms/call",
-            "all_cores": {"value": round(by / dtm / 1e9, 3), "unit": "GB/s", "cores": threads,
-                          "ms_per_call": round(dtm * 1e3, 2)}}
+    return {"value": round(step_bytes / step_1 / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": "configs[1] decode-step GEMV set: each matrix shape (q, k, v, o, gate, up, down, lm_head) "
+                      "run once; step = 36 x layer + lm_head (%.2f s single-thread per step)" % step_1,
+            "all_cores": {"value": round(step_bytes / step_m / 1e9, 3), "unit": "GB/s", "cores": threads,
+                          "nproc": nproc, "cgroup_cpu_quota_cores": quota, "step_s": round(step_m, 3)},
+            "per_matrix_ms_1core": {n: round(v[1] * 1e3, 2) for n, v in per.items()},
+            "configs0_q4k_9728x2560": {"value": round(by / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
+                                       "calls": calls, "ms_per_call": round(dt * 1e3, 2)}}
 
 
 if __name__ == "__main__":
