@@ -50,6 +50,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--skip-extras", action="store_true")
+    ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -178,7 +179,8 @@ def main():
         stage("end-to-end decoder")
         out["e2e"] = bench_e2e(np, torch, dev)
     stage("CPU baseline")
-    out["cpu_baseline"] = cpu_baseline(np, synth, args.cpu_seconds)
+    if not args.skip_cpu:
+        out["cpu_baseline"] = cpu_baseline(np, synth, args.cpu_seconds)
     print(json.dumps(out), flush=True)
 
 

@@ -758,18 +758,25 @@ int mmq_splits(int M, int N, int K) {
     const int64_t tiles = (int64_t)((M + TM - 1) / TM) * ((N + TN - 1) / TN);
     const int nb = K / QK_K;
     if (tiles >= MMQ_MULTI_MIN_TILES || nb < 4) return 1;
-    // ranges of whole super-blocks; pick the count that minimises (rounds of
-    // resident workgroups) x (super-blocks per range) -- 2 workgroups per CU
-    // on 256 CUs; e.g. 160 tiles with 38 super-blocks: 3 ranges (480
-    // workgroups, one round of 13) rather than 4 (640: two rounds of 10).
-    // Fewer ranges win ties (less partial traffic).
-    const int64_t slots = 512;
+    // Ranges of whole super-blocks, chosen by a cost model fitted on MI355X
+    // (Q4_K 9728 / 2560 / 1024 rows, K 2560 / 4096 / 9728, N 64-512): the
+    // kernel is VALU-bound per CU, so a launch takes about
+    //   4 us + g(w) x (super-blocks per range),
+    // w the most workgroups any CU holds (ceil(workgroups / 256); 3 fit at
+    // once), g(1, 2, 3) = 2.85, 4.56, 6.27 us per super-block, linear in w
+    // beyond (more rounds); split-K adds ~5 us (partials + reduce launch)
+    // and the fp32 partials' write and read at ~3 TB/s.  It picks the
+    // measured best count in every fitted case (e.g. N = 256: 1 range,
+    // 47 us, where "fill 512 slots" chose 5 ranges, 63 us).
+    auto g = [](int64_t w) { return w == 1 ? 2.85 : w == 2 ? 4.56 : 6.27 * (double)w / 3.0; };
     int best = 1;
-    int64_t best_cost = ((tiles + slots - 1) / slots) * nb;
-    for (int S = 2; S <= std::min(16, nb / 2); S++) {
+    double best_cost = 0.0;
+    for (int S = 1; S <= std::min(16, nb); S++) {
         const int sps = (nb + S - 1) / S, eff = (nb + sps - 1) / sps;
-        const int64_t cost = ((tiles * eff + slots - 1) / slots) * sps;
-        if (cost < best_cost) { best = eff; best_cost = cost; }
+        const int64_t w = (tiles * eff + 255) / 256;
+        double cost = 4.0 + g(w) * sps;
+        if (eff > 1) cost += 5.0 + (double)eff * N * M * 8.0 / 3.0e6;
+        if (S == 1 || cost < best_cost) { best = eff; best_cost = cost; }
     }
     return best;
 }

@@ -8,6 +8,9 @@
   copy  : a plain device-to-device copy of 256 MiB (calibrates FETCH_SIZE /
           WRITE_SIZE against a known byte count)
   mmq   : the Q4_K prefill GEMM 9728 x 2560 at N = 512 tokens (fp16 out), 5 calls
+  attn  : INT8-KV split-K decode attention (32 q / 8 KV heads, head_dim 128) at
+          ctx 8192 over 16 distinct caches (277 MB), 2 passes; then ctx 512
+          over 240 caches (263 MB), 2 passes
 """
 import os
 import sys
@@ -61,6 +64,20 @@ def main(mode):
         y = torch.empty(512 * 9728, dtype=torch.int16, device=dev)
         for _ in range(5):
             jllm.call("jllm_hip_gemm_quant_batched", y, W, 12, x, 9728, 512, 2560)
+    elif mode == "attn":
+        H, KV, HD = 32, 8, 128
+        q = up(synth.x_f16(g, H * HD))
+        out = torch.empty(H * HD, dtype=torch.int16, device=dev)
+        for ctx, n in ((8192, 16), (512, 240)):
+            k0, v0 = up(synth.kv_int8(g, ctx, KV, HD)), up(synth.kv_int8(g, ctx, KV, HD))
+            s0 = up(synth.kv_scales(g, ctx, KV))
+            caches = [(k0.clone(), v0.clone(), s0.clone()) for _ in range(n)]
+            for _ in range(2):
+                for k, v, s in caches:
+                    jllm.call("jllm_hip_flash_attention_decode", out, q, k, v, H, KV, HD, HD, ctx, 0.0884, 1,
+                              s, s, 0)
+            torch.cuda.synchronize()
+            del caches
     elif mode == "copy":
         a = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
         b = torch.empty_like(a)
