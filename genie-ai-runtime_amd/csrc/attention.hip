@@ -70,6 +70,15 @@ __device__ __forceinline__ h8 kv8_to_h8(const uint8_t* p) {
     }
 }
 
+#ifdef JLLM_ATTN_TRACE
+// probe builds only: per-wave timestamps (s_memrealtime, 100 MHz) of the last
+// decode launch: [start, first tile done, tiles done, partials issued]
+__device__ uint64_t g_attn_trace[8192 * 4];
+#define AT_MARK(i) do { tr[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define AT_MARK(i) do { } while (0)
+#endif
+
 int attn_splits(int seq_len, int n_kv) {
     // one wave per (KV head, split): at least 32 keys (one tile) per split,
     // at most 128 splits (measured on MI355X: short splits keep every SIMD
@@ -92,7 +101,7 @@ size_t attn_scratch_bytes(int n_heads, int n_splits, int head_dim) {
 __host__ __device__ size_t attn_wave_lds_bytes(int n_heads, int n_kv, int head_dim, int tq) {
     const int G = n_heads / n_kv * tq;                                // columns of a wave
     const size_t loop = (size_t)32 * AT_KEYS * 2 + 96 * 4;            // P' rows (fp16) + corr/ks/vs
-    const size_t outb = (size_t)2 * G * head_dim * 4;                 // final hi/lo rows (fp32)
+    const size_t outb = (size_t)((2 * G + 7) & ~7) * head_dim * 4;   // final hi/lo rows (fp32, >= 8 rows)
     return ((loop > outb ? loop : outb) + 15) & ~(size_t)15;
 }
 // a workgroup of W waves: W wave regions, then (m, l) of each wave's columns
@@ -131,6 +140,8 @@ void attn_partial_kernel(AttnArgs a) {
     const int wv = MT ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
     const size_t wave_lds = attn_wave_lds_bytes(a.n_heads, a.n_kv, a.head_dim, a.tq);
     uint8_t* smem = smem_wg + (size_t)wv * wave_lds;
+    uint64_t tr[4] = {0, 0, 0, 0};
+    AT_MARK(0);
     const int kvh = blockIdx.x, split = blockIdx.y, tok0 = MT ? blockIdx.z * a.tq : blockIdx.z;
     const int aseq = (!MT && a.pos_dev) ? __builtin_amdgcn_readfirstlane(*a.pos_dev) + 1 : a.seq;
     const int G = a.n_heads / a.n_kv;
@@ -150,41 +161,6 @@ void attn_partial_kernel(AttnArgs a) {
     const int per = (span + S - 1) / S;
     const int kv0 = lo_pos + split * per;
     const int kv1 = min(kv0 + per, seq);
-
-    _Float16* sP = (_Float16*)smem;                              // [32 rows][32 keys]
-    float* sMisc = (float*)(smem + 32 * AT_KEYS * 2);            // corr[32] | ks[32] | vs[32]
-
-    // q operand: lane (head li, lg), step st -> d = lg*half + 8*st + [0, 8)
-    h8 qa[NST];
-#pragma unroll
-    for (int st = 0; st < NST; st++)
-        qa[st] = li < GC ? __builtin_bit_cast(h8, *(const u32x4a*)(a.q + (int64_t)ctok * a.n_heads * hd +
-                                                                    (int64_t)(kvh * G + li % G) * hd + lg * half + 8 * st))
-                         : h8{};
-    for (int i = l; i < 32 * AT_KEYS; i += 64) sP[i] = (_Float16)0.0f;
-
-    // identity operands of the V transpose.  int8: lane (col li, lg) holds
-    // B[16lg + i][li] = (16lg + i == li).  fp16: two K = 16 halves, lane
-    // (col li, lg) holds B_hh[8lg + e][li] = (16hh + 8lg + e == li).
-    i32x4 eye8;
-    h8 eyeh[2];
-    {
-        uint32_t w[4] = {0u, 0u, 0u, 0u};
-        const int pos = li - 16 * lg;
-        if (pos >= 0 && pos < 16) w[pos >> 2] = 1u << (8 * (pos & 3));
-        eye8 = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-#pragma unroll
-        for (int hh = 0; hh < 2; hh++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) eyeh[hh][e] = (_Float16)((16 * hh + 8 * lg + e == li) ? 1.0f : 0.0f);
-    }
-
-    // running softmax state of column li (meaningful in lanes li < GC; both
-    // lane halves keep identical copies)
-    float run_m = -FLT_MAX, run_l = 0.0f;
-    f32x16 acc[NDT];
-#pragma unroll
-    for (int i = 0; i < NDT; i++) acc[i] = f32x16{};
 
     // raw rows of one tile: lane (li, lg) holds K[key li][lg half] and the V
     // pieces of key li its lane group feeds to the transpose: int8
@@ -209,6 +185,50 @@ void attn_partial_kernel(AttnArgs a) {
         ks_ = (INT8 && a.ks) ? a.ks[(int64_t)pos * a.n_kv + kvh] : 1.0f;
         vs_ = (INT8 && a.vs) ? a.vs[(int64_t)pos * a.n_kv + kvh] : 1.0f;
     };
+
+    // the first tile's loads go out before any other set-up work, so that
+    // their latency overlaps it
+    const int first = kv0 + wv * AT_KEYS, stride = W * AT_KEYS;
+    if (first < kv1) load_tile(first, rk, rv, ksn, vsn);
+    __builtin_amdgcn_sched_barrier(0);
+
+    _Float16* sP = (_Float16*)smem;                              // [32 rows][32 keys]
+    float* sMisc = (float*)(smem + 32 * AT_KEYS * 2);            // corr[32] | ks[32] | vs[32]
+
+    // q operand: lane (head li, lg), step st -> d = lg*half + 8*st + [0, 8)
+    // (every lane loads a valid row -- its column's head modulo G -- so the
+    // loads issue unpredicated; lanes without a column then zero theirs)
+    h8 qa[NST];
+#pragma unroll
+    for (int st = 0; st < NST; st++) {
+        const u32x4a qv = *(const u32x4a*)(a.q + (int64_t)ctok * a.n_heads * hd + (int64_t)(kvh * G + li % G) * hd +
+                                           lg * half + 8 * st);
+        qa[st] = __builtin_bit_cast(h8, li < GC ? qv : u32x4a{0u, 0u, 0u, 0u});
+    }
+    for (int i = l; i < 32 * AT_KEYS; i += 64) sP[i] = (_Float16)0.0f;
+
+    // identity operands of the V transpose.  int8: lane (col li, lg) holds
+    // B[16lg + i][li] = (16lg + i == li).  fp16: two K = 16 halves, lane
+    // (col li, lg) holds B_hh[8lg + e][li] = (16hh + 8lg + e == li).
+    i32x4 eye8;
+    h8 eyeh[2];
+    {
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+        const int pos = li - 16 * lg;
+        if (pos >= 0 && pos < 16) w[pos >> 2] = 1u << (8 * (pos & 3));
+        eye8 = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) eyeh[hh][e] = (_Float16)((16 * hh + 8 * lg + e == li) ? 1.0f : 0.0f);
+    }
+
+    // running softmax state of column li (meaningful in lanes li < GC; both
+    // lane halves keep identical copies)
+    float run_m = -FLT_MAX, run_l = 0.0f;
+    f32x16 acc[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; i++) acc[i] = f32x16{};
 
     // one tile from the registers (ck, cv; key scales ksc, vsc of key li)
     auto tile = [&](int p0, const u32x4a (&ck)[KW], const u32x4a (&cv)[VW], float ksc, float vsc) {
@@ -328,8 +348,6 @@ void attn_partial_kernel(AttnArgs a) {
     // the next tile's rows load into (rk, rv) while the current one (a copy)
     // is computed
     // wave wv of W takes tiles wv, wv + W, ... of the workgroup's key range
-    const int first = kv0 + wv * AT_KEYS, stride = W * AT_KEYS;
-    if (first < kv1) load_tile(first, rk, rv, ksn, vsn);
     for (int p0 = first; p0 < kv1; p0 += stride) {
         u32x4a ck[KW], cv[VW];
 #pragma unroll
@@ -339,7 +357,9 @@ void attn_partial_kernel(AttnArgs a) {
         const float ksc = ksn * a.scale, vsc = vsn;
         if (p0 + stride < kv1) load_tile(p0 + stride, rk, rv, ksn, vsn);
         tile(p0, ck, cv, ksc, vsc);
+        if (p0 == first) AT_MARK(1);
     }
+    AT_MARK(2);
 
     // 4. S == 1: the normalised output straight from this wave; else the
     //    unnormalised partials m, l per head (acc = high rows + low rows)
@@ -347,6 +367,57 @@ void attn_partial_kernel(AttnArgs a) {
     float* sO = (float*)smem;                                  // [2G][hd]
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
+    if constexpr (!MT) {
+        // decode: the rows go to LDS transposed, sOT[d][R] (R = 2G rounded up
+        // to 8), four consecutive rows of a column per 16-byte store, only the
+        // row groups that hold a head; then lane l forms the outputs of
+        // d = l, l + 64, ... for every head (high + low row) and stores them
+        // coalesced along d
+        const int R = (2 * G + 7) & ~7;
+        float* sOT = (float*)smem;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+#pragma unroll
+            for (int m4 = 0; m4 < 4; m4++) {
+                if (8 * m4 >= 2 * G) break;
+                *(f32x4a*)&sOT[(32 * dt + li) * R + 8 * m4 + 4 * lg] =
+                    f32x4a{acc[dt][4 * m4], acc[dt][4 * m4 + 1], acc[dt][4 * m4 + 2], acc[dt][4 * m4 + 3]};
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+        if (S == 1) {
+            const float inv_l = run_l > 0.0f ? 1.0f / run_l : 0.0f;
+            for (int h = 0; h < G; h++) {
+                const float il = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, inv_l), h));
+                uint16_t* ot = a.out + (int64_t)(pbase + h) * hd;
+                for (int d = l; d < hd; d += 64)
+                    ot[d] = f32_to_f16_bits((sOT[d * R + h] + sOT[d * R + G + h]) * il);
+            }
+            return;
+        }
+        float* pm = a.part;
+        float* pl = a.part + (int64_t)a.n_heads * S;
+        if (li < G && lg == 0) {
+            pm[(int64_t)(pbase + li) * S + split] = run_m;
+            pl[(int64_t)(pbase + li) * S + split] = run_l;
+        }
+        float* pacc = a.part + (int64_t)a.n_heads * S * 2 + ((int64_t)pbase * S + split) * hd;
+        for (int h = 0; h < G; h++) {
+            for (int d = l; d < hd; d += 64) pacc[(int64_t)h * S * hd + d] = sOT[d * R + h] + sOT[d * R + G + h];
+        }
+#ifdef JLLM_ATTN_TRACE
+        AT_MARK(3);
+        const int gw = blockIdx.y * gridDim.x + blockIdx.x;
+        if (l < 4 && gw < 8192) {
+            uint64_t tv = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) if (l == i) tv = tr[i];
+            g_attn_trace[gw * 4 + l] = tv;
+        }
+#endif
+        return;
+    }
 #pragma unroll
     for (int dt = 0; dt < NDT; dt++) {
 #pragma unroll
@@ -419,6 +490,16 @@ void attn_reduce_kernel(uint16_t* __restrict__ out, const float* __restrict__ pa
     const float* pm = part + (int64_t)h * S;
     const float* pl = part + (int64_t)n_heads * S + (int64_t)h * S;
     const float* pacc = part + (int64_t)n_heads * S * 2 + (int64_t)h * S * hd;
+    // wave w: splits w, w+8, ...; lane l: d = 2l, 2l+1 -- loaded first, with
+    // (m, l), so that both take one round trip to memory
+    constexpr int NW = AT_RED_THREADS / 64;
+    constexpr int MAXPER = AT_MAXS / NW;
+    float2 pv[MAXPER];
+#pragma unroll
+    for (int i = 0; i < MAXPER; i++) {
+        const int sp = w + NW * i;
+        pv[i] = (sp < S && 2 * l < hd) ? *(const float2*)(pacc + (int64_t)sp * hd + 2 * l) : make_float2(0.0f, 0.0f);
+    }
     const float m = t < S ? pm[t] : -FLT_MAX;
     const float lv = t < S ? pl[t] : 0.0f;
     float mx = m;
@@ -441,17 +522,8 @@ void attn_reduce_kernel(uint16_t* __restrict__ out, const float* __restrict__ pa
 #pragma unroll
     for (int i = 0; i < AT_RED_THREADS / 64; i++) Lt += sRed[i];
     const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
-    // wave w: splits w, w+8, ...; lane l: d = 2l, 2l+1
-    constexpr int NW = AT_RED_THREADS / 64;
-    constexpr int MAXPER = AT_MAXS / NW;
     float2 o = make_float2(0.0f, 0.0f);
     if (2 * l < hd) {
-        float2 pv[MAXPER];
-#pragma unroll
-        for (int i = 0; i < MAXPER; i++) {
-            const int sp = w + NW * i;
-            pv[i] = sp < S ? *(const float2*)(pacc + (int64_t)sp * hd + 2 * l) : make_float2(0.0f, 0.0f);
-        }
 #pragma unroll
         for (int i = 0; i < MAXPER; i++) {
             const int sp = w + NW * i;
@@ -481,6 +553,13 @@ void attn_reduce_wave_kernel(uint16_t* __restrict__ out, const float* __restrict
     const float* pm = part + (int64_t)h * S;
     const float* pl = part + (int64_t)n_heads * S + (int64_t)h * S;
     const float* pacc = part + (int64_t)n_heads * S * 2 + (int64_t)h * S * hd;
+    // the first 16 splits' accumulators are loaded with (m, l): one round
+    // trip to memory for both
+    const bool lane_d = 2 * l < hd;
+    float2 v[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+        v[i] = (i < S && lane_d) ? *(const float2*)(pacc + (int64_t)i * hd + 2 * l) : make_float2(0.0f, 0.0f);
     float mv[AT_MAXS / 64], lv[AT_MAXS / 64];
     float mx = -FLT_MAX;
 #pragma unroll
@@ -504,13 +583,14 @@ void attn_reduce_wave_kernel(uint16_t* __restrict__ out, const float* __restrict
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
-    if (2 * l >= hd) return;
+    if (!lane_d) return;
     float ox = 0.0f, oy = 0.0f;
     for (int s0 = 0; s0 < S; s0 += 16) {
-        float2 v[16];
+        if (s0 > 0) {
 #pragma unroll
-        for (int i = 0; i < 16; i++)
-            v[i] = s0 + i < S ? *(const float2*)(pacc + (int64_t)(s0 + i) * hd + 2 * l) : make_float2(0.0f, 0.0f);
+            for (int i = 0; i < 16; i++)
+                v[i] = s0 + i < S ? *(const float2*)(pacc + (int64_t)(s0 + i) * hd + 2 * l) : make_float2(0.0f, 0.0f);
+        }
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const float wi = s0 + i < S ? sW[s0 + i] : 0.0f;
@@ -521,6 +601,12 @@ void attn_reduce_wave_kernel(uint16_t* __restrict__ out, const float* __restrict
     *(uint32_t*)(out + (int64_t)h * hd + 2 * l) =
         (uint32_t)f32_to_f16_bits(ox * inv) | ((uint32_t)f32_to_f16_bits(oy * inv) << 16);
 }
+
+#ifdef JLLM_ATTN_TRACE
+extern "C" int jllm_hip_attn_trace_read(uint64_t* host) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_attn_trace), sizeof(g_attn_trace), 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+#endif
 
 hipError_t attn_launch(const AttnArgs& a, bool kv_int8, hipStream_t st) {
     if (a.tokens < 1 || a.tq < 1 || (a.tokens > 1 && a.n_splits != 1) || (a.n_splits > 1 && a.tq != 1) ||
