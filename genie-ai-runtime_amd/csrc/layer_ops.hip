@@ -250,6 +250,13 @@ hipError_t rope_launch(uint16_t* q, uint16_t* k, int n_heads, int n_kv, int head
 // Replaces decode.cu:1441-1478 (q/k norm, rope_inplace, fp16_to_int8 x2)
 // and the per-token loop of decode.cu:1806-1842.
 __global__ __launch_bounds__(256) void qk_post_kernel(QKPostArgs a) {
+    // every scalar argument requested at one point (one batch of scalar
+    // loads), then the wave's global loads -- its head's pair, the norm
+    // weights, the position -- before any arithmetic that waits for them
+    asm volatile("" :: "s"(a.q), "s"(a.k), "s"(a.v), "s"(a.q_norm), "s"(a.k_norm), "s"(a.k_dst), "s"(a.v_dst),
+                 "s"(a.k_scales), "s"(a.v_scales), "s"(a.kv_stride), "s"(a.n_heads), "s"(a.n_kv), "s"(a.head_dim),
+                 "s"(a.cache_head_dim), "s"(a.start_pos), "s"(a.N), "s"(a.eps), "s"(a.norm_fp32), "s"(a.neox),
+                 "s"(a.kv_int8), "s"(a.q_in_stride), "s"(a.kv_in_stride), "s"(a.pos_dev));
     const int hd = a.head_dim;
     const int slots = a.n_heads + 2 * a.n_kv;
     const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -262,16 +269,34 @@ __global__ __launch_bounds__(256) void qk_post_kernel(QKPostArgs a) {
     const int64_t ks = a.kv_in_stride ? a.kv_in_stride : (int64_t)a.n_kv * hd;
     const uint16_t* src = kind == 0 ? a.q + t * qs + (int64_t)head * hd
                                     : (kind == 1 ? a.k : a.v) + t * ks + (int64_t)head * hd;
-    const int p0 = a.pos_dev ? __builtin_amdgcn_readfirstlane(*a.pos_dev) : a.start_pos;
+    const void* norm = kind < 2 ? (kind == 0 ? a.q_norm : a.k_norm) : nullptr;
+    const bool act = l < hd / 2;
+    int i0, i1;
+    front_idx(hd, a.neox != 0, l, i0, i1);
+    const int j0 = act ? i0 : 0, j1 = act ? i1 : 0;    // lanes past the pairs read element 0
+    // raw loads first (all in flight together), conversions after
+    const uint16_t x0 = src[j0], x1 = src[j1];
+    uint32_t wr0 = 0, wr1 = 0;
+    if (norm) {
+        if (a.norm_fp32) { wr0 = ((const uint32_t*)norm)[j0]; wr1 = ((const uint32_t*)norm)[j1]; }
+        else { wr0 = ((const uint16_t*)norm)[j0]; wr1 = ((const uint16_t*)norm)[j1]; }
+    }
+    const float fq = a.fr.f[act ? l : 0];
+    const int pd = a.pos_dev ? *a.pos_dev : 0;
+    __builtin_amdgcn_sched_barrier(0);
+    const float v0i = act ? f16_bits_to_f32(x0) : 0.0f, v1i = act ? f16_bits_to_f32(x1) : 0.0f;
+    float v0 = v0i, v1 = v1i, w0 = 0.0f, w1 = 0.0f;
+    if (norm && act) {
+        if (a.norm_fp32) { w0 = __builtin_bit_cast(float, wr0); w1 = __builtin_bit_cast(float, wr1); }
+        else { w0 = f16_bits_to_f32((uint16_t)wr0); w1 = f16_bits_to_f32((uint16_t)wr1); }
+    }
+    const int p0 = a.pos_dev ? __builtin_amdgcn_readfirstlane(pd) : a.start_pos;
     const int64_t r0 = a.pos_dev ? p0 : 0;            // cache row of token 0 relative to k_dst / v_dst
     const int pos = p0 + t;
     float s = 0.0f, c = 1.0f;
-    if (kind < 2) sincosf((float)pos * a.fr.f[l < hd / 2 ? l : 0], &s, &c);
-    float v0, v1;
-    int i0, i1;
-    front_pair(src, hd, a.neox != 0, kind < 2 ? (kind == 0 ? a.q_norm : a.k_norm) : nullptr,
-               a.norm_fp32 != 0, a.eps, kind < 2, c, s, l, v0, v1, i0, i1);
-    if (kind < 2 && l < hd / 2) {
+    if (kind < 2) sincosf((float)pos * fq, &s, &c);
+    front_apply(norm != nullptr, w0, w1, hd, a.eps, kind < 2, c, s, v0, v1);
+    if (kind < 2 && act) {
         uint16_t* dq = kind == 0 ? a.q + t * qs + (int64_t)head * hd : a.k + t * ks + (int64_t)head * hd;
         dq[i0] = f32_to_f16_bits(v0);
         dq[i1] = f32_to_f16_bits(v1);
