@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <mutex>
 #include "../../include/jllm_hip.h"
 
 namespace jllm_hip {
@@ -22,21 +23,39 @@ inline int launch_status(hipError_t e, const char* tag) {
 }
 
 // Per-device, lazily grown device scratch that is never freed (the
-// reference's static scratch semantics, e.g. gemv_q4.cu:1309-1321).
+// reference's static scratch semantics, e.g. gemv_q4.cu:1309-1321).  A
+// request larger than the current buffer allocates a new one (rounded up
+// to a power of two, at least 1 MiB, zeroed once) and RETIRES the old one
+// without freeing it: a HIP graph captured earlier keeps pointing at memory
+// that stays valid (and is no longer handed out).  Growth is a hipMalloc,
+// so it must not happen during stream capture: size the scratch with one
+// eager call (e.g. get_splitk_partials) before capturing.
 struct DeviceScratch {
-    void* ptr[64] = {};
-    size_t cap[64] = {};
+    static constexpr int MAXDEV = 64;
+    void* ptr[MAXDEV] = {};
+    size_t cap[MAXDEV] = {};
+    int retired[MAXDEV] = {};
+    std::mutex mu;
     void* get(size_t bytes) {
         int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXDEV) return nullptr;
+        std::lock_guard<std::mutex> lk(mu);
         if (bytes > cap[dev]) {
-            if (ptr[dev]) (void)hipFree(ptr[dev]);
-            ptr[dev] = nullptr; cap[dev] = 0;
-            if (hipMalloc(&ptr[dev], bytes) != hipSuccess) { ptr[dev] = nullptr; return nullptr; }
+            size_t want = (size_t)1 << 20;
+            while (want < bytes) want <<= 1;
+            void* p = nullptr;
+            if (hipMalloc(&p, want) != hipSuccess) {
+                (void)hipGetLastError();
+                fprintf(stderr, "[scratch] hipMalloc of %zu bytes failed (inside a stream capture? size the "
+                                "scratch with an eager call first)\n", want);
+                return nullptr;
+            }
             // zeroed once, synchronously, at allocation (never inside a
             // stream, so graph capture never records it)
-            if (hipMemset(ptr[dev], 0, bytes) != hipSuccess) { (void)hipFree(ptr[dev]); ptr[dev] = nullptr; return nullptr; }
-            cap[dev] = bytes;
+            if (hipMemset(p, 0, want) != hipSuccess) { (void)hipFree(p); (void)hipGetLastError(); return nullptr; }
+            if (ptr[dev]) retired[dev]++;      // the old buffer stays allocated for graphs that captured it
+            ptr[dev] = p;
+            cap[dev] = want;
         }
         return ptr[dev];
     }

@@ -197,3 +197,37 @@ def test_attention_repeats_and_graph_replays(dev):
             assert torch.equal(o, e), r
         calls()                                      # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_captured_graph_survives_scratch_growth(dev):
+    """A graph captured with the library's split-K partials keeps valid memory
+    when a later, larger call grows that scratch: the old buffer is retired,
+    not freed, so the graph's replays still give the eager result."""
+    print_case("attn_graph_scratch_growth")
+    ctx = 512
+    q, k, v, ks, vs = _case(77, ctx)
+    qd, kd, vd, ksd, vsd = to_dev(q), to_dev(k), to_dev(v), to_dev(ks), to_dev(vs)
+    out = torch.empty(H * HD, dtype=torch.int16, device=dev)
+    args = [out, qd, kd, vd, H, KV, HD, HD, ctx, 1.0 / np.sqrt(HD), 1, ksd, vsd, 0]
+    jllm.call("jllm_hip_flash_attention_decode", *args)
+    want = from_dev(out, np.uint16).copy()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        jllm.call("jllm_hip_flash_attention_decode", *args)
+    out.zero_()
+    gr.replay()
+    assert np.array_equal(from_dev(out, np.uint16), want)
+    # a larger request (64 heads x 256 splits) grows the partials buffer
+    big = 64
+    qb = to_dev(synth.x_f16(synth.rng(78), big * HD))
+    outb = torch.empty(big * HD, dtype=torch.int16, device=dev)
+    jllm.call("jllm_hip_flash_attention_decode_splits", outb, qb, kd, vd, big, KV, HD, HD, ctx, 1.0 / np.sqrt(HD), 1,
+              ksd, vsd, 0, 256)
+    torch.cuda.synchronize()
+    filler = torch.full((64 << 20,), 7, dtype=torch.uint8, device=dev)     # reuse of freed memory would show
+    for _ in range(3):
+        out.zero_()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(from_dev(out, np.uint16), want)
+    del filler
