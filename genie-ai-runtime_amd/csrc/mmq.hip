@@ -212,6 +212,22 @@ __device__ __forceinline__ h8m bytes_to_h8(u32x2m w, float bias) {
     return __builtin_bit_cast(h8m, p) - h8m{b, b, b, b, b, b, b, b};
 }
 
+// 8 Q6_K codes q (bytes 0..63) -> 8 fp16 values (q - 32) * sc, in one fused
+// multiply-add of the biased halves 1024 + q: (1024 + q) sc - 1056 sc is
+// formed exactly before its single rounding, and |(q - 32) sc| <= 1024 is
+// exact in fp16
+__device__ __forceinline__ h8m q6_to_h8_scaled(u32x2m w, _Float16 sc) {
+    const uint32_t hi = 0x64646464u;
+    u32x4m p;
+    p.x = __builtin_amdgcn_perm(hi, w.x, 0x04010400u);
+    p.y = __builtin_amdgcn_perm(hi, w.x, 0x04030402u);
+    p.z = __builtin_amdgcn_perm(hi, w.y, 0x04010400u);
+    p.w = __builtin_amdgcn_perm(hi, w.y, 0x04030402u);
+    const _Float16 off = (_Float16)-1056.0f * sc;       // exact: 1056 * |sc| <= 33792 = 1056 * 2^5
+    return __builtin_elementwise_fma(__builtin_bit_cast(h8m, p), h8m{sc, sc, sc, sc, sc, sc, sc, sc},
+                                     h8m{off, off, off, off, off, off, off, off});
+}
+
 // 8 Q4_K nibbles (low or high halves of 8 code bytes) -> 8 fp16 values 0..15
 __device__ __forceinline__ h8m nib_lo_h8(u32x2m w) { return bytes_to_h8(w & 0x0F0F0F0Fu, 1024.0f); }
 __device__ __forceinline__ h8m nib_hi_h8(u32x2m w) { return bytes_to_h8((w >> 4u) & 0x0F0F0F0Fu, 1024.0f); }
@@ -605,11 +621,14 @@ void mmq_q6k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const u
             const uint32_t nsh = qq >= 2 ? 4u : 0u, hsh = 2u * qq;
             const u32x2m v0 = ((ql0 >> nsh) & 0x0F0F0F0Fu) | (((qh0 >> hsh) & 0x03030303u) << 4u);
             const u32x2m v1 = ((ql1 >> nsh) & 0x0F0F0F0Fu) | (((qh1 >> hsh) & 0x03030303u) << 4u);
-            h8m A0 = bytes_to_h8(v0, 1056.0f), A1 = bytes_to_h8(v1, 1056.0f);   // q - 32
+            h8m A0, A1;
             if (OUT != 2) {
                 const _Float16 s0 = sSC[slot][(2 * j) * TM + arow], s1 = sSC[slot][(2 * j + 1) * TM + arow];
-                A0 = A0 * h8m{s0, s0, s0, s0, s0, s0, s0, s0};   // exact: |(q-32)*sc| <= 1024
-                A1 = A1 * h8m{s1, s1, s1, s1, s1, s1, s1, s1};
+                A0 = q6_to_h8_scaled(v0, s0);             // (q - 32) * sc, exact
+                A1 = q6_to_h8_scaled(v1, s1);
+            } else {
+                A0 = bytes_to_h8(v0, 1056.0f);            // q - 32
+                A1 = bytes_to_h8(v1, 1056.0f);
             }
 #pragma unroll
             for (int tt = 0; tt < 2; tt++) {

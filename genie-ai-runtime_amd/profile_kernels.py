@@ -8,6 +8,7 @@
   copy  : a plain device-to-device copy of 256 MiB (calibrates FETCH_SIZE /
           WRITE_SIZE against a known byte count)
   mmq   : the Q4_K prefill GEMM 9728 x 2560 at N = 512 tokens (fp16 out), 5 calls
+  mmq6  : the Q6_K prefill GEMM 2560 x 9728 at N = 512 tokens (fp16 out), 5 calls
   attn  : INT8-KV split-K decode attention (32 q / 8 KV heads, head_dim 128) at
           ctx 8192 over 16 distinct caches (277 MB), 2 passes; then ctx 512
           over 240 caches (263 MB), 2 passes
@@ -64,6 +65,12 @@ def main(mode):
         y = torch.empty(512 * 9728, dtype=torch.int16, device=dev)
         for _ in range(5):
             jllm.call("jllm_hip_gemm_quant_batched", y, W, 12, x, 9728, 512, 2560)
+    elif mode == "mmq6":
+        W = up(synth.q6k(g, 2560, 9728))
+        x = up(synth.x_f16(g, (512, 9728)))
+        y = torch.empty(512 * 2560, dtype=torch.int16, device=dev)
+        for _ in range(5):
+            jllm.call("jllm_hip_gemm_quant_batched", y, W, 14, x, 2560, 512, 9728)
     elif mode == "attn":
         H, KV, HD = 32, 8, 128
         q = up(synth.x_f16(g, H * HD))
