@@ -37,7 +37,7 @@ int mmq_after_quant(const char* tag, void* y, const void* Wd, int type, const ui
                     const uint16_t* res = nullptr) {
     // split-K when the tile grid alone does not cover the chip: partials to
     // the workspace, then one ordered reduction into y
-    const int splits = out_kind == 2 ? 1 : mmq_splits(M, N, K);
+    const int splits = out_kind == 2 ? 1 : mmq_splits(M, N, K, type);
     void* dst = y;
     if (splits > 1) {
         dst = g_ws.get((size_t)splits * N * M * sizeof(float));

@@ -51,10 +51,10 @@ constexpr int MMQ_MULTI_MIN_TILES = 384;
 hipError_t mmq_q4k_multi_launch(const uint8_t* const* W, void* const* y, const int* M, int nseg, const uint8_t* codes,
                                 const uint32_t* scl, int N, int K, int Npad, hipStream_t st);
 
-// Split count for an N x M x K GEMM: enough workgroups to cover the chip
-// when the tile grid alone does not (at least 2 super-blocks per range,
-// at most 16 ranges); a function of M, ceil(N / 64) and K only.
-int mmq_splits(int M, int N, int K);
+// Split count for an N x M x K GEMM of weight type `type`: ranges of whole
+// super-blocks chosen by a measured cost model (at most 16 ranges for Q4_K /
+// Q5_K, 19 for Q6_K); a function of M, N, K and the type only.
+int mmq_splits(int M, int N, int K, int type);
 
 // y = sum of the `splits` fp32 partials ws[s][n], added in order s = 0, 1, ...
 // (fp16 out with res: y = half(half(sum) + res))

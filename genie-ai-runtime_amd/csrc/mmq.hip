@@ -489,189 +489,228 @@ void mmq_q4k_kernel(MmqSegs sg, const uint8_t* __restrict__ codes,
 }
 
 // ---------------------------------------------------------------------------
-// Q6_K: the raw ql/qh bytes of a half super-block are staged per row
-// (64 + 32 bytes, read from the 2-byte-aligned blocks with dword loads and
-// funnel shifts) and decoded by the lane that feeds them to the MFMA.
+// Q6_K on the f16 matrix cores, 128 x 128 workgroup tiles.
+//
+// (q - 32) * sc (|.| <= 1024) and the q8 codes (fp16 values -127..127) are
+// exact in fp16 and every 32-wide sum stays below 2^24, so two
+// v_mfma_f32_32x32x16_f16 give each 32-wide block's C_g0*sc_g0 + C_g1*sc_g1
+// exactly; the reference's per-half accumulation tmp += C * d8 (per 32),
+// sum += tmp * d (mmq_q6k_llama.cu:264-364) is then one fma per element per
+// block plus one per half.  The weight decode (6-bit code, minus 32, times
+// the group scale) costs the VALU about two operations per weight, so a
+// workgroup of 4 waves covers 128 rows x 128 tokens: each wave 32 rows x
+// 128 tokens (four 32x32 MFMA tiles), every decoded weight operand serving
+// 128 tokens.  K order inside a 32-wide block: lane group g holds elements
+// 16g..16g+15 (one 16-group, so one scale per lane and block, and 16
+// contiguous ql / qh bytes per lane); the activation operand is read from
+// LDS in the same order.  Per half super-block ("stage"): each lane loads
+// its row's three 16-byte pieces (low / high ql, qh) into registers one
+// stage ahead (aligned 20-byte windows realigned with funnel shifts: Q6_K
+// blocks are 2-byte aligned), and the scales + d once per super-block; the
+// 128 tokens' fp16 codes (32 KB) and d8 words go from global memory straight
+// to LDS (buffer_load ... lds), one stage ahead in a ring of two, 16-byte
+// pieces of a token XOR-swizzled so the operand reads are conflict-free.
 
-constexpr int R6_STRIDE = 104;          // LDS bytes per row: ql (64) + qh (32) of a half super-block + pad
+constexpr int Q6_TN = 128;                   // tokens per workgroup tile
+constexpr int Q6_ST_B = Q6_TN * 256;         // fp16 codes of a stage: 128 tokens x 128 values
+constexpr int Q6_ST_S = 4 * Q6_TN * 4;       // d8 words: 4 blocks x 128 tokens
+constexpr int Q6_ST_BYTES = Q6_ST_B + Q6_ST_S;
 
-template <int OUT>   // 0: fp16 y, 1: fp32 y, 2: int32 group dots [N][M][K/16]
+// piece P (16 B, 8 codes) of token t's 128 codes of a stage sits at position
+// P ^ (t & 15): 16 consecutive tokens reading one piece hit 16 bank groups
+__device__ __forceinline__ int swz6(int tok) { return tok & 15; }
+
+// 16 bytes at byte offset `off` of a buffer, read as an aligned 20-byte
+// window (the window may run past the end of the buffer: those bytes read
+// as zero) and realigned
+__device__ __forceinline__ u32x4m load16_2a(__amdgpu_buffer_rsrc_t r, int off) {
+    const int al = off & ~3;
+    const uint32_t sh = (uint32_t)(off & 3) * 8u;
+    const u32x4m w = __builtin_amdgcn_raw_buffer_load_b128(r, al, 0, 0);
+    const uint32_t w4 = __builtin_amdgcn_raw_buffer_load_b32(r, al + 16, 0, 0);
+    return u32x4m{__builtin_amdgcn_alignbit(w.y, w.x, sh), __builtin_amdgcn_alignbit(w.z, w.y, sh),
+                  __builtin_amdgcn_alignbit(w.w, w.z, sh), __builtin_amdgcn_alignbit(w4, w.w, sh)};
+}
+
+template <int OUT>   // 0: fp16 y, 1: fp32 y (split-K partials), 2: int32 group dots [N][M][K/16]
 __global__ __launch_bounds__(MMQ_THREADS, 2)
 void mmq_q6k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const uint16_t* __restrict__ codes,
                     const uint32_t* __restrict__ scl, int M, int N, int K, int Npad, int sps) {
-    __shared__ __attribute__((aligned(16))) uint8_t sR[2][TM * R6_STRIDE];
-    __shared__ __attribute__((aligned(16))) uint8_t sB[2][TN * B_STRIDE];
-    __shared__ __attribute__((aligned(16))) _Float16 sSC[2][16 * TM];    // int8 scales as fp16, per [group][row]
-    __shared__ __attribute__((aligned(16))) float sDA[2][TM];            // d per row
-    __shared__ __attribute__((aligned(16))) float sD8[2][8 * TN];        // d8 per [j][token]
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * Q6_ST_BYTES];
+    __shared__ __attribute__((aligned(16))) float sDA[TM];             // d of the wave's rows, current super-block
 
     const int nb = K / QK_K, nst = 2 * nb;
-    // split-K: this workgroup's stages [k0, k1) (whole super-blocks)
     const int k0 = 2 * (int)blockIdx.y * sps, k1 = min(nst, k0 + 2 * sps);
-    const int n_rt = (M + TM - 1) / TM, n_tt = Npad / TN;
+    const int n_rt = (M + TM - 1) / TM, n_tt = (Npad + Q6_TN - 1) / Q6_TN;
     const int tile = xcd_tile(blockIdx.x, n_rt * n_tt);
-    const int row0 = (tile / n_tt) * TM, col0 = (tile % n_tt) * TN;
+    const int row0 = (tile / n_tt) * TM, col0 = (tile % n_tt) * Q6_TN;
     const int t = threadIdx.x, w = t >> 6, l = t & 63, li = l & 31, g = l >> 5;
     const int arow = 32 * w + li;
 
-    // staging registers: 6 pieces of 8 raw bytes (3 aligned dwords each), the
-    // activation codes, and at the first half of a super-block the row's scale
-    // bytes and d (5 dwords) and two d8 words
-    uint32_t rr[6][3], rsc[5] = {0u, 0u, 0u, 0u, 0u}, rd = 0u;
-    u32x4m rb[4];
-    uint32_t rs[2];
-    auto piece_src = [&](int k, int i, int& row) -> const uint8_t* {
-        const int b = k >> 1, s = k & 1;
-        const int idx = i * MMQ_THREADS + t;
-        row = idx / 12;
-        const int pc = idx % 12;
-        const uint8_t* blk = W + ((int64_t)min(row0 + row, M - 1) * nb + b) * Q6K_BYTES;
-        return pc < 8 ? blk + 64 * s + 8 * pc : blk + 128 + 32 * s + 8 * (pc - 8);
+    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0,
+                                                                         (int)((int64_t)M * nb * Q6K_BYTES), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rC = __builtin_amdgcn_make_buffer_rsrc((void*)codes, (short)0,
+                                                                         (int)((int64_t)K * Npad * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc((void*)scl, (short)0,
+                                                                         (int)((int64_t)(K / 32) * Npad * 4), 0x00020000);
+    const int voRow = min(row0 + arow, M - 1) * nb * Q6K_BYTES;     // this lane's row
+
+    // DMA: instruction i (0..7) of wave w fills LDS bytes [(8w + i) KiB, +1 KiB)
+    // of the codes region: tokens 4(8w + i) + l/16, position l % 16
+    const int lh = l >> 4, pl = l & 15;
+    int xq[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) xq[j] = 16 * (pl ^ (4 * j + lh));
+    const int voB = (col0 + 32 * w + lh) * 512;                      // + 2048 i + xq[i & 3]
+    auto issue_b = [&](int k) {
+        uint8_t* st = smem + (k & 1) * Q6_ST_BYTES;
+        const int b = k >> 1, h = k & 1;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rC, (lds_void*)(st + (8 * w + i) * 1024), 16, voB + xq[i & 3],
+                                                     b * Npad * 512 + 256 * h + 2048 * i, 0, 0);
+        // d8 of block 4h + w for tokens 64i + l
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rS, (lds_void*)(st + Q6_ST_B + (2 * w + i) * 256), 4,
+                                                     (col0 + 64 * i + l) * 4, (b * 8 + 4 * h + w) * Npad * 4, 0, 0);
     };
-    auto fetch = [&](int k) {
-        const int b = k >> 1, s = k & 1;
-#pragma unroll
-        for (int i = 0; i < 6; i++) {
-            int row;
-            const uint8_t* src = piece_src(k, i, row);
-            const uint32_t* wp = (const uint32_t*)((uintptr_t)src & ~(uintptr_t)3);
-            rr[i][0] = wp[0]; rr[i][1] = wp[1]; rr[i][2] = wp[2];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int idx = i * MMQ_THREADS + t, tok = idx >> 4, piece = idx & 15;
-            rb[i] = *(const u32x4m*)(codes + ((int64_t)b * Npad + col0 + tok) * 256 + 128 * s + 8 * piece);
-        }
-        if (s == 0) {
-            if (t < TM) {
-                // scales: bytes 192..207 from the aligned dwords covering them (the fifth
-                // only when the block is not dword aligned, so nothing past byte 209 is
-                // read); d: bytes 208..209
-                const uint8_t* p = W + ((int64_t)min(row0 + t, M - 1) * nb + b) * Q6K_BYTES + 192;
-                const uint32_t* wp = (const uint32_t*)((uintptr_t)p & ~(uintptr_t)3);
-#pragma unroll
-                for (int i = 0; i < 4; i++) rsc[i] = wp[i];
-                rsc[4] = ((uintptr_t)p & 3u) ? wp[4] : 0u;
-                rd = *(const uint16_t*)(p + 16);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const int e = i * MMQ_THREADS + t, j = e / TN, tok = e % TN;
-                rs[i] = scl[(int64_t)(b * 8 + j) * Npad + col0 + tok];
-            }
-        }
+    // this lane's weight pieces of stage k: ql bytes [16g, +16) and [32 + 16g, +16)
+    // of the half, qh bytes [16g, +16)
+    auto load_a = [&](int k, u32x4m (&a)[3]) {
+        const int b = k >> 1, h = k & 1;
+        const int base = voRow + b * Q6K_BYTES;
+        a[0] = load16_2a(rW, base + 64 * h + 16 * g);
+        a[1] = load16_2a(rW, base + 64 * h + 32 + 16 * g);
+        a[2] = load16_2a(rW, base + 128 + 32 * h + 16 * g);
     };
-    auto commit = [&](int k) {
-        const int b = k >> 1, s = k & 1, slot = b & 1;
-#pragma unroll
-        for (int i = 0; i < 6; i++) {
-            int row;
-            const uint8_t* src = piece_src(k, i, row);
-            const uint32_t sh = (uint32_t)((uintptr_t)src & 3u) * 8u;
-            const int pc = (i * MMQ_THREADS + t) % 12;
-            *(u32x2m*)&sR[s][row * R6_STRIDE + 8 * pc] =
-                u32x2m{__builtin_amdgcn_alignbit(rr[i][1], rr[i][0], sh), __builtin_amdgcn_alignbit(rr[i][2], rr[i][1], sh)};
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int idx = i * MMQ_THREADS + t, tok = idx >> 4, piece = idx & 15;
-            *(u32x4m*)&sB[s][tok * B_STRIDE + 16 * piece] = rb[i];
-        }
-        if (s == 0) {
-            if (t < TM) {
-                const uint8_t* p = W + ((int64_t)min(row0 + t, M - 1) * nb + b) * Q6K_BYTES + 192;
-                const uint32_t sh = (uint32_t)((uintptr_t)p & 3u) * 8u;
-                uint32_t v[4];                         // scale bytes 192..207 of the block, realigned
-#pragma unroll
-                for (int i = 0; i < 4; i++) v[i] = __builtin_amdgcn_alignbit(rsc[i + 1], rsc[i], sh);
-#pragma unroll
-                for (int gi = 0; gi < 16; gi++)
-                    sSC[slot][gi * TM + t] = (_Float16)(float)(int8_t)(v[gi >> 2] >> (8 * (gi & 3)));
-                sDA[slot][t] = f16_bits_to_f32(rd);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; i++) sD8[slot][i * MMQ_THREADS + t] = __builtin_bit_cast(float, rs[i]);
-        }
+    // scales[16] and d of super-block b: bytes 192..209 (a 20-byte window)
+    auto load_hdr = [&](int b, u32x4m& sc, uint32_t& d) {
+        const int off = voRow + b * Q6K_BYTES + 192;
+        const int al = off & ~3;
+        const uint32_t sh = (uint32_t)(off & 3) * 8u;
+        const u32x4m ww = __builtin_amdgcn_raw_buffer_load_b128(rW, al, 0, 0);
+        const uint32_t w4 = __builtin_amdgcn_raw_buffer_load_b32(rW, al + 16, 0, 0);
+        sc = u32x4m{__builtin_amdgcn_alignbit(ww.y, ww.x, sh), __builtin_amdgcn_alignbit(ww.z, ww.y, sh),
+                    __builtin_amdgcn_alignbit(ww.w, ww.z, sh), __builtin_amdgcn_alignbit(w4, ww.w, sh)};
+        d = sh ? (w4 >> 16) : (w4 & 0xFFFFu);
     };
 
-    f32x16m acc[2];
-    acc[0] = f32x16m{};
-    acc[1] = f32x16m{};
+    f32x16m acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = f32x16m{};
 
-    fetch(k0);
-    commit(k0);
-    __syncthreads();
-#pragma unroll 1
-    for (int k = k0; k < k1; k++) {
-        const int b = k >> 1, s = k & 1, slot = b & 1;
-        if (k + 1 < k1) fetch(k + 1);
-        const uint8_t* Rw = &sR[s][arow * R6_STRIDE];
-        const uint8_t* B = sB[s];
-        f32x16m tmp[2];
-        tmp[0] = f32x16m{};
-        tmp[1] = f32x16m{};
-#pragma unroll 1
-        for (int qq = 0; qq < 4; qq++) {                 // the four 32-wide quarters of this half
-            const int j = 4 * s + qq;                    // 32-wide block within the super-block
-            // lane (row arow, g): elements l = 8g..8g+7 (group 2j) and 16+8g.. (group 2j+1)
-            const u32x2m ql0 = *(const u32x2m*)(Rw + 32 * (qq & 1) + 8 * g);
-            const u32x2m ql1 = *(const u32x2m*)(Rw + 32 * (qq & 1) + 16 + 8 * g);
-            const u32x2m qh0 = *(const u32x2m*)(Rw + 64 + 8 * g);
-            const u32x2m qh1 = *(const u32x2m*)(Rw + 64 + 16 + 8 * g);
-            const uint32_t nsh = qq >= 2 ? 4u : 0u, hsh = 2u * qq;
-            const u32x2m v0 = ((ql0 >> nsh) & 0x0F0F0F0Fu) | (((qh0 >> hsh) & 0x03030303u) << 4u);
-            const u32x2m v1 = ((ql1 >> nsh) & 0x0F0F0F0Fu) | (((qh1 >> hsh) & 0x03030303u) << 4u);
-            h8m A0, A1;
+    auto compute = [&](int k, const u32x4m (&a)[3], const u32x4m& hsc) {
+        const uint8_t* st = smem + (k & 1) * Q6_ST_BYTES;
+        const int b = k >> 1, h = k & 1;
+        const float* sD8 = (const float*)(st + Q6_ST_B);
+        // the weight operands of the four 32-wide blocks: codes of elements
+        // 32q + 16g .. +15 of the half, (ql >> nsh) & 15 | ((qh >> 2q) & 3) << 4,
+        // as (q - 32) * sc (OUT 2: q - 32)
+        h8m A[4][2];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const u32x4m ql = (q & 1) ? a[1] : a[0];
+            const uint32_t nsh = q >= 2 ? 4u : 0u, hsh = 2u * q;
+            const u32x4m cw = ((ql >> nsh) & 0x0F0F0F0Fu) | (((a[2] >> hsh) & 0x03030303u) << 4u);
             if (OUT != 2) {
-                const _Float16 s0 = sSC[slot][(2 * j) * TM + arow], s1 = sSC[slot][(2 * j + 1) * TM + arow];
-                A0 = q6_to_h8_scaled(v0, s0);             // (q - 32) * sc, exact
-                A1 = q6_to_h8_scaled(v1, s1);
+                const int gi = 8 * h + 2 * q + g;                // 16-group of this lane's elements
+                const _Float16 sc = (_Float16)(float)(int)(int8_t)(uint8_t)(hsc[gi >> 2] >> (8 * (gi & 3)));
+                A[q][0] = q6_to_h8_scaled(u32x2m{cw.x, cw.y}, sc);
+                A[q][1] = q6_to_h8_scaled(u32x2m{cw.z, cw.w}, sc);
             } else {
-                A0 = bytes_to_h8(v0, 1056.0f);            // q - 32
-                A1 = bytes_to_h8(v1, 1056.0f);
+                A[q][0] = bytes_to_h8(u32x2m{cw.x, cw.y}, 1056.0f);
+                A[q][1] = bytes_to_h8(u32x2m{cw.z, cw.w}, 1056.0f);
             }
+        }
+        f32x4m dA[4];
+        if (OUT != 2) {
 #pragma unroll
-            for (int tt = 0; tt < 2; tt++) {
-                const int btok = 32 * tt + li;
-                const h8m B0 = *(const h8m*)(B + btok * B_STRIDE + 64 * qq + 16 * g);
-                const h8m B1 = *(const h8m*)(B + btok * B_STRIDE + 64 * qq + 32 + 16 * g);
+            for (int m4 = 0; m4 < 4; m4++) dA[m4] = *(const f32x4m*)(&sDA[32 * w + 8 * m4 + 4 * g]);
+        }
+        // token tile by token tile: tmp = sum over the blocks q (in order) of
+        // C * d8, then acc += tmp * d
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++) {
+            const int tok = 32 * tt + li;
+            const uint8_t* bt = st + tok * 256;
+            f32x16m tmp = f32x16m{};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int P = 4 * q + 2 * g;
+                const h8m B0 = *(const h8m*)(bt + 16 * (P ^ swz6(tok)));
+                const h8m B1 = *(const h8m*)(bt + 16 * ((P + 1) ^ swz6(tok)));
                 if (OUT == 2) {
-                    const f32x16m C0 = mfma16(A0, B0, f32x16m{});
-                    const f32x16m C1 = mfma16(A1, B1, f32x16m{});
+                    // the two 16-groups separately: the other lane group's weights zeroed
 #pragma unroll
-                    for (int v = 0; v < 16; v++) {
-                        const int r = row0 + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3);
-                        const int tok = col0 + btok;
-                        if (r < M && tok < N) {
-                            int* o = (int*)y + ((int64_t)tok * M + r) * (K / 16) + b * 16 + 2 * j;
-                            o[0] = (int)C0[v];
-                            o[1] = (int)C1[v];
+                    for (int gg = 0; gg < 2; gg++) {
+                        const h8m z = h8m{};
+                        f32x16m C = mfma16(g == gg ? A[q][0] : z, B0, f32x16m{});
+                        C = mfma16(g == gg ? A[q][1] : z, B1, C);
+#pragma unroll
+                        for (int v = 0; v < 16; v++) {
+                            const int r = row0 + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3);
+                            const int tk = col0 + tok;
+                            if (r < M && tk < N)
+                                ((int*)y)[((int64_t)tk * M + r) * (K / 16) + b * 16 + 8 * h + 2 * q + gg] = (int)C[v];
                         }
                     }
                 } else {
-                    f32x16m C = mfma16(A0, B0, f32x16m{});
-                    C = mfma16(A1, B1, C);                    // = C_g0*sc_g0 + C_g1*sc_g1, exact
-                    const float d8 = sD8[slot][j * TN + btok];
+                    f32x16m C = mfma16(A[q][0], B0, f32x16m{});
+                    C = mfma16(A[q][1], B1, C);                 // = C_g0*sc_g0 + C_g1*sc_g1, exact
+                    const float d8 = sD8[q * Q6_TN + tok];
 #pragma unroll
-                    for (int v = 0; v < 16; v++) tmp[tt][v] = __builtin_fmaf(C[v], d8, tmp[tt][v]);
+                    for (int v = 0; v < 16; v++) tmp[v] = __builtin_fmaf(C[v], d8, tmp[v]);
                 }
             }
+            if (OUT != 2) {
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[tt][v] = __builtin_fmaf(tmp[v], dA[v >> 2][v & 3], acc[tt][v]);
+            }
         }
-        if (OUT != 2) {
-            f32x4m dA[4];
-#pragma unroll
-            for (int m4 = 0; m4 < 4; m4++) dA[m4] = *(const f32x4m*)(&sDA[slot][32 * w + 8 * m4 + 4 * g]);
-#pragma unroll
-            for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-                for (int v = 0; v < 16; v++) acc[tt][v] = __builtin_fmaf(tmp[tt][v], dA[v >> 2][v & 3], acc[tt][v]);
-        }
-        if (k + 1 < k1) commit(k + 1);
-        __syncthreads();
+    };
+
+    // Stage pipeline: stage k+1's weight pieces (and, before an even stage,
+    // the next super-block's scales) into the other register set and its
+    // codes + d8 into the other LDS buffer while stage k is computed; then
+    // wait for everything (vmcnt(0)) and one barrier, which also orders all
+    // reads of buffer k & 1 before the DMA of stage k+2 overwrites it.
+    u32x4m a0[3], a1[3], hs0, hs1;
+    uint32_t hd0, hd1;
+    load_hdr(k0 >> 1, hs0, hd0);
+    load_a(k0, a0);
+    issue_b(k0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __builtin_amdgcn_s_barrier();
+#pragma unroll 1
+    for (int k = k0; k < k1; k += 2) {
+        const int kl = k1 - 1;
+        // even stage k: first half of super-block k/2 (scales hs0 / hd0)
+        if (OUT != 2 && g == 0) sDA[arow] = f16_bits_to_f32(hd0);
+        load_a(k + 1, a1);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_b(k + 1);
+        __builtin_amdgcn_wave_barrier();
+        compute(k, a0, hs0);
+        // next super-block's header (clamped: past the range it re-reads the last one)
+        load_hdr(min(k + 2, kl) >> 1, hs1, hd1);
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __builtin_amdgcn_s_barrier();
+        // odd stage k+1: second half, same scales
+        // (past the last stage: stage k again, into the buffer nobody reads now)
+        const int kn = k + 2 <= kl ? k + 2 : k;
+        load_a(kn, a0);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_b(kn);
+        compute(k + 1, a1, hs0);
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __builtin_amdgcn_s_barrier();
+        hs0 = hs1;
+        hd0 = hd1;
     }
     if (OUT == 2) return;
 #pragma unroll
-    for (int tt = 0; tt < 2; tt++) {
+    for (int tt = 0; tt < 4; tt++) {
         const int tok = col0 + 32 * tt + li;
 #pragma unroll
         for (int v = 0; v < 16; v++) {
@@ -686,7 +725,8 @@ void mmq_q6k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const u
 
 hipError_t mmq_launch(void* y, const uint8_t* W, int type, const void* codes, const uint32_t* scl, int M, int N,
                       int K, int Npad, int out_kind, int splits, hipStream_t st) {
-    const int tiles = ((M + TM - 1) / TM) * (Npad / TN);
+    const int tn = type == TYPE_Q4_K ? TN : Q6_TN;
+    const int tiles = ((M + TM - 1) / TM) * ((Npad + tn - 1) / tn);
     const int nb = K / QK_K;
     const int sps = (nb + splits - 1) / splits;
     if (splits < 1 || (splits > 1 && out_kind != 1) || (splits - 1) * sps >= nb) return hipErrorInvalidValue;
@@ -773,28 +813,37 @@ hipError_t mmq_q4k_multi_launch(const uint8_t* const* W, void* const* y, const i
     return hipGetLastError();
 }
 
-int mmq_splits(int M, int N, int K) {
-    const int64_t tiles = (int64_t)((M + TM - 1) / TM) * ((N + TN - 1) / TN);
+int mmq_splits(int M, int N, int K, int type) {
+    const bool q6 = type == TYPE_Q6_K;
+    const int tn = q6 ? Q6_TN : TN;
+    const int64_t tiles = (int64_t)((M + TM - 1) / TM) * ((N + tn - 1) / tn);
     const int nb = K / QK_K;
-    if (tiles >= MMQ_MULTI_MIN_TILES || nb < 4) return 1;
-    // Ranges of whole super-blocks, chosen by a cost model fitted on MI355X
-    // (Q4_K 9728 / 2560 / 1024 rows, K 2560 / 4096 / 9728, N 64-512): the
-    // kernel is VALU-bound per CU, so a launch takes about
-    //   4 us + g(w) x (super-blocks per range),
-    // w the most workgroups any CU holds (ceil(workgroups / 256); 3 fit at
-    // once), g(1, 2, 3) = 2.85, 4.56, 6.27 us per super-block, linear in w
-    // beyond (more rounds); split-K adds ~5 us (partials + reduce launch)
-    // and the fp32 partials' write and read at ~3 TB/s.  It picks the
-    // measured best count in every fitted case (e.g. N = 256: 1 range,
-    // 47 us, where "fill 512 slots" chose 5 ranges, 63 us).
-    auto g = [](int64_t w) { return w == 1 ? 2.85 : w == 2 ? 4.56 : 6.27 * (double)w / 3.0; };
+    if ((!q6 && tiles >= MMQ_MULTI_MIN_TILES) || nb < 4) return 1;
+    // Ranges of whole super-blocks, chosen by a cost model fitted on MI355X.
+    // The kernels are VALU-bound per CU: a launch takes about
+    //   4 us + rounds x g(w) x (super-blocks per range),
+    // w the workgroups a CU holds at once (ceil(workgroups / 256), at most
+    // 3 for Q4_K, 2 for Q6_K, whose workgroups hold 69 KB of LDS), rounds the
+    // waves of workgroups that takes; Q4_K g(1, 2, 3) = 2.85, 4.56, 6.27 us
+    // (fitted on 9728 / 2560 / 1024 rows, K 2560 / 4096 / 9728, N 64-512),
+    // Q6_K g(1, 2) = 6.0, 7.0 us (2560 / 9728 rows, K 4096 / 9728 / 2560,
+    // N 64-1261); split-K adds ~5 us (Q4_K) / ~8 us (Q6_K) for the partials
+    // and the reduce launch, and the fp32 partials' write and read at ~3 TB/s.
+    // It picks the measured best count, or one within 2 %, in every fitted
+    // case.
+    const int wmax = q6 ? 2 : 3;
+    auto g = [&](int64_t w) {
+        if (q6) return w == 1 ? 6.0 : 7.0;
+        return w == 1 ? 2.85 : (w == 2 ? 4.56 : 6.27);
+    };
     int best = 1;
     double best_cost = 0.0;
-    for (int S = 1; S <= std::min(16, nb); S++) {
+    for (int S = 1; S <= std::min(q6 ? 19 : 16, nb); S++) {
         const int sps = (nb + S - 1) / S, eff = (nb + sps - 1) / sps;
-        const int64_t w = (tiles * eff + 255) / 256;
-        double cost = 4.0 + g(w) * sps;
-        if (eff > 1) cost += 5.0 + (double)eff * N * M * 8.0 / 3.0e6;
+        const int64_t c = (tiles * eff + 255) / 256;                 // workgroups per CU
+        const int64_t rounds = (c + wmax - 1) / wmax, w = std::min<int64_t>(c, wmax);
+        double cost = 4.0 + (double)rounds * g(w) * sps;
+        if (eff > 1) cost += (q6 ? 8.0 : 5.0) + (double)eff * N * M * 8.0 / 3.0e6;
         if (S == 1 || cost < best_cost) { best = eff; best_cost = cost; }
     }
     return best;
