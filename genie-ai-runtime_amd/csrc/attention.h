@@ -26,16 +26,20 @@ struct AttnArgs {
     // query tokens per wave (prefill): the wave's columns are tq tokens x
     // the G heads of its KV head, tq * G <= ATTN_MAX_COLUMNS; 1 for decode.
     int tq;
-    // waves per workgroup (prefill): the workgroup's key tiles are dealt to
-    // its waves round-robin by absolute tile position, and their softmax
-    // states are combined in LDS in wave order; 1 for decode.
+    // waves per workgroup (<= ATTN_MAX_WAVES): the workgroup's key tiles are
+    // dealt to its waves round-robin by absolute tile position, and their
+    // softmax states are combined in LDS in wave order (decode: into the
+    // output, or into the workgroup's partial when n_splits > 1).
     int wsplit;
 };
+constexpr int ATTN_MAX_WAVES = 8;
 constexpr int ATTN_PREFILL_WAVES = 2;   // measured: 1 wave 41.4 us, 2 waves 37.5 us, 4 waves 38.6 us (512-token prefill, one layer)
 
 constexpr int ATTN_MAX_SPLITS = 256;
 constexpr int ATTN_MAX_COLUMNS = 16;   // (token, head) columns per wave
 int attn_splits(int seq_len, int n_kv);
+// waves per decode workgroup for n_splits key ranges
+int attn_decode_waves(int n_splits);
 size_t attn_partials_floats(int n_heads, int n_splits, int head_dim);
 // Scratch layout: ATTN_COUNTER_BYTES of per-KV-head counters (fixed offset,
 // zero before the first call, reset by every call) followed by the partials.

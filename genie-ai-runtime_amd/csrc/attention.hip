@@ -89,6 +89,18 @@ int attn_splits(int seq_len, int n_kv) {
     return s < 128 ? s : 128;
 }
 
+int attn_decode_waves(int n_splits) {
+    // measured on MI355X (32 / 8 heads x 128, INT8 KV, >= 256 MB of distinct
+    // caches): 4 waves per workgroup from 64 key ranges on (ctx 2048 / 4096 /
+    // 8192: 10.9 -> 10.5, 13.2 -> 12.1, 15.3 -> 14.6 us), since the split
+    // combination then reads a quarter of the partials; below that the LDS
+    // combination costs more than it saves (ctx 512, 16 ranges: 8.2 us with
+    // one wave per workgroup, 9.6 / 10.1 / 11.9 us with 2 / 4 / 8), and one
+    // workgroup per head (no second launch) is slower still (12.1 us): its
+    // waves share a CU's SIMDs, where the per-tile arithmetic is the bound
+    return n_splits >= 64 ? 4 : 1;
+}
+
 size_t attn_partials_floats(int n_heads, int n_splits, int head_dim) {
     return (size_t)n_heads * n_splits * 2 + (size_t)n_heads * n_splits * head_dim;
 }
@@ -106,7 +118,8 @@ __host__ __device__ size_t attn_wave_lds_bytes(int n_heads, int n_kv, int head_d
 }
 // a workgroup of W waves: W wave regions, then (m, l) of each wave's columns
 __host__ __device__ size_t attn_lds_bytes(int n_heads, int n_kv, int head_dim, int tq, int W) {
-    return (size_t)W * attn_wave_lds_bytes(n_heads, n_kv, head_dim, tq) + (W > 1 ? (size_t)W * 2 * 32 * 4 : 0);
+    return (size_t)W * attn_wave_lds_bytes(n_heads, n_kv, head_dim, tq) +
+           (W > 1 ? (size_t)W * 2 * 32 * 4 + (size_t)(ATTN_MAX_WAVES + 1) * 32 * 4 + (size_t)W * 32 * 4 : 0);
 }
 
 // One wave per (KV head, split[, block of tq query tokens]).  The wave's
@@ -127,7 +140,7 @@ __host__ __device__ size_t attn_lds_bytes(int n_heads, int n_kv, int head_dim, i
 // MT: several query tokens per wave (per-column causal bounds); the
 // single-token form (decode, or tq == 1) compiles without the column masks.
 template <bool INT8, int HD, bool MT>
-__global__ __launch_bounds__(64 * ATTN_PREFILL_WAVES) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(64 * ATTN_MAX_WAVES) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_partial_kernel(AttnArgs a) {
     constexpr int EB = INT8 ? 1 : 2;
     constexpr int hd = HD, half = HD / 2;
@@ -136,8 +149,8 @@ void attn_partial_kernel(AttnArgs a) {
     constexpr int VW = NDT * EB;                        // V: 16-byte chunks per lane
     constexpr int NST = half / 8;                       // Q.K^T MFMA steps
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_wg[];
-    const int W = MT ? a.wsplit : 1;
-    const int wv = MT ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
+    const int W = a.wsplit;
+    const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const size_t wave_lds = attn_wave_lds_bytes(a.n_heads, a.n_kv, a.head_dim, a.tq);
     uint8_t* smem = smem_wg + (size_t)wv * wave_lds;
     uint64_t tr[4] = {0, 0, 0, 0};
@@ -386,6 +399,61 @@ void attn_partial_kernel(AttnArgs a) {
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);
         __builtin_amdgcn_wave_barrier();
+        if (W > 1) {
+            // combine the W waves' states per head, waves in order:
+            // M = max_w m_w, num = sum_w acc_w e^(m_w - M), den = sum_w l_w e^(m_w - M);
+            // the workgroup's output (S == 1) or its partial (M, den, num).
+            // Wave weights e^(m_w - M) are formed once per (wave, head), then
+            // every thread issues all its LDS reads before it adds.
+            float* sML = (float*)(smem_wg + (size_t)W * wave_lds);     // [W][m[32] | l[32]], then f [W][32]
+            float* sF = sML + W * 64;
+            if (lg == 0) { sML[wv * 64 + li] = run_m; sML[wv * 64 + 32 + li] = run_l; }
+            __syncthreads();
+            const int t = (int)threadIdx.x;
+            if (t < W * G) {
+                const int u = t / G, h = t % G;
+                float M = -FLT_MAX;
+                for (int w = 0; w < W; w++) M = fmaxf(M, sML[w * 64 + h]);
+                sF[u * 32 + h] = expf(sML[u * 64 + h] - M);
+                if (u == 0) sF[ATTN_MAX_WAVES * 32 + h] = M;
+            }
+            __syncthreads();
+            float* pm = a.part;
+            float* pl = a.part + (int64_t)a.n_heads * S;
+            float* pacc = a.part + (int64_t)a.n_heads * S * 2;
+            for (int e = t; e < G * hd; e += 64 * W) {
+                const int d = e / G, h = e % G;     // lanes: consecutive heads of one d, then d
+                float hi[ATTN_MAX_WAVES], lo[ATTN_MAX_WAVES], f[ATTN_MAX_WAVES], lv[ATTN_MAX_WAVES];
+#pragma unroll
+                for (int u = 0; u < ATTN_MAX_WAVES; u++) {
+                    if (u < W) {
+                        const float* so = (const float*)(smem_wg + (size_t)u * wave_lds);
+                        hi[u] = so[d * R + h];
+                        lo[u] = so[d * R + G + h];
+                        f[u] = sF[u * 32 + h];
+                        lv[u] = sML[u * 64 + 32 + h];
+                    }
+                }
+                float num = 0.0f, den = 0.0f;
+#pragma unroll
+                for (int u = 0; u < ATTN_MAX_WAVES; u++) {
+                    if (u < W) {
+                        num += (hi[u] + lo[u]) * f[u];
+                        den += lv[u] * f[u];
+                    }
+                }
+                if (S == 1) {
+                    a.out[(int64_t)(pbase + h) * hd + d] = f32_to_f16_bits(den > 0.0f ? num / den : 0.0f);
+                } else {
+                    pacc[((int64_t)(pbase + h) * S + split) * hd + d] = num;
+                    if (d == 0) {
+                        pm[(int64_t)(pbase + h) * S + split] = sF[ATTN_MAX_WAVES * 32 + h];
+                        pl[(int64_t)(pbase + h) * S + split] = den;
+                    }
+                }
+            }
+            return;
+        }
         if (S == 1) {
             const float inv_l = run_l > 0.0f ? 1.0f / run_l : 0.0f;
             for (int h = 0; h < G; h++) {
@@ -614,12 +682,12 @@ hipError_t attn_launch(const AttnArgs& a, bool kv_int8, hipStream_t st) {
         return hipErrorInvalidValue;
     dim3 grid(a.n_kv, a.n_splits, (a.tokens + a.tq - 1) / a.tq);
     const bool mt = a.tq > 1;
-    const int W = mt ? a.wsplit : 1;
-    if (W < 1 || W > ATTN_PREFILL_WAVES) return hipErrorInvalidValue;
+    const int W = a.wsplit;
+    if (W < 1 || W > ATTN_MAX_WAVES) return hipErrorInvalidValue;
     const size_t lds = attn_lds_bytes(a.n_heads, a.n_kv, a.head_dim, a.tq, W);
 #define ATTN_CASE(I8, HDV)                                                                                   \
     if (mt) hipLaunchKernelGGL((attn_partial_kernel<I8, HDV, true>), grid, dim3(64 * W), lds, st, a);       \
-    else    hipLaunchKernelGGL((attn_partial_kernel<I8, HDV, false>), grid, dim3(64), lds, st, a);
+    else    hipLaunchKernelGGL((attn_partial_kernel<I8, HDV, false>), grid, dim3(64 * W), lds, st, a);
     switch (a.head_dim * 2 + (kv_int8 ? 1 : 0)) {
     case 64:  ATTN_CASE(false, 32) break;
     case 65:  ATTN_CASE(true, 32) break;

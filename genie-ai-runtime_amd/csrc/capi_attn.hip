@@ -82,7 +82,11 @@ int attn_run(uint16_t* out, const uint16_t* q, const void* k, const void* v, int
     a.counters = counters;
     a.part = part;
     a.n_heads = n_heads; a.n_kv = n_kv; a.head_dim = hd; a.cache_head_dim = chd;
-    a.seq = seq; a.window = window; a.n_splits = n_splits; a.scale = scale; a.tokens = 1; a.tq = 1; a.wsplit = 1;
+    // the n_splits key ranges run as workgroups of W waves whose states are
+    // combined in LDS: n_splits / W partials (one launch when that is 1)
+    const int W = attn_decode_waves(n_splits);
+    const int groups = (n_splits + W - 1) / W;
+    a.seq = seq; a.window = window; a.n_splits = groups; a.scale = scale; a.tokens = 1; a.tq = 1; a.wsplit = W;
     a.pos_dev = pos_dev;
     return launch_status(attn_launch(a, kv_int8 != 0, (hipStream_t)stream), "attention");
 }
