@@ -49,13 +49,13 @@ constexpr int AT_MAXG = 16;          // max query heads per KV head
 constexpr int AT_MAXS = ATTN_MAX_SPLITS;   // max splits
 
 // 4 signed int8 (one word) -> 4 exact fp16 values (two words): with u = b ^ 0x80
-// in [1, 255], the half with bits 0x6400 + u is 1024 + u, minus 1152 gives b.
+// in [1, 255], the half with bits 0x64 : u is 1024 + u (byte permutes against
+// a word of 0x64 bytes), minus 1152 gives b.
 __device__ __forceinline__ u32x2a i8x4_to_h4(uint32_t w) {
     const half2_t bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-    const uint32_t p01 = __builtin_amdgcn_perm(w, w, 0x0C010C00u);
-    const uint32_t p23 = __builtin_amdgcn_perm(w, w, 0x0C030C02u);
-    const uint32_t a = (p01 ^ 0x00800080u) + 0x64006400u;
-    const uint32_t b = (p23 ^ 0x00800080u) + 0x64006400u;
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
     return u32x2a{h2_bits(as_h2(a) + bias), h2_bits(as_h2(b) + bias)};
 }
 
@@ -139,7 +139,9 @@ __host__ __device__ size_t attn_lds_bytes(int n_heads, int n_kv, int head_dim, i
 // current tile is computed.
 // MT: several query tokens per wave (per-column causal bounds); the
 // single-token form (decode, or tq == 1) compiles without the column masks.
-template <bool INT8, int HD, bool MT>
+// G4: at most 4 columns (decode with <= 4 q heads per KV head): the P.V rows
+// 8 and up hold nothing, so their accumulators are never rescaled.
+template <bool INT8, int HD, bool MT, bool G4>
 __global__ __launch_bounds__(64 * ATTN_MAX_WAVES) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_partial_kernel(AttnArgs a) {
     constexpr int EB = INT8 ? 1 : 2;
@@ -312,9 +314,10 @@ void attn_partial_kernel(AttnArgs a) {
         // 3. acc = acc * corr + P'.V.  The transpose delivers keys
         //    8*(v/4) + 4lg + v%4 in element v; MFMA step st takes v = 8st..8st+7,
         //    so P' is read at keys 16st + 4lg + [0,4) and 16st + 8 + 4lg + [0,4).
+        constexpr int NLIVE = G4 ? 4 : 16;              // accumulator elements that can hold a row
         float cr[16];
 #pragma unroll
-        for (int vv = 0; vv < 16; vv++) {
+        for (int vv = 0; vv < NLIVE; vv++) {
             const int r = 8 * (vv >> 2) + 4 * lg + (vv & 3);
             cr[vv] = r < 2 * GC ? sMisc[r < GC ? r : r - GC] : 1.0f;
         }
@@ -342,7 +345,7 @@ void attn_partial_kernel(AttnArgs a) {
                     for (int vv = 0; vv < 16; vv++) vt[vv] = ct[vv];
                 }
 #pragma unroll
-                for (int vv = 0; vv < 16; vv++) acc[dt][vv] *= cr[vv];
+                for (int vv = 0; vv < NLIVE; vv++) acc[dt][vv] *= cr[vv];
 #pragma unroll
                 for (int st = 0; st < 2; st++) {
                     h8 vb;
@@ -685,9 +688,11 @@ hipError_t attn_launch(const AttnArgs& a, bool kv_int8, hipStream_t st) {
     const int W = a.wsplit;
     if (W < 1 || W > ATTN_MAX_WAVES) return hipErrorInvalidValue;
     const size_t lds = attn_lds_bytes(a.n_heads, a.n_kv, a.head_dim, a.tq, W);
+    const bool g4 = !mt && a.n_heads / a.n_kv <= 4;
 #define ATTN_CASE(I8, HDV)                                                                                   \
-    if (mt) hipLaunchKernelGGL((attn_partial_kernel<I8, HDV, true>), grid, dim3(64 * W), lds, st, a);       \
-    else    hipLaunchKernelGGL((attn_partial_kernel<I8, HDV, false>), grid, dim3(64 * W), lds, st, a);
+    if (mt)      hipLaunchKernelGGL((attn_partial_kernel<I8, HDV, true, false>), grid, dim3(64 * W), lds, st, a); \
+    else if (g4) hipLaunchKernelGGL((attn_partial_kernel<I8, HDV, false, true>), grid, dim3(64 * W), lds, st, a); \
+    else         hipLaunchKernelGGL((attn_partial_kernel<I8, HDV, false, false>), grid, dim3(64 * W), lds, st, a);
     switch (a.head_dim * 2 + (kv_int8 ? 1 : 0)) {
     case 64:  ATTN_CASE(false, 32) break;
     case 65:  ATTN_CASE(true, 32) break;
