@@ -274,13 +274,20 @@ void attn_partial_kernel(AttnArgs a) {
         // 2. online softmax for column li (lanes li < GC do the useful work)
         float mx = -FLT_MAX;
 #pragma unroll
-        for (int vv = 0; vv < 16; vv++) {
-            const int key = 8 * (vv >> 2) + 4 * lg + (vv & 3);
-            const int pos = p0 + key;
-            const bool live = MT ? (key < n && pos < seq_c && pos >= lo_c) : key < n;
-            sc[vv] = live ? sc[vv] * kscl[vv] : -INFINITY;
-            mx = fmaxf(mx, sc[vv]);
+        for (int vv = 0; vv < 16; vv++) sc[vv] *= kscl[vv];
+        // key masks only where a tile can hold dead keys (uniform branch):
+        // prefill columns, or a decode tile of fewer than AT_KEYS keys
+        if (MT || n < AT_KEYS) {
+#pragma unroll
+            for (int vv = 0; vv < 16; vv++) {
+                const int key = 8 * (vv >> 2) + 4 * lg + (vv & 3);
+                const int pos = p0 + key;
+                const bool live = MT ? (key < n && pos < seq_c && pos >= lo_c) : key < n;
+                sc[vv] = live ? sc[vv] : -INFINITY;
+            }
         }
+#pragma unroll
+        for (int vv = 0; vv < 16; vv++) mx = fmaxf(mx, sc[vv]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float m_new = fmaxf(run_m, mx);
         const float corr = __expf(run_m - m_new);
