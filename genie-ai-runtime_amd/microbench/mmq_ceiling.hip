@@ -27,6 +27,11 @@
 //           (mul + fma per element)
 //   mode 13 Q4_K-style, f16 16x16 tiles with S from a v_mfma_f32_16x16x16_f16
 //           outer product (K slot 0) + fma
+//   mode 14 mode 1 with the int->float conversion done by the matrix core:
+//           the int32 accumulator starts at the bits of 12582912.0f, so the
+//           result bits are the float 12582912 + C (exact, |C| < 2^22), and
+//           one subtract replaces the cvt
+//   mode 15 mode 11 (S from the matrix cores) with that conversion
 // Throughput is reported as int8-equivalent TOPS (2 * 32 * 32 * 32 per tile
 // step) and as a fraction of the 5.0 POPS dense int8 peak.
 //
@@ -148,6 +153,23 @@ __global__ __launch_bounds__(256) void ceiling_kernel(float* out, int seed) {
             }
             ah[0] += (_Float16)1.0f;
             bx += 1e-7f;
+        } else if (MODE == 14 || MODE == 15) {
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            i32x16 magic;
+#pragma unroll
+            for (int r = 0; r < 16; r++) magic[r] = 0x4B400000;
+            const i32x16 c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, magic, 0, 0, 0);
+            f32x16 sm;
+            if (MODE == 15) {
+                const h4 as = {(_Float16)bx, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+                const h4 bs = {(_Float16)ax[it & 15], (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+                sm = __builtin_amdgcn_mfma_f32_32x32x8f16(as, bs, f32x16{}, 0, 0, 0);
+            }
+            a.x += 1;
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                acc[r] = __builtin_fmaf(MODE == 15 ? sm[r] : S[r], __int_as_float(c[r]) - 12582912.0f, acc[r]);
+            bx += 1e-7f;
         } else if (MODE == 9) {
             typedef float f32x4l __attribute__((ext_vector_type(4)));
             f32x4l c4 = {acc[0], acc[1], acc[2], acc[3]};
@@ -211,6 +233,8 @@ int main() {
         run<11>(wps, buf);
         run<12>(wps, buf);
         run<13>(wps, buf);
+        run<14>(wps, buf);
+        run<15>(wps, buf);
     }
     (void)hipFree(buf);
     return 0;
