@@ -32,6 +32,8 @@
 //           result bits are the float 12582912 + C (exact, |C| < 2^22), and
 //           one subtract replaces the cvt
 //   mode 15 mode 11 (S from the matrix cores) with that conversion
+//           (__int_as_float of the element: hipcc 7.2 compiles
+//           __builtin_bit_cast(float, v[i]) of a vector element as element 0)
 // Throughput is reported as int8-equivalent TOPS (2 * 32 * 32 * 32 per tile
 // step) and as a fraction of the 5.0 POPS dense int8 peak.
 //
