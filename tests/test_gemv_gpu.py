@@ -17,8 +17,10 @@ from gpu_util import empty_f16, empty_f32, f16_to_f64, from_dev, print_case, rel
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
 
-SHAPES = [  # (rows, K) -- BASELINE config 1/2 shapes, trimmed rows, plus odd row counts
+SHAPES = [  # (rows, K) -- BASELINE config 1/2 shapes, trimmed rows, plus odd row counts; K above
+    # 10240 takes the second activation-staging pass, 28672 is the largest K accepted
     (9728, 2560), (4096, 2560), (1024, 2560), (2560, 4096), (2560, 9728), (37, 256), (1, 512), (203, 1280),
+    (77, 12288), (40, 28672),
 ]
 
 
@@ -195,6 +197,10 @@ def test_gemv_errors(dev):
             jllm.gemv_quant(y, W, bad, x, 4, 512)
     with pytest.raises(jllm.JllmError, match="invalid"):
         jllm.gemv_quant(y, W, 12, x, 4, 300)
+    xl = to_dev(synth.x_f16(synth.rng(3), 28928))
+    Wl = to_dev(synth.q4k(synth.rng(4), 1, 28928))
+    with pytest.raises(jllm.JllmError, match="invalid"):           # K above 28672
+        jllm.gemv_quant(empty_f16(1), Wl, 12, xl, 1, 28928)
     host = torch.zeros(4 * 2 * 144, dtype=torch.uint8)           # plain host memory: no fallback
     with pytest.raises(jllm.JllmError, match="visible"):
         jllm.gemv_quant(y, host, 12, x, 4, 512)

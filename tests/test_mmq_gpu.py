@@ -98,7 +98,8 @@ def test_mmq_int32_dots_bit_exact(dev, t, M, N, K):
 
 
 @pytest.mark.parametrize("t", [12, 14])
-@pytest.mark.parametrize("M,N,K", [(300, 70, 2560), (128, 64, 1024), (97, 130, 512), (256, 2, 256)])
+@pytest.mark.parametrize("M,N,K", [(300, 70, 2560), (128, 64, 1024), (97, 130, 512), (256, 2, 256),
+                                   (70, 66, 28672)])      # the largest K: 112 super-blocks, many split ranges
 def test_mmq_f32_and_f16(dev, t, M, N, K):
     print_case("mmq", t, M, N, K)
     g = synth.rng(1000 + M + N + K + t)
@@ -155,7 +156,7 @@ def _oracle_q5_batched(W, x, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(300, 70, 2560), (128, 64, 1024), (97, 130, 512), (256, 2, 256), (1, 3, 256),
-                                   (130, 65, 4096)])
+                                   (130, 65, 4096), (40, 3, 28672)])
 def test_q5k_batched_f32_and_f16(dev, M, N, K):
     print_case("q5k_gemm", M, N, K)
     g = synth.rng(3000 + M + N + K)
