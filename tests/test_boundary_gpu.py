@@ -106,11 +106,12 @@ def test_attention_dyn_equals_static(dev, int8, seq, splits, window):
     assert torch.equal(a, b)
 
 
-def test_attention_dyn_graph_replays(dev):
+@pytest.mark.parametrize("S_", [16, 128])        # 128 key ranges run as workgroups of 4 waves
+def test_attention_dyn_graph_replays(dev, S_):
     """One captured graph (d_pos read at execution time) replayed for several
     positions equals the eager host-position call at each of them."""
     q, k, v, ks, vs = _kv_case(3, 2048, True)
-    scale, S_ = 1.0 / np.sqrt(HD), 16
+    scale = 1.0 / np.sqrt(HD)
     assert jllm.lib().jllm_hip_get_splitk_partials(H, S_, HD)
     d_pos = pos_tensor(0)
     out, ref = dev16(H * HD), dev16(H * HD)
@@ -120,7 +121,7 @@ def test_attention_dyn_graph_replays(dev):
     with torch.cuda.graph(gr):
         jllm.call("jllm_hip_flash_attention_decode_dyn", out, q, k, v, H, KV, HD, HD, d_pos, scale, 1, ks, vs, 0, S_)
     for p in (0, 31, 32, 500, 2047, 100):
-        print_case("attn_dyn_graph", p)
+        print_case("attn_dyn_graph", S_, p)
         d_pos.fill_(p)
         gr.replay()
         jllm.call("jllm_hip_flash_attention_decode_splits", ref, q, k, v, H, KV, HD, HD, p + 1, scale, 1, ks, vs, 0,
