@@ -55,6 +55,7 @@ struct StreamArgs {
     int rows_q[2], rows_r[2];       // rows per workgroup (quotient, remainder) per class
     int slots_per_wg;       // LDS block slots per workgroup (max rows per workgroup * nb, x2 for OUT_SWIGLU)
     int swiglu;             // OUT_SWIGLU launch: row sequence = the M (gate, up) row pairs
+    int ilv;                // 1: a workgroup's rounds are dealt to its waves round-robin
     GemvPre pre;
 };
 

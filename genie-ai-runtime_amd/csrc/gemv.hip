@@ -535,6 +535,45 @@ __device__ __forceinline__ RoundDesc round_desc(const StreamArgs& a, const Piece
 #ifndef JLLM_GEMV_CPOL
 #define JLLM_GEMV_CPOL 2   // nt: the weights are streamed once (measured 5 % faster than the default policy)
 #endif
+// Weight rounds go from global memory straight into a per-wave LDS ring of
+// JLLM_GEMV_DMA rounds (buffer_load ... lds) when nonzero; 0 keeps the two
+// register stages and the register -> LDS copy.
+#ifndef JLLM_GEMV_DMA
+#define JLLM_GEMV_DMA 0
+#endif
+constexpr int GEMV_NR = JLLM_GEMV_DMA > 0 ? JLLM_GEMV_DMA : 1;    // LDS round buffers per wave
+typedef __attribute__((address_space(3))) void gemv_lds_void;
+
+// The DMA instructions are issued from inline assembly: the compiler then
+// neither inserts a wait for them before every LDS read (it cannot tell
+// the ring buffers from the activation) nor counts them; the kernel waits
+// for them itself (GEMV_WAIT_VM) and issues no compiler-visible vector
+// memory load while any is in flight except where that load's own wait
+// may drain the ring.
+template <int L>
+__device__ __forceinline__ void dma_round(const RoundDesc& d, uint8_t* dst, int lane) {
+    typedef uint32_t sq4 __attribute__((ext_vector_type(4)));
+    const uint64_t b = (uint64_t)(uintptr_t)d.base;
+    const sq4 rs = {(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, (uint32_t)d.nrec, 0x00020000u};
+    const uint32_t m = (uint32_t)(uintptr_t)(gemv_lds_void*)dst;
+    const uint32_t vo = (uint32_t)lane * 16u;
+    static_assert(L == 4, "the DMA round issues four 1 KiB instructions");
+    asm volatile(
+        "s_mov_b32 m0, %1\n\ts_nop 0\n\t"
+        "buffer_load_dwordx4 %0, %2, 0 offen nt lds\n\t"
+        "s_add_u32 m0, %1, 0x400\n\ts_nop 0\n\t"
+        "buffer_load_dwordx4 %3, %2, 0 offen nt lds\n\t"
+        "s_add_u32 m0, %1, 0x800\n\ts_nop 0\n\t"
+        "buffer_load_dwordx4 %4, %2, 0 offen nt lds\n\t"
+        "s_add_u32 m0, %1, 0xc00\n\ts_nop 0\n\t"
+        "buffer_load_dwordx4 %5, %2, 0 offen nt lds"
+        :: "v"(vo), "s"(m), "s"(rs), "v"(vo + 1024u), "v"(vo + 2048u), "v"(vo + 3072u)
+        : "memory", "m0", "scc");
+}
+
+// s_waitcnt vmcnt(n) (expcnt, lgkmcnt unconstrained)
+#define GEMV_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | 0x70 | 0xF00)
+
 template <int L>
 __device__ __forceinline__ void issue_round(const RoundDesc& d, u32x4 (&v)[L], int lane) {
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)d.base, (short)0, d.nrec, 0x00020000);
@@ -623,11 +662,14 @@ __device__ __forceinline__ void wg_rows(const StreamArgs& a, int wg, int& g0, in
 // segment it touches.  Slots are indexed by the block's place in the
 // workgroup sequence.
 template <int TYPE, int L, int OUT, int T>
-__device__ __forceinline__ int make_pieces(const StreamArgs& a, int g0, int g1, int wv, Piece (&pc)[3]) {
+__device__ __forceinline__ int make_pieces(const StreamArgs& a, int g0, int g1, int wv, bool ilv, Piece (&pc)[3]) {
     constexpr int NB = WGeom<TYPE, L>::NBLK;
     const int nb = a.nb, nrow = g1 - g0;
     const int seq = nrow * nb * (OUT == OUT_SWIGLU ? 2 : 1);
-    const int j0 = (int)((int64_t)seq * wv / (T / 64)), j1 = (int)((int64_t)seq * (wv + 1) / (T / 64));
+    // a.ilv: the pieces are the whole workgroup's (its rounds are dealt to
+    // the waves round-robin, see wave_body); else the wave's own range
+    const int j0 = ilv ? 0 : (int)((int64_t)seq * wv / (T / 64));
+    const int j1 = ilv ? seq : (int)((int64_t)seq * (wv + 1) / (T / 64));
     int nr = 0;
 #pragma unroll
     for (int s = 0; s < 3; s++) {
@@ -645,6 +687,7 @@ __device__ __forceinline__ int make_pieces(const StreamArgs& a, int g0, int g1, 
         pc[s].rounds = (pc[s].nblk + NB - 1) / NB;
         nr += pc[s].rounds;
     }
+    if (ilv) nr = nr > wv ? (nr - wv + (T / 64) - 1) / (T / 64) : 0;   // this wave's share
     return nr;
 }
 
@@ -709,7 +752,14 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
     tr[7] = ((uint64_t)__builtin_amdgcn_s_getreg((31 << 11) | 20) << 32) | (uint64_t)__builtin_amdgcn_s_getreg((31 << 11) | 4);
 #endif
     Piece pc[3];
-    const int nr = make_pieces<TYPE, L, OUT, T>(a, g0, g1, wv, pc);
+    // the residual forms with K <= 8 T (one activation chunk per lane) may
+    // deal rounds round-robin; the other kernels compile without the choice
+    // (a runtime branch in every kernel measured 0.15-0.25 us slower for the
+    // launches that do not use it)
+    const bool ilv = OUT == OUT_ADD && NX == 1 && a.ilv;
+    const int nr = make_pieces<TYPE, L, OUT, T>(a, g0, g1, wv, ilv, pc);
+    // the descriptor of this wave's round k
+    auto RD = [&](int k) { return round_desc<TYPE, L>(a, pc, ilv ? wv + k * (T / 64) : k); };
     u32x4 R0[L], R1[L];
     {
         // activation (and residual) loads first, on every wave, then a barrier,
@@ -737,14 +787,22 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         if (OUT == OUT_ADD && (int)threadIdx.x < nres) rv = a.seg[0].res[g0 + threadIdx.x];
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        issue_round<L>(round_desc<TYPE, L>(a, pc, 0), R0, lane);
-        issue_round<L>(round_desc<TYPE, L>(a, pc, 1), R1, lane);
+        if constexpr (JLLM_GEMV_DMA > 0) {
+            GEMV_WAIT_VM(0);        // the activation (and residual) loads, before any DMA is in flight
+#pragma unroll
+            for (int k = 0; k < GEMV_NR; k++)
+                dma_round<L>(RD(k), lds + a.xlds_bytes + (wv * GEMV_NR + k) * (64 * 16 * L), lane);
+        } else {
+            issue_round<L>(RD(0), R0, lane);
+            issue_round<L>(RD(1), R1, lane);
+        }
         __builtin_amdgcn_sched_barrier(0);
         GT_MARK(1);
         if (PRE == PRE_RMS) {
             // sum of squares of the whole activation (K <= NX * T * 8 here):
-            // lanes, then waves through LDS (the first words of wave 0's round
-            // buffer, not written before the staging barrier below)
+            // lanes, then waves through LDS (the first words of the block
+            // slots, not written before the staging barrier below; the round
+            // buffers may already be receiving weights)
             float ss = 0.0f;
 #pragma unroll
             for (int i = 0; i < NX; i++) {
@@ -753,7 +811,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
             }
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-            float* red = (float*)(lds + a.xlds_bytes);
+            float* red = (float*)(lds + a.xlds_bytes + (T / 64) * GEMV_NR * (64 * 16 * L));
             if (lane == 0) red[wv] = ss;
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
             __builtin_amdgcn_s_barrier();
@@ -799,8 +857,30 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     GT_MARK(2);
     const uint8_t* xlds = lds;
-    uint8_t* buf = lds + a.xlds_bytes + wv * (64 * 16 * L);
-    float* slots = (float*)(lds + a.xlds_bytes + (T / 64) * (64 * 16 * L));    // the workgroup's block slots
+    uint8_t* buf = lds + a.xlds_bytes + wv * GEMV_NR * (64 * 16 * L);
+    float* slots = (float*)(lds + a.xlds_bytes + (T / 64) * GEMV_NR * (64 * 16 * L));    // the workgroup's block slots
+    if constexpr (JLLM_GEMV_DMA > 0) {
+        // Step k: wait until round k has landed in ring buffer k mod NR (the
+        // NR - 1 later rounds may still be in flight), compute it, then
+        // refill that buffer with round k + NR once its LDS reads are done.
+        // Rounds past the wave's last are empty (no bytes) but still issued,
+        // so the count of loads in flight after round k is fixed.
+        constexpr int RB = 64 * 16 * L;
+        for (int k0 = 0; k0 < nr; k0 += GEMV_NR) {
+#pragma unroll
+            for (int j = 0; j < GEMV_NR; j++) {
+                const int k = k0 + j;
+                if (k >= nr) break;
+                GEMV_WAIT_VM(L * (GEMV_NR - 1));
+                __builtin_amdgcn_wave_barrier();
+                compute_round<MMVQ, TYPE>(RD(k), buf + j * RB, xlds, slots, K, nb, lane);
+                __builtin_amdgcn_s_waitcnt(0xc07f);       // lgkmcnt(0): this buffer's reads are done
+                __builtin_amdgcn_wave_barrier();
+                dma_round<L>(RD(k + GEMV_NR), buf + j * RB, lane);
+            }
+        }
+        GEMV_WAIT_VM(0);            // the trailing (empty) rounds
+    } else {
     // Round r travels in register stage r mod 2.  Step k: compute round k
     // from the wave's LDS buffer, move round k+1 from its registers into the
     // buffer, and reuse those registers for round k+3 (round k+2 stays in
@@ -809,14 +889,14 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
     write_round<L>(buf, R0, lane);
     __builtin_amdgcn_wave_barrier();
     GT_MARK(3);
-    issue_round<L>(round_desc<TYPE, L>(a, pc, 2), R0, lane);
+    issue_round<L>(RD(2), R0, lane);
     auto step = [&](int k, u32x4 (&nxt)[L]) {
 #ifdef JLLM_GEMV_TRACE
         const int64_t gw = (int64_t)blockIdx.x * (T / 64) + wv;
         const bool rt = gw < 4096 && k < 16 && lane == 0;
         if (rt) g_gemv_rtrace[gw * 48 + k * 3] = __builtin_amdgcn_s_memrealtime();
 #endif
-        compute_round<MMVQ, TYPE>(round_desc<TYPE, L>(a, pc, k), buf, xlds, slots, K, nb, lane);
+        compute_round<MMVQ, TYPE>(RD(k), buf, xlds, slots, K, nb, lane);
         __builtin_amdgcn_wave_barrier();
 #ifdef JLLM_GEMV_TRACE
         if (rt) g_gemv_rtrace[gw * 48 + k * 3 + 1] = __builtin_amdgcn_s_memrealtime();
@@ -826,7 +906,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
 #ifdef JLLM_GEMV_TRACE
         if (rt) g_gemv_rtrace[gw * 48 + k * 3 + 2] = __builtin_amdgcn_s_memrealtime();
 #endif
-        issue_round<L>(round_desc<TYPE, L>(a, pc, k + 3), nxt, lane);
+        issue_round<L>(RD(k + 3), nxt, lane);
     };
     int k = 0;
     for (; k + 2 <= nr; k += 2) {
@@ -834,6 +914,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         step(k + 1, R0);
     }
     if (k < nr) step(k, R1);
+    }
     GT_MARK(4);
     // every wave's slots are written: LDS-only barrier (no wait on global loads)
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -925,7 +1006,7 @@ void gemv_stream_kernel(StreamArgs a_in) {
     int g0, g1;
     bool q4;
     wg_rows(a, blockIdx.x, g0, g1, q4);
-    uint16_t* res_lds = (uint16_t*)(lds + a.xlds_bytes + (T / 64) * (64 * 16 * L) + 4 * a.slots_per_wg);
+    uint16_t* res_lds = (uint16_t*)(lds + a.xlds_bytes + (T / 64) * GEMV_NR * (64 * 16 * L) + 4 * a.slots_per_wg);
     // (both bodies hold the same workgroup barriers; a workgroup serves one class)
     if constexpr (OUT == OUT_SWIGLU) {
         wave_body<MMVQ, OUT, TA, L, NX, PRE, T>(a, lds, g0, g1, lane, wv, res_lds);
@@ -1043,8 +1124,12 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     // 9.3-9.6 -> 9.0-9.2 us; not the residual form -- down 8.4 -> 8.8 -- nor
     // the RMSNorm / SwiGLU fusions) and above 64 MB (lm_head 62 -> 61 us)
     const bool mid_plain = in.pre.kind != PRE_RMS && !sw && out_kind != OUT_ADD;
-    const int threads = (wbytes < ((int64_t)12 << 20) || wbytes > ((int64_t)64 << 20) || mid_plain) ? ST_T_SMALL : ST_T;
-    const size_t wbuf = (size_t)(threads / 64) * (size_t)(64 * 16 * ST_L);
+    int threads = (wbytes < ((int64_t)12 << 20) || wbytes > ((int64_t)64 << 20) || mid_plain) ? ST_T_SMALL : ST_T;
+    // (8 waves' round buffers and a large activation may not fit one CU's LDS: then 4 waves)
+    if (threads == ST_T_SMALL &&
+        (size_t)a.xlds_bytes + (size_t)(ST_T_SMALL / 64) * GEMV_NR * (64 * 16 * ST_L) + 16384 > LDS_CU)
+        threads = ST_T;
+    const size_t wbuf = (size_t)(threads / 64) * GEMV_NR * (size_t)(64 * 16 * ST_L);
     // JLLM_GEMV_WG_PER_CU workgroups per CU when LDS allows, split between
     // the classes by bytes; a workgroup takes a contiguous row range
     int64_t grid = 0;
@@ -1062,7 +1147,7 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     };
     auto lds_of = [&]() {
         const size_t res = out_kind == OUT_ADD ? (size_t)max_rows * 2 : 0;
-        return (size_t)a.xlds_bytes + wbuf + (size_t)4 * slot_rows * max_rows * a.nb + res;
+        return (size_t)a.xlds_bytes + wbuf + (size_t)4 * std::max<int64_t>(slot_rows * max_rows * a.nb, 16) + res;
     };
     // (the residual rows of a workgroup are staged one per lane)
     auto fits = [&](int per_cu) { return (size_t)per_cu * lds_of() <= LDS_CU && !(out_kind == OUT_ADD && max_rows > threads); };
@@ -1084,7 +1169,17 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     a.wg_split = (int)w4;
     a.rows_q[0] = w4 > 0 ? (int)(rows4 / w4) : 0; a.rows_r[0] = w4 > 0 ? (int)(rows4 % w4) : 0;
     a.rows_q[1] = w6 > 0 ? (int)(rows6 / w6) : 0; a.rows_r[1] = w6 > 0 ? (int)(rows6 % w6) : 0;
-    a.slots_per_wg = (int)(slot_rows * max_rows * a.nb);
+    a.slots_per_wg = (int)std::max<int64_t>(slot_rows * max_rows * a.nb, 16);   // >= 16: the RMSNorm staging's wave sums
+    {
+        // Rounds dealt round-robin (residual forms only) when a wave's own
+        // range would hold at most two rounds: measured (graphs of 36 layers)
+        // O + residual, Q4_K 2560 x 4096, 5.46 -> 4.79 us; QKV triple
+        // unchanged; with ~6 rounds per wave it costs (gate/up pair 8.8 ->
+        // 9.0 us, Q6_K down 8.21 -> 8.37 us)
+        const int nbk = WGeom<TYPE_Q6_K, ST_L>::NBLK;     // 16 blocks per round for every type
+        const int64_t per_wave = (int64_t)a.slots_per_wg / (threads / 64);
+        a.ilv = per_wave <= 2 * nbk ? 1 : 0;
+    }
     const size_t lds = lds_of();
     const int g = (int)grid;
     a.pre = in.pre;
