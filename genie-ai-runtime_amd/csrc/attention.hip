@@ -631,12 +631,13 @@ void attn_reduce_wave_kernel(uint16_t* __restrict__ out, const float* __restrict
     const float* pm = part + (int64_t)h * S;
     const float* pl = part + (int64_t)n_heads * S + (int64_t)h * S;
     const float* pacc = part + (int64_t)n_heads * S * 2 + (int64_t)h * S * hd;
-    // the first 16 splits' accumulators are loaded with (m, l): one round
-    // trip to memory for both
+    // every split's accumulator (this kernel serves <= 32) is loaded with
+    // (m, l): one round trip to memory for all of them
+    constexpr int NB = 32;
     const bool lane_d = 2 * l < hd;
-    float2 v[16];
+    float2 v[NB];
 #pragma unroll
-    for (int i = 0; i < 16; i++)
+    for (int i = 0; i < NB; i++)
         v[i] = (i < S && lane_d) ? *(const float2*)(pacc + (int64_t)i * hd + 2 * l) : make_float2(0.0f, 0.0f);
     float mv[AT_MAXS / 64], lv[AT_MAXS / 64];
     float mx = -FLT_MAX;
@@ -663,14 +664,14 @@ void attn_reduce_wave_kernel(uint16_t* __restrict__ out, const float* __restrict
     __builtin_amdgcn_wave_barrier();
     if (!lane_d) return;
     float ox = 0.0f, oy = 0.0f;
-    for (int s0 = 0; s0 < S; s0 += 16) {
+    for (int s0 = 0; s0 < S; s0 += NB) {
         if (s0 > 0) {
 #pragma unroll
-            for (int i = 0; i < 16; i++)
+            for (int i = 0; i < NB; i++)
                 v[i] = s0 + i < S ? *(const float2*)(pacc + (int64_t)(s0 + i) * hd + 2 * l) : make_float2(0.0f, 0.0f);
         }
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
+        for (int i = 0; i < NB; i++) {
             const float wi = s0 + i < S ? sW[s0 + i] : 0.0f;
             ox += v[i].x * wi;
             oy += v[i].y * wi;
