@@ -809,8 +809,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
                 const int c = (int)threadIdx.x + T * i;
                 if (c < nch) ss += sumsq8(xv[i]);
             }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            ss = wave_sum(ss);
             float* red = (float*)(lds + a.xlds_bytes + (T / 64) * GEMV_NR * (64 * 16 * L));
             if (lane == 0) red[wv] = ss;
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");

@@ -87,6 +87,34 @@ __device__ __forceinline__ int swap_lane1(int v) {
     return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
 }
 
+// Wave64 reductions that stay out of the LDS pipe (a butterfly of
+// __shfl_xor is six dependent ds_bpermute round trips): four DPP steps
+// (lane ^ 1, lane ^ 2, then the mirrors within 8 and within 16 lanes)
+// leave each 16-lane row's result in all its lanes; the four row results
+// are read out and combined in a fixed order, so every lane returns the
+// same value.  All 64 lanes must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_mov_f<0xB1>(v);     // quad_perm [1,0,3,2]
+    v += dpp_mov_f<0x4E>(v);     // quad_perm [2,3,0,1]
+    v += dpp_mov_f<0x141>(v);    // row_half_mirror
+    v += dpp_mov_f<0x140>(v);    // row_mirror
+    return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_mov_f<0xB1>(v));
+    v = fmaxf(v, dpp_mov_f<0x4E>(v));
+    v = fmaxf(v, dpp_mov_f<0x141>(v));
+    v = fmaxf(v, dpp_mov_f<0x140>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {
 #pragma unroll

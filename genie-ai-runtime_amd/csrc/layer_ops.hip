@@ -26,17 +26,6 @@ namespace jllm_hip {
 
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
 // ---------------------------------------------------------------------------
 // RMSNorm: out = half((x + res) * rrms * w), rrms = 1/sqrt(sum((x+res)^2)/dim
 // + eps).  GS threads per row (64: one wave per row for head-sized rows, 256:

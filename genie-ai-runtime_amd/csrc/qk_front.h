@@ -11,16 +11,8 @@
 
 namespace jllm_hip {
 
-__device__ __forceinline__ float front_wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-__device__ __forceinline__ float front_wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
+__device__ __forceinline__ float front_wave_sum(float v) { return wave_sum(v); }
+__device__ __forceinline__ float front_wave_max(float v) { return wave_max(v); }
 
 __device__ __forceinline__ void front_rotate(float v0, float v1, float c, float s, float& r0, float& r1) {
 #pragma clang fp contract(off)
