@@ -581,8 +581,7 @@ void attn_reduce_kernel(uint16_t* __restrict__ out, const float* __restrict__ pa
     const float m = t < S ? pm[t] : -FLT_MAX;
     const float lv = t < S ? pl[t] : 0.0f;
     float mx = m;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mx = wave_max(mx);
     if (l == 0) sRed[w] = mx;
     __syncthreads();
     mx = sRed[0];
@@ -591,8 +590,7 @@ void attn_reduce_kernel(uint16_t* __restrict__ out, const float* __restrict__ pa
     const float wgt = t < S ? expf(m - mx) : 0.0f;
     if (t < AT_MAXS) sW[t] = wgt;
     float L = lv * wgt;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+    L = wave_sum(L);
     __syncthreads();
     if (l == 0) sRed[w] = L;
     __syncthreads();
@@ -648,8 +646,7 @@ void attn_reduce_wave_kernel(uint16_t* __restrict__ out, const float* __restrict
         lv[i] = sp < S ? pl[sp] : 0.0f;
         mx = fmaxf(mx, mv[i]);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mx = wave_max(mx);
     float L = 0.0f;
 #pragma unroll
     for (int i = 0; i < AT_MAXS / 64; i++) {
@@ -657,8 +654,7 @@ void attn_reduce_wave_kernel(uint16_t* __restrict__ out, const float* __restrict
         sW[l + 64 * i] = wgt;
         L += lv[i] * wgt;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+    L = wave_sum(L);
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();

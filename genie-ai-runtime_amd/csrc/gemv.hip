@@ -933,7 +933,8 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
             }
             vg += dpp_x1(vg); vu += dpp_x1(vu);
             vg += dpp_x2(vg); vu += dpp_x2(vu);
-            vg += __shfl_xor(vg, 4, 64); vu += __shfl_xor(vu, 4, 64);
+            // the other quad of the 8 lanes (every lane of a quad holds its sum)
+            vg += dpp_mov_f<0x141>(vg); vu += dpp_mov_f<0x141>(vu);
             if (j == 0 && t < nrow) {
                 // half(silu(g) * u) of the half-rounded pair outputs (swiglu_kernel, convert.cu:85-112)
 #pragma clang fp contract(off)
@@ -963,7 +964,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         }
         v += dpp_x1(v);
         v += dpp_x2(v);
-        v += __shfl_xor(v, 4, 64);
+        v += dpp_mov_f<0x141>(v);      // the other quad of the 8 lanes (row_half_mirror)
         if (j == 0 && t < nrow) {
             const int g = g0 + t;
             const int sg = g >= a.row_off[1] ? (g >= a.row_off[2] ? 2 : 1) : 0;

@@ -410,6 +410,26 @@ __device__ __forceinline__ void arg_merge(float ov, int oi, float& bv, int& bi) 
     if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
 }
 
+// the wave's best (value, index) in every lane: DPP steps within each
+// 16-lane row, then the four row winners (arg_merge is a total order, so
+// the merge order does not change the result)
+__device__ __forceinline__ void wave_arg_merge(float& bv, int& bi) {
+#define JLLM_AM_STEP(C) arg_merge(dpp_mov_f<C>(bv), __builtin_amdgcn_mov_dpp(bi, C, 0xF, 0xF, false), bv, bi)
+    JLLM_AM_STEP(0xB1);
+    JLLM_AM_STEP(0x4E);
+    JLLM_AM_STEP(0x141);
+    JLLM_AM_STEP(0x140);
+#undef JLLM_AM_STEP
+    float v0 = readlane_f(bv, 0), v1 = readlane_f(bv, 16), v2 = readlane_f(bv, 32), v3 = readlane_f(bv, 48);
+    int i0 = __builtin_amdgcn_readlane(bi, 0), i1 = __builtin_amdgcn_readlane(bi, 16);
+    int i2 = __builtin_amdgcn_readlane(bi, 32), i3 = __builtin_amdgcn_readlane(bi, 48);
+    arg_merge(v1, i1, v0, i0);
+    arg_merge(v3, i3, v2, i2);
+    arg_merge(v2, i2, v0, i0);
+    bv = v0;
+    bi = i0;
+}
+
 __global__ __launch_bounds__(AM_THREADS) void argmax_part_kernel(const float* __restrict__ x, int n, int chunk) {
     __shared__ float sv[AM_THREADS / 64];
     __shared__ int si[AM_THREADS / 64];
@@ -430,8 +450,7 @@ __global__ __launch_bounds__(AM_THREADS) void argmax_part_kernel(const float* __
     } else {
         for (int j = b0 + t; j < b1; j += AM_THREADS) arg_better(x[j], j, bv, bi);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) arg_merge(__shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64), bv, bi);
+    wave_arg_merge(bv, bi);
     if ((t & 63) == 0) { sv[t >> 6] = bv; si[t >> 6] = bi; }
     __syncthreads();
     if (t == 0) {
@@ -446,8 +465,7 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(int32_t* out, int nblo
     float bv = -INFINITY;
     int bi = INT_MAX;
     for (int b = t; b < nblocks; b += 64) arg_merge(g_am_val[b], g_am_idx[b], bv, bi);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) arg_merge(__shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64), bv, bi);
+    wave_arg_merge(bv, bi);
     if (t == 0) out[0] = bi == INT_MAX ? 0 : bi;
 }
 
