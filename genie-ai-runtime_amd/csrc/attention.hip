@@ -288,7 +288,11 @@ void attn_partial_kernel(AttnArgs a) {
         }
 #pragma unroll
         for (int vv = 0; vv < 16; vv++) mx = fmaxf(mx, sc[vv]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        {
+            float a0, a1;
+            wave_halves(mx, a0, a1);
+            mx = fmaxf(a0, a1);
+        }
         const float m_new = fmaxf(run_m, mx);
         const float corr = __expf(run_m - m_new);
         float ps = 0.0f;
@@ -303,7 +307,11 @@ void attn_partial_kernel(AttnArgs a) {
             hi2[vv / 2] = h2_bits(half2_t{h0, h1});
             lo2[vv / 2] = h2_bits(half2_t{l0, l1});
         }
-        ps += __shfl_xor(ps, 32, 64);
+        {
+            float a0, a1;
+            wave_halves(ps, a0, a1);
+            ps = a0 + a1;
+        }
         run_l = run_l * corr + ps;
         run_m = m_new;
         if (li < GC) {

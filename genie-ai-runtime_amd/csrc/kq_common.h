@@ -115,6 +115,16 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
+// The values of lanes l & 31 and (l & 31) + 32 -- lane l and lane l ^ 32 --
+// in every lane, lower half's first (one v_permlane32_swap, no LDS pipe);
+// a commutative op of the two equals op(v, __shfl_xor(v, 32)) bit for bit.
+__device__ __forceinline__ void wave_halves(float v, float& lo, float& hi) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto s = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    lo = __builtin_bit_cast(float, (unsigned)s[0]);
+    hi = __builtin_bit_cast(float, (unsigned)s[1]);
+}
+
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {
 #pragma unroll
