@@ -1120,10 +1120,12 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     a.xlds_bytes = (int)((gemv_lds_bytes(mmvq, a.K) + 15) & ~(size_t)15);
     const int64_t wbytes = bytes4 + bytes6;
     // 512 threads (the same waves per CU in half the workgroups) where it
-    // measured faster: under 12 MB, plain products of 12-64 MB (gate/up pair
-    // 9.3-9.6 -> 9.0-9.2 us; not the residual form -- down 8.4 -> 8.8 -- nor
-    // the RMSNorm / SwiGLU fusions) and above 64 MB (lm_head 62 -> 61 us)
-    const bool mid_plain = in.pre.kind != PRE_RMS && !sw && out_kind != OUT_ADD;
+    // measured faster: under 12 MB, above 64 MB (lm_head 62 -> 61 us) and in
+    // between for every product except the residual form from 16 MB up
+    // (gate/up pair 9.3-9.6 -> 9.0-9.2 us, RMSNorm + gate/up + SwiGLU 8.59 ->
+    // 8.52 us, Q4_K down + residual (14 MB) 7.07 -> 6.84 us; Q6_K down +
+    // residual (20 MB) 8.19 -> 8.33 us, so 256 there)
+    const bool mid_plain = out_kind != OUT_ADD || wbytes < ((int64_t)16 << 20);
     int threads = (wbytes < ((int64_t)12 << 20) || wbytes > ((int64_t)64 << 20) || mid_plain) ? ST_T_SMALL : ST_T;
     // (8 waves' round buffers and a large activation may not fit one CU's LDS: then 4 waves)
     if (threads == ST_T_SMALL &&
