@@ -157,7 +157,9 @@ void attn_partial_kernel(AttnArgs a) {
     uint8_t* smem = smem_wg + (size_t)wv * wave_lds;
     uint64_t tr[4] = {0, 0, 0, 0};
     AT_MARK(0);
-    const int kvh = blockIdx.x, split = blockIdx.y, tok0 = MT ? blockIdx.z * a.tq : blockIdx.z;
+    // prefill: the last token blocks (the most key tiles) are dispatched first
+    const int kvh = blockIdx.x, split = blockIdx.y;
+    const int tok0 = MT ? ((int)gridDim.z - 1 - (int)blockIdx.z) * a.tq : blockIdx.z;
     const int aseq = (!MT && a.pos_dev) ? __builtin_amdgcn_readfirstlane(*a.pos_dev) + 1 : a.seq;
     const int G = a.n_heads / a.n_kv;
     const int ntok = MT ? min(a.tq, a.tokens - tok0) : 1;       // tokens of this wave
