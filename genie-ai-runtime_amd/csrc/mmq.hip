@@ -137,12 +137,14 @@ __global__ __launch_bounds__(256) void quantize_mmq_f16_kernel(const uint16_t* _
     float amax = 0.0f, t[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) { amax = fmaxf(amax, fabsf(v[e])); t[e] = v[e]; }
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    // lane ^ 1 and lane ^ 2 within the block's 4 lanes through DPP quad
+    // permutes (the same partner values and add order as the shuffles)
+    amax = fmaxf(amax, dpp_mov_f<0xB1>(amax));
+    amax = fmaxf(amax, dpp_mov_f<0x4E>(amax));
 #pragma unroll
-    for (int e = 0; e < 8; e++) t[e] += __shfl_xor(t[e], 2, 64);       // index bit 4
+    for (int e = 0; e < 8; e++) t[e] += dpp_mov_f<0x4E>(t[e]);       // index bit 4 (lane ^ 2)
 #pragma unroll
-    for (int e = 0; e < 8; e++) t[e] += __shfl_xor(t[e], 1, 64);       // index bit 3
+    for (int e = 0; e < 8; e++) t[e] += dpp_mov_f<0xB1>(t[e]);       // index bit 3 (lane ^ 1)
     const float s2[4] = {t[0] + t[4], t[1] + t[5], t[2] + t[6], t[3] + t[7]};
     const float s1[2] = {s2[0] + s2[2], s2[1] + s2[3]};
     const float sum = s1[0] + s1[1];
