@@ -106,6 +106,23 @@ def test_gemv_add(dev, t):
     assert ok, err
 
 
+@pytest.mark.parametrize("t,rows,K", [(12, 1, 256), (12, 7, 768), (12, 100, 1024), (14, 333, 2560),
+                                      (13, 1000, 4096), (12, 2560, 9728), (14, 4096, 1280), (12, 5000, 2560)])
+def test_gemv_add_shapes(dev, t, rows, K):
+    """Residual GEMV at ragged shapes: one row, rows that do not fill a
+    workgroup's waves (rounds dealt round-robin), both workgroup sizes (the
+    Q4_K 2560 x 9728 down takes 512 threads, the larger Q6_K ones 256)."""
+    print_case("gemv_add_shape", t, rows, K)
+    W, x = _case(t, rows, K, 410 + rows)
+    res = synth.x_f16(synth.rng(411 + rows), rows)
+    y = empty_f16(rows)
+    jllm.gemv_quant_add(y, to_dev(W), t, to_dev(x), to_dev(res), rows, K)
+    proj = oracle.gemv_quant_cpu(W, t, x, rows, K).astype(np.float16).astype(np.float32)
+    want = proj + f16_to_f64(res).astype(np.float32)
+    ok, err = _close_f16(from_dev(y, np.uint16), want)
+    assert ok, err
+
+
 def test_gemv_pair_and_triple(dev):
     K = 2560
     g = synth.rng(500)
