@@ -209,7 +209,7 @@ def test_argmax(dev, n):
     g = synth.rng(n)
     x = g.standard_normal(n).astype(np.float32)
     out = torch.zeros(1, dtype=torch.int32, device=dev)
-    for case in range(4):
+    for case in range(6):
         if case == 1:
             x[n // 3] = x[n - 1] = 50.0                      # tie: the lower index wins
         if case == 2:
@@ -217,6 +217,15 @@ def test_argmax(dev, n):
             x[0] = np.nan
         if case == 3:
             x[:] = np.nan
+        if case == 4:
+            # ties inside one wave of the first workgroup, across the lane
+            # rows and halves the reduction merges (element 4 t is lane t's)
+            x = g.standard_normal(n).astype(np.float32)
+            for i in (4 * 50, 4 * 3, 4 * 33, 4 * 17):
+                if i < n:
+                    x[i] = 60.0
+        if case == 5:
+            x = np.full(n, -np.inf, np.float32)              # no finite value: index 0
         jllm.call("jllm_hip_argmax_f32", out, to_dev(x), n)
         assert int(from_dev(out)[0]) == oracle.argmax(x), case
 
