@@ -535,45 +535,6 @@ __device__ __forceinline__ RoundDesc round_desc(const StreamArgs& a, const Piece
 #ifndef JLLM_GEMV_CPOL
 #define JLLM_GEMV_CPOL 2   // nt: the weights are streamed once (measured 5 % faster than the default policy)
 #endif
-// Weight rounds go from global memory straight into a per-wave LDS ring of
-// JLLM_GEMV_DMA rounds (buffer_load ... lds) when nonzero; 0 keeps the two
-// register stages and the register -> LDS copy.
-#ifndef JLLM_GEMV_DMA
-#define JLLM_GEMV_DMA 0
-#endif
-constexpr int GEMV_NR = JLLM_GEMV_DMA > 0 ? JLLM_GEMV_DMA : 1;    // LDS round buffers per wave
-typedef __attribute__((address_space(3))) void gemv_lds_void;
-
-// The DMA instructions are issued from inline assembly: the compiler then
-// neither inserts a wait for them before every LDS read (it cannot tell
-// the ring buffers from the activation) nor counts them; the kernel waits
-// for them itself (GEMV_WAIT_VM) and issues no compiler-visible vector
-// memory load while any is in flight except where that load's own wait
-// may drain the ring.
-template <int L>
-__device__ __forceinline__ void dma_round(const RoundDesc& d, uint8_t* dst, int lane) {
-    typedef uint32_t sq4 __attribute__((ext_vector_type(4)));
-    const uint64_t b = (uint64_t)(uintptr_t)d.base;
-    const sq4 rs = {(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, (uint32_t)d.nrec, 0x00020000u};
-    const uint32_t m = (uint32_t)(uintptr_t)(gemv_lds_void*)dst;
-    const uint32_t vo = (uint32_t)lane * 16u;
-    static_assert(L == 4, "the DMA round issues four 1 KiB instructions");
-    asm volatile(
-        "s_mov_b32 m0, %1\n\ts_nop 0\n\t"
-        "buffer_load_dwordx4 %0, %2, 0 offen nt lds\n\t"
-        "s_add_u32 m0, %1, 0x400\n\ts_nop 0\n\t"
-        "buffer_load_dwordx4 %3, %2, 0 offen nt lds\n\t"
-        "s_add_u32 m0, %1, 0x800\n\ts_nop 0\n\t"
-        "buffer_load_dwordx4 %4, %2, 0 offen nt lds\n\t"
-        "s_add_u32 m0, %1, 0xc00\n\ts_nop 0\n\t"
-        "buffer_load_dwordx4 %5, %2, 0 offen nt lds"
-        :: "v"(vo), "s"(m), "s"(rs), "v"(vo + 1024u), "v"(vo + 2048u), "v"(vo + 3072u)
-        : "memory", "m0", "scc");
-}
-
-// s_waitcnt vmcnt(n) (expcnt, lgkmcnt unconstrained)
-#define GEMV_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | 0x70 | 0xF00)
-
 template <int L>
 __device__ __forceinline__ void issue_round(const RoundDesc& d, u32x4 (&v)[L], int lane) {
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)d.base, (short)0, d.nrec, 0x00020000);
@@ -787,15 +748,8 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         if (OUT == OUT_ADD && (int)threadIdx.x < nres) rv = a.seg[0].res[g0 + threadIdx.x];
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (JLLM_GEMV_DMA > 0) {
-            GEMV_WAIT_VM(0);        // the activation (and residual) loads, before any DMA is in flight
-#pragma unroll
-            for (int k = 0; k < GEMV_NR; k++)
-                dma_round<L>(RD(k), lds + a.xlds_bytes + (wv * GEMV_NR + k) * (64 * 16 * L), lane);
-        } else {
-            issue_round<L>(RD(0), R0, lane);
-            issue_round<L>(RD(1), R1, lane);
-        }
+        issue_round<L>(RD(0), R0, lane);
+        issue_round<L>(RD(1), R1, lane);
         __builtin_amdgcn_sched_barrier(0);
         GT_MARK(1);
         if (PRE == PRE_RMS) {
@@ -810,7 +764,7 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
                 if (c < nch) ss += sumsq8(xv[i]);
             }
             ss = wave_sum(ss);
-            float* red = (float*)(lds + a.xlds_bytes + (T / 64) * GEMV_NR * (64 * 16 * L));
+            float* red = (float*)(lds + a.xlds_bytes + (T / 64) * (64 * 16 * L));
             if (lane == 0) red[wv] = ss;
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
             __builtin_amdgcn_s_barrier();
@@ -856,30 +810,8 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     GT_MARK(2);
     const uint8_t* xlds = lds;
-    uint8_t* buf = lds + a.xlds_bytes + wv * GEMV_NR * (64 * 16 * L);
-    float* slots = (float*)(lds + a.xlds_bytes + (T / 64) * GEMV_NR * (64 * 16 * L));    // the workgroup's block slots
-    if constexpr (JLLM_GEMV_DMA > 0) {
-        // Step k: wait until round k has landed in ring buffer k mod NR (the
-        // NR - 1 later rounds may still be in flight), compute it, then
-        // refill that buffer with round k + NR once its LDS reads are done.
-        // Rounds past the wave's last are empty (no bytes) but still issued,
-        // so the count of loads in flight after round k is fixed.
-        constexpr int RB = 64 * 16 * L;
-        for (int k0 = 0; k0 < nr; k0 += GEMV_NR) {
-#pragma unroll
-            for (int j = 0; j < GEMV_NR; j++) {
-                const int k = k0 + j;
-                if (k >= nr) break;
-                GEMV_WAIT_VM(L * (GEMV_NR - 1));
-                __builtin_amdgcn_wave_barrier();
-                compute_round<MMVQ, TYPE>(RD(k), buf + j * RB, xlds, slots, K, nb, lane);
-                __builtin_amdgcn_s_waitcnt(0xc07f);       // lgkmcnt(0): this buffer's reads are done
-                __builtin_amdgcn_wave_barrier();
-                dma_round<L>(RD(k + GEMV_NR), buf + j * RB, lane);
-            }
-        }
-        GEMV_WAIT_VM(0);            // the trailing (empty) rounds
-    } else {
+    uint8_t* buf = lds + a.xlds_bytes + wv * (64 * 16 * L);
+    float* slots = (float*)(lds + a.xlds_bytes + (T / 64) * (64 * 16 * L));    // the workgroup's block slots
     // Round r travels in register stage r mod 2.  Step k: compute round k
     // from the wave's LDS buffer, move round k+1 from its registers into the
     // buffer, and reuse those registers for round k+3 (round k+2 stays in
@@ -913,7 +845,6 @@ __device__ __forceinline__ void wave_body(const StreamArgs& a, uint8_t* lds, int
         step(k + 1, R0);
     }
     if (k < nr) step(k, R1);
-    }
     GT_MARK(4);
     // every wave's slots are written: LDS-only barrier (no wait on global loads)
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -1006,7 +937,7 @@ void gemv_stream_kernel(StreamArgs a_in) {
     int g0, g1;
     bool q4;
     wg_rows(a, blockIdx.x, g0, g1, q4);
-    uint16_t* res_lds = (uint16_t*)(lds + a.xlds_bytes + (T / 64) * GEMV_NR * (64 * 16 * L) + 4 * a.slots_per_wg);
+    uint16_t* res_lds = (uint16_t*)(lds + a.xlds_bytes + (T / 64) * (64 * 16 * L) + 4 * a.slots_per_wg);
     // (both bodies hold the same workgroup barriers; a workgroup serves one class)
     if constexpr (OUT == OUT_SWIGLU) {
         wave_body<MMVQ, OUT, TA, L, NX, PRE, T>(a, lds, g0, g1, lane, wv, res_lds);
@@ -1129,9 +1060,9 @@ hipError_t gemv_launch(const GemvArgs& in, bool mmvq, int out_kind, hipStream_t 
     int threads = (wbytes < ((int64_t)12 << 20) || wbytes > ((int64_t)64 << 20) || mid_plain) ? ST_T_SMALL : ST_T;
     // (8 waves' round buffers and a large activation may not fit one CU's LDS: then 4 waves)
     if (threads == ST_T_SMALL &&
-        (size_t)a.xlds_bytes + (size_t)(ST_T_SMALL / 64) * GEMV_NR * (64 * 16 * ST_L) + 16384 > LDS_CU)
+        (size_t)a.xlds_bytes + (size_t)(ST_T_SMALL / 64) * (64 * 16 * ST_L) + 16384 > LDS_CU)
         threads = ST_T;
-    const size_t wbuf = (size_t)(threads / 64) * GEMV_NR * (size_t)(64 * 16 * ST_L);
+    const size_t wbuf = (size_t)(threads / 64) * (size_t)(64 * 16 * ST_L);
     // JLLM_GEMV_WG_PER_CU workgroups per CU when LDS allows, split between
     // the classes by bytes; a workgroup takes a contiguous row range
     int64_t grid = 0;
