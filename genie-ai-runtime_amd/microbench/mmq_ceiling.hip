@@ -34,6 +34,9 @@
 //   mode 15 mode 11 (S from the matrix cores) with that conversion
 //           (__int_as_float of the element: hipcc 7.2 compiles
 //           __builtin_bit_cast(float, v[i]) of a vector element as element 0)
+//   mode 16 Q4_K-style, f16 32x32 tiles with S from the matrix cores: two
+//           v_mfma_f32_32x32x16_f16 (exact dots) + v_mfma_f32_32x32x8_f16
+//           outer product (S) + fma (no cvt)
 // Throughput is reported as int8-equivalent TOPS (2 * 32 * 32 * 32 per tile
 // step) and as a fraction of the 5.0 POPS dense int8 peak.
 //
@@ -172,6 +175,17 @@ __global__ __launch_bounds__(256) void ceiling_kernel(float* out, int seed) {
             for (int r = 0; r < 16; r++)
                 acc[r] = __builtin_fmaf(MODE == 15 ? sm[r] : S[r], __int_as_float(c[r]) - 12582912.0f, acc[r]);
             bx += 1e-7f;
+        } else if (MODE == 16) {
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            f32x16 c = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, f32x16{}, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_32x32x16_f16(bh, ah, c, 0, 0, 0);
+            const h4 as = {(_Float16)bx, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+            const h4 bs = {(_Float16)ax[it & 15], (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+            const f32x16 sm = __builtin_amdgcn_mfma_f32_32x32x8f16(as, bs, f32x16{}, 0, 0, 0);
+            ah[0] += (_Float16)1.0f;
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[r] = __builtin_fmaf(sm[r], c[r], acc[r]);
+            bx += 1e-7f;
         } else if (MODE == 9) {
             typedef float f32x4l __attribute__((ext_vector_type(4)));
             f32x4l c4 = {acc[0], acc[1], acc[2], acc[3]};
@@ -237,6 +251,7 @@ int main() {
         run<13>(wps, buf);
         run<14>(wps, buf);
         run<15>(wps, buf);
+        run<16>(wps, buf);
     }
     (void)hipFree(buf);
     return 0;
