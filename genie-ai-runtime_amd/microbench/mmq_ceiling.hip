@@ -37,6 +37,8 @@
 //   mode 16 Q4_K-style, f16 32x32 tiles with S from the matrix cores: two
 //           v_mfma_f32_32x32x16_f16 (exact dots) + v_mfma_f32_32x32x8_f16
 //           outer product (S) + fma (no cvt)
+//   mode 17 f16 MFMA 32x32x16 only, accumulating in place (two instructions
+//           per step, no VALU: mode 4 adds every result into acc as well)
 // Throughput is reported as int8-equivalent TOPS (2 * 32 * 32 * 32 per tile
 // step) and as a fraction of the 5.0 POPS dense int8 peak.
 //
@@ -186,6 +188,9 @@ __global__ __launch_bounds__(256) void ceiling_kernel(float* out, int seed) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[r] = __builtin_fmaf(sm[r], c[r], acc[r]);
             bx += 1e-7f;
+        } else if (MODE == 17) {
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(bh, ah, acc, 0, 0, 0);
         } else if (MODE == 9) {
             typedef float f32x4l __attribute__((ext_vector_type(4)));
             f32x4l c4 = {acc[0], acc[1], acc[2], acc[3]};
@@ -252,6 +257,7 @@ int main() {
         run<14>(wps, buf);
         run<15>(wps, buf);
         run<16>(wps, buf);
+        run<17>(wps, buf);
     }
     (void)hipFree(buf);
     return 0;
