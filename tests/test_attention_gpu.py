@@ -50,7 +50,10 @@ def _close(got, want):
 
 
 @pytest.mark.parametrize("ctx,window", [(1, 0), (37, 0), (64, 0), (100, 0), (512, 0), (4096, 0), (8192, 0),
-                                        (4096, 512), (8192, 512), (300, 64), (200, 500)])
+                                        (4096, 512), (8192, 512), (300, 64), (200, 500),
+                                        # ragged key ranges around the 4-wave groups (64 ranges) and the
+                                        # 128-range cap: a partial last range, a partial last group
+                                        (2047, 0), (2049, 0), (6001, 0), (8193, 0), (5000, 1000)])
 def test_attention_vs_oracle(dev, ctx, window):
     print_case("attn", ctx, window)
     q, k, v, ks, vs = _case(ctx + window, ctx)
