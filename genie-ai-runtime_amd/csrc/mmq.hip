@@ -12,25 +12,29 @@
 //
 // Matrix-core mapping.  The reference scales every 32-wide int32 dot in
 // fp32, and on gfx950 one fp32 VALU op costs as much as ~64 int8 MACs on the
-// matrix cores, so an int8-MFMA kernel is bound by that epilogue.  Here the
-// dots run on v_mfma_f32_32x32x16_f16 instead: weight codes (0..15, or
-// (q-32)*sc with |.| <= 1024) and activation codes (-127..127) are exact in
-// fp16, their products are exact in fp32 and every partial sum stays below
-// 2^24, so the fp32 accumulator of a 32-wide dot IS the int32 dot (or, for
-// Q6_K, exactly C_g0*sc_g0 + C_g1*sc_g1).  What is left for the VALU is one
-// fma per dot: the Q4_K scale products half(d*sc_j)*d8_j (exact: two fp16
-// values) come from a second MFMA as an outer product, the min term
-// sum_j half(-dmin*m_j)*sumx_j is a K = 8 MFMA per super-block, and Q6_K's
-// per-token d8 is a lane constant.  The activation quantiser writes its
-// codes directly as fp16 (same values as the reference's int8 codes), so
-// only the weights are converted in the kernel (nibble / byte -> fp16 with
-// v_perm_b32 and one packed-fp16 subtract).
+// matrix cores, so both kernels are bound by that epilogue, not by the
+// matrix cores.
+//   Q4_K: each 32-wide dot is one v_mfma_i32_32x32x32_i8 per 32 x 32 tile
+//         (exact int32, K = 32 = one sub-block); the scale products
+//         half(d*sc_j)*d8_j (exact: two fp16 values) come from a
+//         v_mfma_f32_32x32x8_f16 outer product, so each element costs one
+//         cvt and one fma per sub-block; the min term
+//         sum_j half(-dmin*m_j)*sumx_j is one K = 8 f16 MFMA per half
+//         super-block.  Activation codes are int8.
+//   Q6_K: (q-32)*sc (|.| <= 1024) and the activation codes (-127..127) are
+//         exact in fp16, their products exact in fp32, every partial sum
+//         below 2^24, so v_mfma_f32_32x32x16_f16 gives C_g0*sc_g0 +
+//         C_g1*sc_g1 exactly; the per-token d8 is a lane constant.
+//         Activation codes are written by the quantiser as fp16 values, and
+//         the weights are converted in the kernel (byte -> fp16 with
+//         v_perm_b32 and one packed-fp16 fma).
 //
-// A workgroup computes a 128-row x 64-token tile (4 waves, each 32 rows x
-// 64 tokens = two 32x32 MFMA tiles), staging half a super-block (128 K) of
-// weight bytes and activation codes in LDS per step, double-buffered: the
-// next step's global loads are in flight while the current one computes.  Tiles are handed out
-// so that each XCD (blockIdx % 8) works on a contiguous range of row tiles.
+// Tiles: Q4_K 128 rows x 64 tokens (4 waves of 32 x 64), Q6_K 128 x 128
+// (4 waves of 32 x 128).  The K loop runs over half super-blocks; each
+// lane's weight bytes go straight into registers one stage ahead, the
+// activation codes shared by the workgroup go from global memory straight
+// to LDS (buffer_load ... lds).  Tiles are handed out so that each XCD
+// (blockIdx % 8) works on a contiguous range of row tiles.
 #include "kq_common.h"
 #include "mmq.h"
 #include <algorithm>
@@ -49,8 +53,6 @@ typedef float f32x16m __attribute__((ext_vector_type(16)));
 constexpr int MMQ_THREADS = 256;
 constexpr int TM = 128;                 // rows per workgroup tile (4 waves x 32)
 constexpr int TN = MMQ_TILE_N;          // tokens per workgroup tile (64)
-constexpr int A4_STRIDE = 72;           // LDS bytes per row: 64 Q4_K code bytes of a half super-block + pad
-constexpr int B_STRIDE = 272;           // LDS bytes per token: 128 fp16 activation codes + pad
 
 // ---------------------------------------------------------------------------
 // activation quantiser (quantize_mmq_q8_1_ds4 / _d4, mmq_q4k_llama.cu:383-404,
@@ -94,7 +96,7 @@ hipError_t quantize_mmq_launch(const uint16_t* x, void* q8, int N, int K, int Np
 // The same quantisation (same codes, d and sum, same butterfly order) in the
 // layout the MMQ kernels read: codes as fp16 values, [K/256][Npad][256], and
 // one 32-bit scale word per 32 values, [K/32][Npad] (DS4: half d | half sum
-// << 16; D4: float d).  One thread per value, 32 lanes per block.
+// << 16; D4: float d).
 // Four lanes per 32-value block, 8 values (one 16-byte load) per lane.  The
 // block sum is added in the order of a 32-lane butterfly (xor 16, 8, 4, 2,
 // 1 over the value index), the order of the reference-layout quantiser
@@ -230,22 +232,10 @@ __device__ __forceinline__ h8m q6_to_h8_scaled(u32x2m w, _Float16 sc) {
                                      h8m{off, off, off, off, off, off, off, off});
 }
 
-// 8 Q4_K nibbles (low or high halves of 8 code bytes) -> 8 fp16 values 0..15
-__device__ __forceinline__ h8m nib_lo_h8(u32x2m w) { return bytes_to_h8(w & 0x0F0F0F0Fu, 1024.0f); }
-__device__ __forceinline__ h8m nib_hi_h8(u32x2m w) { return bytes_to_h8((w >> 4u) & 0x0F0F0F0Fu, 1024.0f); }
-// 8 signed bytes -> 8 fp16 values (-128..127): bias the bytes by 128 first
-__device__ __forceinline__ h8m i8_to_h8(u32x2m w) { return bytes_to_h8(w ^ 0x80808080u, 1152.0f); }
 
 __device__ __forceinline__ f32x16m mfma16(h8m a, h8m b, f32x16m c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
-
-// ---------------------------------------------------------------------------
-// Pipeline shared by both kernels: the K loop runs over half super-blocks
-// ("stages" of 128 weights).  Stage k+1's global loads are issued into
-// registers before stage k is computed from LDS buffer k&1, then written to
-// LDS buffer (k+1)&1; one barrier per stage.  Per-super-block scales live in
-// a second two-slot ring indexed by the super-block's parity.
 
 // ---------------------------------------------------------------------------
 // Q4_K on the int8 matrix cores.
