@@ -33,6 +33,10 @@
 #include "kq_common.h"
 #include "attention.h"
 
+#ifndef ATTN_RED_XCD
+#define ATTN_RED_XCD 1
+#endif
+
 namespace jllm_hip {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -568,13 +572,30 @@ void attn_partial_kernel(AttnArgs a) {
 // waves per head: the split weights go to LDS, then wave w sums the splits
 // s = w, w + 8, ... for two d per lane (all its partial loads in flight at
 // once), and the 8 wave sums are added in a fixed order.
+// The head a combination workgroup takes.  Workgroup b of a launch runs on
+// XCD b % 8, and the partial kernel's workgroup (kvh, range) has linear
+// index kvh + n_kv * range, so with n_kv a multiple of 8 every key range of
+// KV head kvh ran on XCD kvh % 8; handing workgroup b the head (b % n_kv) *
+// G + b / n_kv puts the combination on that XCD too, where the partials may
+// still sit in its L2.  (Any n_kv: still a permutation of the heads.)
+__device__ __forceinline__ int red_head(int n_heads, int n_kv) {
+#if ATTN_RED_XCD
+    const int b = blockIdx.x;
+    return (b % n_kv) * (n_heads / n_kv) + b / n_kv;
+#else
+    (void)n_heads; (void)n_kv;
+    return blockIdx.x;
+#endif
+}
+
 constexpr int AT_RED_THREADS = 512;
 __global__ __launch_bounds__(AT_RED_THREADS)
-void attn_reduce_kernel(uint16_t* __restrict__ out, const float* __restrict__ part, int n_heads, int hd, int S) {
+void attn_reduce_kernel(uint16_t* __restrict__ out, const float* __restrict__ part, int n_heads, int n_kv, int hd,
+                        int S) {
     __shared__ float sW[AT_MAXS];
     __shared__ float sRed[AT_RED_THREADS / 64];
     __shared__ float sSum[AT_RED_THREADS / 64][AT_MAXHD];
-    const int h = blockIdx.x, t = threadIdx.x, w = t >> 6, l = t & 63;
+    const int h = red_head(n_heads, n_kv), t = threadIdx.x, w = t >> 6, l = t & 63;
     const float* pm = part + (int64_t)h * S;
     const float* pl = part + (int64_t)n_heads * S + (int64_t)h * S;
     const float* pacc = part + (int64_t)n_heads * S * 2 + (int64_t)h * S * hd;
@@ -633,9 +654,10 @@ void attn_reduce_kernel(uint16_t* __restrict__ out, const float* __restrict__ pa
 // ... (m, l) and then sums the acc of every split for d = 2l, 2l+1 in split
 // order; no workgroup barriers.
 __global__ __launch_bounds__(64)
-void attn_reduce_wave_kernel(uint16_t* __restrict__ out, const float* __restrict__ part, int n_heads, int hd, int S) {
+void attn_reduce_wave_kernel(uint16_t* __restrict__ out, const float* __restrict__ part, int n_heads, int n_kv, int hd,
+                             int S) {
     __shared__ float sW[AT_MAXS];
-    const int h = blockIdx.x, l = threadIdx.x;
+    const int h = red_head(n_heads, n_kv), l = threadIdx.x;
     const float* pm = part + (int64_t)h * S;
     const float* pl = part + (int64_t)n_heads * S + (int64_t)h * S;
     const float* pacc = part + (int64_t)n_heads * S * 2 + (int64_t)h * S * hd;
@@ -725,10 +747,10 @@ hipError_t attn_launch(const AttnArgs& a, bool kv_int8, hipStream_t st) {
     // reduce), 8 waves per head beyond (128 splits: 13.0 us against 16.1)
     if (a.n_splits <= 32)
         hipLaunchKernelGGL(attn_reduce_wave_kernel, dim3(a.n_heads), dim3(64), 0, st, a.out, (const float*)a.part,
-                           a.n_heads, a.head_dim, a.n_splits);
+                           a.n_heads, a.n_kv, a.head_dim, a.n_splits);
     else
         hipLaunchKernelGGL(attn_reduce_kernel, dim3(a.n_heads), dim3(AT_RED_THREADS), 0, st, a.out,
-                           (const float*)a.part, a.n_heads, a.head_dim, a.n_splits);
+                           (const float*)a.part, a.n_heads, a.n_kv, a.head_dim, a.n_splits);
     return hipGetLastError();
 }
 
