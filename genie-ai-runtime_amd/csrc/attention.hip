@@ -30,6 +30,8 @@
 // a high and a low fp16 part stacked as extra rows of the A operand, so the
 // P.V products keep ~22 bits.
 #include <float.h>
+#include <stdlib.h>
+#include <string.h>
 #include "kq_common.h"
 #include "attention.h"
 
@@ -83,12 +85,22 @@ __device__ uint64_t g_attn_trace[8192 * 4];
 #define AT_MARK(i) do { } while (0)
 #endif
 
+// JLLM_SPLITK=0 switches split-K off (one split per head), read once, as the
+// reference's splitk_enabled does (attention.cu:990-996)
+bool attn_splitk_enabled() {
+    static const bool enabled = [] {
+        const char* v = getenv("JLLM_SPLITK");
+        return !v || strcmp(v, "0") != 0;
+    }();
+    return enabled;
+}
+
 int attn_splits(int seq_len, int n_kv) {
     // one wave per (KV head, split): at least 32 keys (one tile) per split,
     // at most 128 splits (measured on MI355X: short splits keep every SIMD
     // busy; past 128 the partials and the reduce cost more than they save)
     (void)n_kv;
-    if (seq_len <= 0) return 1;
+    if (!attn_splitk_enabled() || seq_len <= 0) return 1;
     const int s = (seq_len + 31) / 32;
     return s < 128 ? s : 128;
 }

@@ -132,10 +132,12 @@ int jllm_hip_flash_attention_decode_noalloc(uint16_t* out, const uint16_t* q, co
                                             int seq_len, float scale, int kv_int8, const float* k_scales,
                                             const float* v_scales, int window, void* stream) {
     const int n_splits = attn_splits(seq_len, n_kv_heads);
-    if (n_heads > 0 && head_dim > 0 &&
-        attn_partials_floats(n_heads, n_splits, head_dim) * sizeof(float) > NOALLOC_SCRATCH_BYTES) {
-        fprintf(stderr, "[attention] decode_noalloc: %d heads x %d splits x (2 + %d) floats exceed the %zu-byte "
-                        "static partials buffer\n", n_heads, n_splits, head_dim, NOALLOC_SCRATCH_BYTES);
+    // the partials attn_run writes: one per workgroup of W key ranges
+    const int W = attn_decode_waves(n_splits), groups = (n_splits + W - 1) / W;
+    if (n_heads > 0 && head_dim > 0 && groups > 1 &&
+        attn_partials_floats(n_heads, groups, head_dim) * sizeof(float) > NOALLOC_SCRATCH_BYTES) {
+        fprintf(stderr, "[attention] decode_noalloc: %d heads x %d partials x (2 + %d) floats exceed the %zu-byte "
+                        "static partials buffer\n", n_heads, groups, head_dim, NOALLOC_SCRATCH_BYTES);
         return JLLM_ERR_INVALID;
     }
     // argument errors first, so that no device state is touched for them

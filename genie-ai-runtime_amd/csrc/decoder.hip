@@ -277,6 +277,43 @@ int jllm_hip_decoder_generate(jllm_hip_decoder* d, const int32_t* prompt, int n_
     return JLLM_OK;
 }
 
+int jllm_hip_decoder_layer(jllm_hip_decoder* d, int layer, uint16_t* x, int N, int start_pos, void* stream) {
+    if (!d || !x || layer < 0 || layer >= d->cfg.n_layers || N <= 0 || N > d->max_batch || start_pos < 0 ||
+        start_pos + N > d->cfg.max_seq)
+        return JLLM_ERR_INVALID;
+    const size_t bytes = (size_t)N * d->cfg.hidden_dim * 2;
+    hipStream_t st = (hipStream_t)stream;
+    TRY(launch_status(hipMemcpyAsync(d->x, x, bytes, hipMemcpyDeviceToDevice, st), "decoder"));
+    TRY(N == 1 ? decode_layer(d, layer, start_pos, stream) : prefill_layer(d, layer, start_pos, N, stream));
+    return launch_status(hipMemcpyAsync(x, d->x, bytes, hipMemcpyDeviceToDevice, st), "decoder");
+}
+
+int jllm_hip_decoder_copy_kv(jllm_hip_decoder* d, int layer, int n_pos, void* k, void* v, float* k_scales,
+                             float* v_scales, void* stream) {
+    if (!d || layer < 0 || layer >= d->cfg.n_layers || n_pos < 0 || n_pos > d->cfg.max_seq) return JLLM_ERR_INVALID;
+    const jllm_hip_decoder_config& c = d->cfg;
+    const size_t rows = (size_t)n_pos * c.n_kv_heads * c.head_dim * (c.kv_int8 ? 1 : 2);
+    const size_t sc = (size_t)n_pos * c.n_kv_heads * 4;
+    hipStream_t st = (hipStream_t)stream;
+    if (k) TRY(launch_status(hipMemcpyAsync(k, layer_k(d, layer), rows, hipMemcpyDeviceToDevice, st), "decoder"));
+    if (v) TRY(launch_status(hipMemcpyAsync(v, layer_v(d, layer), rows, hipMemcpyDeviceToDevice, st), "decoder"));
+    if (c.kv_int8 && k_scales)
+        TRY(launch_status(hipMemcpyAsync(k_scales, layer_ks(d, layer), sc, hipMemcpyDeviceToDevice, st), "decoder"));
+    if (c.kv_int8 && v_scales)
+        TRY(launch_status(hipMemcpyAsync(v_scales, layer_vs(d, layer), sc, hipMemcpyDeviceToDevice, st), "decoder"));
+    return JLLM_OK;
+}
+
+int jllm_hip_decoder_copy_act(jllm_hip_decoder* d, int which, int rows, uint16_t* dst, void* stream) {
+    if (!d || !dst || rows <= 0 || rows > d->max_batch) return JLLM_ERR_INVALID;
+    const jllm_hip_decoder_config& c = d->cfg;
+    const size_t QD = (size_t)c.n_heads * c.head_dim;
+    const uint16_t* src = which == 0 ? d->q : which == 1 ? d->attn : which == 2 ? d->x2 : nullptr;
+    if (!src) return JLLM_ERR_INVALID;
+    const size_t bytes = (size_t)rows * (which == 2 ? (size_t)c.hidden_dim : QD) * 2;
+    return launch_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream), "decoder");
+}
+
 int jllm_hip_decoder_copy_logits(const jllm_hip_decoder* d, float* dst, void* stream) {
     if (!d || !dst) return JLLM_ERR_INVALID;
     return launch_status(hipMemcpyAsync(dst, d->logits, (size_t)d->cfg.vocab_size * 4, hipMemcpyDeviceToDevice,

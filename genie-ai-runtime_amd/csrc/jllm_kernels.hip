@@ -3,28 +3,31 @@
 #include "jllm_kernels.h"
 #include "jllm_hip.h"
 #include "kq_common.h"
+#include "fill_size.h"
 #include <cstdio>
 
 namespace {
 
-__global__ void zero_fill_kernel(uint16_t* p, size_t n) {
+using jllm_fill::fill_bytes;
+
+__global__ void zero_fill_kernel(uint8_t* p, size_t n) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         p[i] = 0;
 }
 
-// zero `bytes` (a multiple of 2) at p on the stream, with a kernel (no memset
-// node, so a captured graph replays it correctly)
+// zero `bytes` bytes at p on the stream, with a kernel (no memset node, so a
+// captured graph replays it correctly); sizes come from fill_bytes, which is
+// 0 for a negative or overflowing shape
 void zero_fill(void* p, size_t bytes, hipStream_t st) {
-    const size_t n = bytes / 2;
-    if (!p || n == 0) return;
-    const size_t blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
-    hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (uint16_t*)p, n);
+    if (!p || bytes == 0) return;
+    const size_t blocks = (bytes + 255) / 256 < 4096 ? (bytes + 255) / 256 : 4096;
+    hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (uint8_t*)p, bytes);
 }
 
 void report(int st, const char* fn, void* out, size_t bytes, hipStream_t stream) {
     if (st == JLLM_OK) return;
     fprintf(stderr, "[jllm] %s failed: %s; %s\n", fn, jllm_hip_status_string(st),
-            out ? "output zero-filled" : "data left unchanged");
+            out && bytes ? "output zero-filled" : "data left unchanged");
     zero_fill(out, bytes, stream);
 }
 
@@ -40,41 +43,41 @@ void gemv_q4(half* y, const void* W_q4, const half*, const half* x, int M, int K
 }
 
 void gemv_quant(half* y, const void* W, int type, const half* x, int M, int K, hipStream_t stream) {
-    report(jllm_hip_gemv_quant(H(y), W, type, H(x), M, K, stream), "gemv_quant", y, (size_t)M * 2, stream);
+    report(jllm_hip_gemv_quant(H(y), W, type, H(x), M, K, stream), "gemv_quant", y, fill_bytes({M}, 2), stream);
 }
 
 void gemv_quant_add(half* y, const void* W, int type, const half* x, const half* residual, int M, int K,
                     hipStream_t stream) {
     report(jllm_hip_gemv_quant_add(H(y), W, type, H(x), H(residual), M, K, stream), "gemv_quant_add", y,
-           (size_t)M * 2, stream);
+           fill_bytes({M}, 2), stream);
 }
 
 void gemv_quant_pair(half* y0, const void* W0, int t0, int M0, half* y1, const void* W1, int t1, int M1,
                      const half* x, int K, hipStream_t stream) {
     const int st = jllm_hip_gemv_quant_pair(H(y0), W0, t0, M0, H(y1), W1, t1, M1, H(x), K, stream);
-    report(st, "gemv_quant_pair", y0, (size_t)M0 * 2, stream);
-    if (st) zero_fill(y1, (size_t)M1 * 2, stream);
+    report(st, "gemv_quant_pair", y0, fill_bytes({M0}, 2), stream);
+    if (st) zero_fill(y1, fill_bytes({M1}, 2), stream);
 }
 
 void gemv_quant_triple(half* y0, const void* W0, int t0, int M0, half* y1, const void* W1, int t1, int M1,
                        half* y2, const void* W2, int t2, int M2, const half* x, int K, hipStream_t stream) {
     const int st = jllm_hip_gemv_quant_triple(H(y0), W0, t0, M0, H(y1), W1, t1, M1, H(y2), W2, t2, M2, H(x), K,
                                               stream);
-    report(st, "gemv_quant_triple", y0, (size_t)M0 * 2, stream);
-    if (st) { zero_fill(y1, (size_t)M1 * 2, stream); zero_fill(y2, (size_t)M2 * 2, stream); }
+    report(st, "gemv_quant_triple", y0, fill_bytes({M0}, 2), stream);
+    if (st) { zero_fill(y1, fill_bytes({M1}, 2), stream); zero_fill(y2, fill_bytes({M2}, 2), stream); }
 }
 
 void gemv_quant_f32(float* y, const void* W, int type, const half* x, int M, int K, hipStream_t stream) {
-    report(jllm_hip_gemv_quant_f32(y, W, type, H(x), M, K, stream), "gemv_quant_f32", y, (size_t)M * 4, stream);
+    report(jllm_hip_gemv_quant_f32(y, W, type, H(x), M, K, stream), "gemv_quant_f32", y, fill_bytes({M}, 4), stream);
 }
 
 void gemm_quant_batched(half* y, const void* W, int type, const half* x, int M, int N, int K, hipStream_t stream) {
     report(jllm_hip_gemm_quant_batched(H(y), W, type, H(x), M, N, K, stream), "gemm_quant_batched", y,
-           (size_t)M * (N > 0 ? N : 0) * 2, stream);
+           fill_bytes({M, N}, 2), stream);
 }
 
 void quantize_q8_1(const half* x, void* y, int K, hipStream_t stream) {
-    report(jllm_hip_quantize_q8_1(H(x), y, K, stream), "quantize_q8_1", y, (size_t)(K / 32) * 36, stream);
+    report(jllm_hip_quantize_q8_1(H(x), y, K, stream), "quantize_q8_1", y, fill_bytes({K / 32}, 36), stream);
 }
 
 void gemm_q4k_mmq_llama(half* y, const void* W, const half* x, int M, int N, int K, hipStream_t stream) {
@@ -92,13 +95,13 @@ void flash_attention_decode(half* output, const half* q, const void* k_cache, co
     report(jllm_hip_flash_attention_decode(H(output), H(q), k_cache, v_cache, n_heads, n_kv_heads, head_dim,
                                            cache_head_dim, seq_len, scale, kv_int8 ? 1 : 0, k_scales, v_scales,
                                            window, stream),
-           "flash_attention_decode", output, (size_t)n_heads * head_dim * 2, stream);
+           "flash_attention_decode", output, fill_bytes({n_heads, head_dim}, 2), stream);
 }
 
 void flash_attention_decode_dyn(half* output, const half* q, const void* k_cache, const void* v_cache, int n_heads,
                                 int n_kv_heads, int head_dim, int cache_head_dim, const int* d_pos, float scale,
                                 bool kv_int8, const float* kv_scales, int window, int n_splits, hipStream_t stream) {
-    const size_t bytes = (size_t)(n_heads > 0 ? n_heads : 0) * (head_dim > 0 ? head_dim : 0) * 2;
+    const size_t bytes = fill_bytes({n_heads, head_dim}, 2);
     if (kv_int8) {
         fprintf(stderr, "[jllm] flash_attention_decode_dyn: an INT8 cache needs separate K and V scales (use the "
                         "overload taking k_scales and v_scales); output zero-filled\n");
@@ -119,8 +122,7 @@ void flash_attention_decode_dyn(half* output, const half* q, const void* k_cache
     report(jllm_hip_flash_attention_decode_dyn(H(output), H(q), k_cache, v_cache, n_heads, n_kv_heads, head_dim,
                                                cache_head_dim, d_pos, scale, kv_int8 ? 1 : 0, k_scales, v_scales,
                                                window, n_splits, stream),
-           "flash_attention_decode_dyn", output, (size_t)(n_heads > 0 ? n_heads : 0) * (head_dim > 0 ? head_dim : 0) * 2,
-           stream);
+           "flash_attention_decode_dyn", output, fill_bytes({n_heads, head_dim}, 2), stream);
 }
 
 // in-place on fp32 logits: left unchanged on failure
@@ -135,13 +137,14 @@ float* get_splitk_partials(int n_heads, int n_splits, int head_dim) {
 }
 
 void fp16_to_int8(int8_t* dst, float* scale_out, const half* src, int rows, int cols, hipStream_t stream) {
-    report(jllm_hip_fp16_to_int8(dst, scale_out, H(src), rows, cols, stream), "fp16_to_int8", dst,
-           (size_t)rows * cols & ~(size_t)1, stream);
+    const int st = jllm_hip_fp16_to_int8(dst, scale_out, H(src), rows, cols, stream);
+    report(st, "fp16_to_int8", dst, fill_bytes({rows, cols}, 1), stream);
+    if (st) zero_fill(scale_out, fill_bytes({rows}, 4), stream);
 }
 
 bool dequant_embedding_row(half* dst, const void* W, int ggml_type, int token_id, int hidden_dim, hipStream_t stream) {
     const int st = jllm_hip_dequant_embedding_row(H(dst), W, ggml_type, token_id, hidden_dim, stream);
-    report(st, "dequant_embedding_row", dst, (size_t)(hidden_dim > 0 ? hidden_dim : 0) * 2, stream);
+    report(st, "dequant_embedding_row", dst, fill_bytes({hidden_dim}, 2), stream);
     return st == JLLM_OK;
 }
 
@@ -149,13 +152,13 @@ void fused_rmsnorm_residual(half* output, const half* x, const half* residual, c
                             int hidden_dim, float eps, bool weight_fp32, hipStream_t stream) {
     report(jllm_hip_fused_rmsnorm_residual(H(output), H(x), H(residual), weight, rows, hidden_dim, eps,
                                            weight_fp32 ? 1 : 0, stream),
-           "fused_rmsnorm_residual", output, (size_t)(rows > 0 ? rows : 0) * (hidden_dim > 0 ? hidden_dim : 0) * 2,
+           "fused_rmsnorm_residual", output, fill_bytes({rows, hidden_dim}, 2),
            stream);
 }
 
 void fused_swiglu(half* output, const half* gate, const half* up, int rows, int intermediate_dim, hipStream_t stream) {
     report(jllm_hip_fused_swiglu(H(output), H(gate), H(up), rows, intermediate_dim, stream), "fused_swiglu", output,
-           (size_t)(rows > 0 ? rows : 0) * (intermediate_dim > 0 ? intermediate_dim : 0) * 2, stream);
+           fill_bytes({rows, intermediate_dim}, 2), stream);
 }
 
 void rope_precompute_table(int max_seq, int head_dim, float theta_base) {
@@ -215,7 +218,7 @@ void rope_inplace_dyn(half* q, half* k, int n_heads, int n_kv_heads, int head_di
 
 void fused_geglu(half* output, const half* gate, const half* up, int rows, int intermediate_dim, hipStream_t stream) {
     report(jllm_hip_fused_geglu(H(output), H(gate), H(up), rows, intermediate_dim, stream), "fused_geglu", output,
-           (size_t)(rows > 0 ? rows : 0) * (intermediate_dim > 0 ? intermediate_dim : 0) * 2, stream);
+           fill_bytes({rows, intermediate_dim}, 2), stream);
 }
 
 void vec_scale(half* x, int n, float s, hipStream_t stream) {
@@ -228,12 +231,12 @@ void logit_softcap(float* x, int n, float cap, hipStream_t stream) {
 
 void gemv_dense(half* out, const void* W, int wtype, const half* x, int M, int K, hipStream_t stream) {
     report(jllm_hip_gemv_dense(H(out), W, wtype, H(x), M, K, stream), "gemv_dense", out,
-           (size_t)(M > 0 ? M : 0) * 2, stream);
+           fill_bytes({M}, 2), stream);
 }
 
 void gemm_dense_batched(half* out, const void* W, int wtype, const half* x, int M, int N, int K, hipStream_t stream) {
     report(jllm_hip_gemm_dense_batched(H(out), W, wtype, H(x), M, N, K, stream), "gemm_dense_batched", out,
-           (size_t)(M > 0 ? M : 0) * (N > 0 ? N : 0) * 2, stream);
+           fill_bytes({M, N}, 2), stream);
 }
 
 void flash_attention_prefill_batched(half* output, const half* q, const void* k_cache, const void* v_cache,
@@ -244,7 +247,7 @@ void flash_attention_prefill_batched(half* output, const half* q, const void* k_
                                                     cache_head_dim, N, start_pos, scale, kv_int8 ? 1 : 0, k_scales,
                                                     v_scales, window, stream),
            "flash_attention_prefill_batched", output,
-           (size_t)(N > 0 ? N : 0) * (n_heads > 0 ? n_heads : 0) * (head_dim > 0 ? head_dim : 0) * 2, stream);
+           fill_bytes({N, n_heads, head_dim}, 2), stream);
 }
 
 }  // namespace jllm

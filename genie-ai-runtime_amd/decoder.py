@@ -214,6 +214,36 @@ class Decoder:
     def generate(self, prompt, n_gen, out):
         jllm.call("jllm_hip_decoder_generate", self.h, prompt, prompt.numel(), n_gen, out)
 
+    def layer(self, l, x, N, start):
+        """Run layer l alone on the device rows x [N][hidden] (fp16 as int16),
+        in place, at positions start..start+N-1 (decode path for N == 1)."""
+        jllm.call("jllm_hip_decoder_layer", self.h, l, x, N, start)
+
+    def kv(self, l, n_pos):
+        """Layer l's KV cache, positions 0..n_pos-1, copied to the host:
+        (k, v) int8 [n_pos][n_kv][head_dim], (k_scales, v_scales) fp32
+        [n_pos][n_kv]."""
+        import torch
+        s = self.shape
+        shp = (n_pos, s.n_kv_heads, s.head_dim)
+        k, v = (torch.empty(shp, dtype=torch.int8, device="cuda:0") for _ in range(2))
+        ks, vs = (torch.empty((n_pos, s.n_kv_heads), dtype=torch.float32, device="cuda:0") for _ in range(2))
+        jllm.call("jllm_hip_decoder_copy_kv", self.h, l, n_pos, k, v, ks, vs)
+        torch.cuda.synchronize()
+        return k.cpu().numpy(), v.cpu().numpy(), ks.cpu().numpy(), vs.cpu().numpy()
+
+    def act(self, which, rows):
+        """Intermediate of the last layer run, first `rows` rows, as host fp16
+        bits: which 0 = rotated q, 1 = attention output, 2 = hidden state
+        after the attention residual."""
+        import torch
+        s = self.shape
+        width = s.hidden_dim if which == 2 else s.n_heads * s.head_dim
+        out = torch.empty(rows * width, dtype=torch.int16, device="cuda:0")
+        jllm.call("jllm_hip_decoder_copy_act", self.h, which, rows, out)
+        torch.cuda.synchronize()
+        return out.cpu().numpy().view(np.uint16).reshape(rows, width)
+
     def logits(self):
         """fp32 logits [vocab] of the last prefill/step, as a new device tensor."""
         import torch

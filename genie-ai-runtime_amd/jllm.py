@@ -99,6 +99,9 @@ SIGNATURES = {
     "jllm_hip_decoder_step": (I, [P, P, I, P, P]),
     "jllm_hip_decoder_generate": (I, [P, P, I, I, P, P]),
     "jllm_hip_decoder_copy_logits": (I, [P, P, P]),
+    "jllm_hip_decoder_layer": (I, [P, I, P, I, I, P]),
+    "jllm_hip_decoder_copy_kv": (I, [P, I, I, P, P, P, P, P]),
+    "jllm_hip_decoder_copy_act": (I, [P, I, I, P, P]),
 }
 
 

@@ -231,8 +231,11 @@ int jllm_hip_flash_attention_decode_dyn(uint16_t* out, const uint16_t* q, const 
  * partials live in a fixed 4 MiB array per device (allocated with the
  * library's code object, held until the process ends) instead of the
  * grown-on-demand buffer; this call makes no hipMalloc / hipFree.
- * n_heads * splits * (2 + head_dim) * 4 bytes must fit in 4 MiB (32 heads of
- * 128 at the 128-split maximum need 2.1 MiB), else JLLM_ERR_INVALID.  Every
+ * The partials written -- n_heads * P * (2 + head_dim) * 4 bytes, where P =
+ * ceil(splits / W) and W (4 from 64 splits on, else 1) is the number of
+ * key ranges one workgroup combines -- must fit in 4 MiB (32 heads of 128
+ * at the 128-split maximum: 0.53 MiB; 256 heads: 4.26 MB, refused), else
+ * JLLM_ERR_INVALID.  Every
  * call on a device shares that device's array: calls that overlap on one
  * GPU (several streams) race. */
 int jllm_hip_flash_attention_decode_noalloc(uint16_t* out, const uint16_t* q, const void* k, const void* v,
@@ -244,7 +247,8 @@ int jllm_hip_flash_attention_decode_noalloc(uint16_t* out, const uint16_t* q, co
  * get_splitk_partials, jllm_kernels.h:402-403 (attention.cu:975-1005).  The
  * MI355X policy is ceil(seq/32) splits capped at 128 (one wave per KV head
  * and split, so 8 KV heads put 1024 waves on 256 CUs), not the reference's
- * 1/4/8.  With one split the output is written directly (no reduce).  The buffer (floats: m[H*S] | l[H*S] |
+ * 1/4/8; JLLM_SPLITK=0 in the environment (read once) gives 1 split for
+ * every length, as in the reference.  With one split the output is written directly (no reduce).  The buffer (floats: m[H*S] | l[H*S] |
  * acc[H*S*head_dim]) is allocated on first use and never freed; call
  * jllm_hip_get_splitk_partials before graph capture.  NULL on failure. */
 int    jllm_hip_decode_attn_splits(int seq_len);
@@ -455,6 +459,29 @@ int jllm_hip_decoder_step(jllm_hip_decoder* d, const int32_t* token, int pos, in
  * the generated ids.  Asynchronous: no host synchronisation inside. */
 int jllm_hip_decoder_generate(jllm_hip_decoder* d, const int32_t* prompt, int n_prompt, int n_gen, int32_t* out,
                               void* stream);
+
+/* Test hook (no reference counterpart): runs decoder layer `layer` alone
+ * on the caller's hidden rows x[N][hidden_dim] (fp16, DEVICE), in place, at
+ * positions start_pos..start_pos+N-1 -- the decode step's layer
+ * (transformer_layer, decode.cu:1168-1246) for N == 1, the prefill layer
+ * (transformer_prefill, decode.cu:1760-1884) for 1 < N <= max_batch --
+ * writing that layer's KV-cache rows, so that a test can feed each layer an
+ * input of its choice and compare the layer's output. */
+int jllm_hip_decoder_layer(jllm_hip_decoder* d, int layer, uint16_t* x, int N, int start_pos, void* stream);
+
+/* Test hook (no reference counterpart): enqueue copies of positions
+ * 0..n_pos-1 of layer `layer`'s KV cache into caller buffers (DEVICE) --
+ * K and V [n_pos][n_kv_heads * head_dim] (int8, or fp16) and, for an INT8
+ * cache, the fp32 scales [n_pos][n_kv_heads].  Any destination may be NULL. */
+int jllm_hip_decoder_copy_kv(jllm_hip_decoder* d, int layer, int n_pos, void* k, void* v, float* k_scales,
+                             float* v_scales, void* stream);
+
+/* Test hook (no reference counterpart): enqueue a copy of the first `rows`
+ * rows of an intermediate of the last layer run (fp16, into dst, DEVICE):
+ * which 0 = q after q-RMSNorm and RoPE [rows][n_heads * head_dim], 1 = the
+ * attention output [rows][n_heads * head_dim], 2 = the hidden state after
+ * the attention block's residual add [rows][hidden_dim]. */
+int jllm_hip_decoder_copy_act(jllm_hip_decoder* d, int which, int rows, uint16_t* dst, void* stream);
 
 /* Enqueue a copy of the fp32 logits [vocab] of the last prefill/step into
  * dst (device memory). */

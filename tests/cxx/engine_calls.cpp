@@ -61,6 +61,7 @@ void ec_flash_attention_prefill_batched(void* out, const void* q, const void* k,
     jllm::flash_attention_prefill_batched(HP(out), CHP(q), k, v, H, KV, hd, chd, N, start, scale, i8 != 0, ks, vs,
                                           window, ST(s));
 }
+void ec_quantize_q8_1(const void* x, void* y, int K, void* s) { jllm::quantize_q8_1(CHP(x), y, K, ST(s)); }
 int ec_decode_attn_splits(int seq) { return jllm::decode_attn_splits(seq); }
 float* ec_get_splitk_partials(int H, int S, int hd) { return jllm::get_splitk_partials(H, S, hd); }
 void ec_fp16_to_int8(int8_t* dst, float* sc, const void* src, int rows, int cols, void* s) {

@@ -378,6 +378,122 @@ def test_cxx_layer_errors_zero_fill(dev):
     assert torch.equal(sm, torch.ones(10, device=dev))
 
 
+def test_cxx_layer_negative_sizes_write_nothing(dev):
+    """A negative (or overflowing) size is rejected and the C++ layer's error
+    path writes nothing -- the zero fill is sized by fill_bytes, 0 for such
+    shapes -- so a canary buffer handed in as the output stays as it was
+    (the reference's invalid sizes fail at launch and write nothing,
+    gemv_q4.cu:2633-2775)."""
+    l = ec()
+    g = synth.rng(14)
+    M, K = 256, 2560
+    W, x = to_dev(synth.q4k(g, M, K)), to_dev(synth.x_f16(g, K))
+    c0, c1, c2 = _filled(4096), _filled(4096), _filled(4096)
+    cf = _filled(4096, torch.float32)
+    ref16, reff = c0.clone(), cf.clone()
+    l.ec_gemv_quant(P(c0), P(W), 12, P(x), -M, K, S())
+    l.ec_gemv_quant_add(P(c0), P(W), 12, P(x), P(x), -M, K, S())
+    l.ec_gemv_quant_pair(P(c0), P(W), 12, -M, P(c1), P(W), 12, -1, P(x), K, S())
+    l.ec_gemv_quant_triple(P(c0), P(W), 12, -M, P(c1), P(W), 12, -2, P(c2), P(W), 14, -3, P(x), K, S())
+    l.ec_gemv_quant_f32(P(cf), P(W), 12, P(x), -M, K, S())
+    l.ec_gemm_quant_batched(P(c0), P(W), 12, P(x), -M, 4, K, S())
+    l.ec_gemm_quant_batched(P(c0), P(W), 12, P(x), M, -4, K, S())
+    l.ec_gemm_quant_batched(P(c0), P(W), 12, P(x), 1 << 30, 1 << 30, 300, S())   # M*N*2 = 2^61 bytes
+    l.ec_quantize_q8_1(P(x), P(c0), -2560, S())
+    q, k, v, ks, vs = _kv_case(6, 64, True)
+    l.ec_flash_attention_decode(P(c0), P(q), P(k), P(v), -H, KV, HD, HD, 10, F(0.1), 1, P(ks), P(vs), 0, S())
+    l.ec_flash_attention_decode(P(c0), P(q), P(k), P(v), H, KV, -HD, HD, 10, F(0.1), 1, P(ks), P(vs), 0, S())
+    l.ec_flash_attention_prefill_batched(P(c0), P(q), P(k), P(v), H, KV, HD, HD, -3, 0, F(0.1), 1, P(ks), P(vs),
+                                         0, S())
+    l.ec_fused_rmsnorm_residual(P(c0), P(x), P(x), P(x), -1, K, F(1e-6), 1, S())
+    l.ec_fused_swiglu(P(c0), P(x), P(x), 1, -K, S())
+    assert l.ec_dequant_embedding_row(P(c0), P(W), 12, 0, -K, S()) == 0
+    i8 = torch.ones(4096, dtype=torch.int8, device=dev)
+    sc = torch.ones(64, device=dev)
+    l.ec_fp16_to_int8(P(i8), P(sc), P(x), -8, 128, S())
+    torch.cuda.synchronize()
+    for t in (c0, c1, c2):
+        assert torch.equal(t, ref16)
+    assert torch.equal(cf, reff)
+    assert bool((i8 == 1).all()) and bool((sc == 1).all())
+
+
+def test_cxx_fp16_to_int8_error_fill_is_byte_exact(dev):
+    """On a rejected call with a valid shape (src missing), fp16_to_int8 zero
+    fills exactly rows x cols bytes of dst -- an odd count included -- and the
+    rows scales; the bytes after them are untouched."""
+    l = ec()
+    rows, cols = 8, 127
+    i8 = torch.ones(1024, dtype=torch.int8, device=dev)
+    sc = torch.ones(16, device=dev)
+    l.ec_fp16_to_int8(P(i8), P(sc), None, rows, cols, S())
+    torch.cuda.synchronize()
+    got, gs = from_dev(i8), from_dev(sc)
+    assert not got[:rows * cols].any() and (got[rows * cols:] == 1).all()
+    assert not gs[:rows].any() and (gs[rows:] == 1).all()
+
+
+SPLITK_CHILD = r"""
+import ctypes, sys
+sys.path[:0] = [sys.argv[1]]
+ec = ctypes.CDLL(sys.argv[2])
+print("splits", [ec.ec_decode_attn_splits(s) for s in (1, 63, 64, 700, 8192)])
+"""
+
+
+@pytest.mark.parametrize("env,want", [(None, [1, 2, 2, 22, 128]), ("1", [1, 2, 2, 22, 128]),
+                                      ("0", [1, 1, 1, 1, 1])])
+def test_splitk_switch(dev, env, want):
+    """JLLM_SPLITK=0 makes decode_attn_splits return 1 for every length (the
+    reference's splitk_enabled, attention.cu:990-1005); read once per
+    process, so each setting runs in a child process of its own."""
+    e = dict(os.environ)
+    e.pop("JLLM_SPLITK", None)
+    if env is not None:
+        e["JLLM_SPLITK"] = env
+    r = subprocess.run([sys.executable, "-c", SPLITK_CHILD, os.path.join(ROOT, "genie-ai-runtime_amd"), EC_PATH],
+                       capture_output=True, text=True, timeout=120, env=e)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert f"splits {want}" in r.stdout, r.stdout
+
+
+SPLITK_ATTN_CHILD = r"""
+import ctypes, sys
+import numpy as np
+sys.path[:0] = [sys.argv[1], sys.argv[2]]
+import torch, jllm, synth
+from gpu_util import to_dev
+H, KV, HD, ctx = 32, 8, 128, 700
+g = synth.rng(21)
+q, k, v = synth.x_f16(g, H * HD), synth.kv_int8(g, ctx, KV, HD), synth.kv_int8(g, ctx, KV, HD)
+ks, vs = synth.kv_scales(g, ctx, KV), synth.kv_scales(g, ctx, KV)
+out = torch.zeros(H * HD, dtype=torch.int16, device="cuda:0")
+jllm.call("jllm_hip_flash_attention_decode", out, to_dev(q), to_dev(k), to_dev(v), H, KV, HD, HD, ctx,
+          1.0 / np.sqrt(HD), 1, to_dev(ks), to_dev(vs), 0)
+one = torch.zeros_like(out)
+jllm.call("jllm_hip_flash_attention_decode_splits", one, to_dev(q), to_dev(k), to_dev(v), H, KV, HD, HD, ctx,
+          1.0 / np.sqrt(HD), 1, to_dev(ks), to_dev(vs), 0, 1)
+torch.cuda.synchronize()
+print("same_as_one_split", bool(torch.equal(out, one)))
+"""
+
+
+@pytest.mark.parametrize("env,same", [("0", True), (None, False)])
+def test_splitk_switch_static_entry(dev, env, same):
+    """With JLLM_SPLITK=0 the static decode entry runs one split: its output
+    is bit-identical to an explicit one-split call (and, with split-K on,
+    it is not -- 22 key ranges combine in another order)."""
+    e = dict(os.environ)
+    e.pop("JLLM_SPLITK", None)
+    if env is not None:
+        e["JLLM_SPLITK"] = env
+    r = subprocess.run([sys.executable, "-c", SPLITK_ATTN_CHILD, os.path.join(ROOT, "genie-ai-runtime_amd"),
+                        os.path.dirname(os.path.abspath(__file__))], capture_output=True, text=True, timeout=300,
+                       env=e)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert f"same_as_one_split {same}" in r.stdout, r.stdout
+
+
 REGISTRY_CHILD = r"""
 import ctypes, sys
 import numpy as np

@@ -177,3 +177,15 @@ def test_pointer_returning_entry_points_keep_64_bit_results():
     for n in ptr_fns:
         assert jllm.SIGNATURES[n][0] in (ctypes.c_void_p, ctypes.c_char_p), n
         assert getattr(jllm.lib(), n).restype in (ctypes.c_void_p, ctypes.c_char_p), n
+
+
+def test_zero_fill_size_helper(tmp_path):
+    """The C++ layer's zero fill on an error path is sized by fill_bytes:
+    0 for a negative dimension or a product over 2^40 bytes, the exact byte
+    count otherwise (the reference's invalid sizes write nothing,
+    gemv_q4.cu:2633-2775)."""
+    exe = tmp_path / "fill_size_test"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-I", os.path.join(ROOT, "genie-ai-runtime_amd", "csrc"),
+                    os.path.join(ROOT, "tests", "cxx", "fill_size_test.cpp"), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert got == [19456, 0, 0, 0, 0, 0, 1 << 40, 0, 0, 4194304, 1016]

@@ -227,6 +227,117 @@ def test_decoder_oracle_prefill_chunking_and_steps():
     assert np.abs(a.logits).max() > 0.5                   # the random model is not degenerate
 
 
+def test_layer_functions_match_decoder_oracle():
+    """The one-layer oracle functions the full-size per-layer GPU test uses
+    (prefill_layer_rows on a subset of the prompt rows, decode_layer) give
+    exactly the layers of OracleDecoder's prefill and decode step, KV rows
+    included: the prefill layer is per token except for the attention, and
+    the MMQ arithmetic of a token does not depend on the other tokens."""
+    import decoder
+    import decoder_oracle
+    shape = decoder.Shape(**TINY)
+    model = decoder.synth_np(shape, 81)
+    prompt = list(synth.rng(82).integers(0, shape.vocab_size, 24))
+    od = decoder_oracle.OracleDecoder(shape, model, 32)
+    od.trace = []
+    nxt = od.prefill(prompt)
+    rows = [0, 5, 11, 23]
+    H = shape.hidden_dim
+    for l, x_in, x_out in od.trace:
+        got, k, v, ks, vs = decoder_oracle.prefill_layer_rows(
+            shape, model["layers"][l], x_in.reshape(-1, H)[rows], rows, od.kc[l], od.vc[l], od.ks[l], od.vs[l])
+        assert np.array_equal(got, x_out.reshape(-1, H)[rows]), l
+        assert np.array_equal(k, od.kc[l][rows]) and np.array_equal(v, od.vc[l][rows]), l
+        assert np.array_equal(ks, od.ks[l][rows]) and np.array_equal(vs, od.vs[l][rows]), l
+    before = [(od.kc[l].copy(), od.vc[l].copy(), od.ks[l].copy(), od.vs[l].copy()) for l in range(shape.n_layers)]
+    od.trace = []
+    od.step(nxt, 24)
+    for l, x_in, x_out in od.trace:
+        kc, vc, ks, vs = before[l]
+        got = decoder_oracle.decode_layer(shape, model["layers"][l], x_in, 24, kc, vc, ks, vs)
+        assert np.array_equal(got, x_out), l
+        assert np.array_equal(kc, od.kc[l]) and np.array_equal(vs, od.vs[l]), l
+
+
+def _qwen3_float64(shape, model, theta=None):
+    """A Hugging Face transformers Qwen3ForCausalLM (an implementation of the
+    architecture written independently of the reference engine and of this
+    repository) in float64 over the DEQUANTISED weights of `model`."""
+    import torch
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    H, I = shape.hidden_dim, shape.intermediate_dim
+    cfg = Qwen3Config(vocab_size=shape.vocab_size, hidden_size=H, intermediate_size=I,
+                      num_hidden_layers=shape.n_layers, num_attention_heads=shape.n_heads,
+                      num_key_value_heads=shape.n_kv_heads, head_dim=shape.head_dim, rms_norm_eps=shape.rms_eps,
+                      rope_theta=theta or shape.rope_theta, tie_word_embeddings=False, attention_bias=False,
+                      max_position_embeddings=4096, use_cache=False)
+    cfg._attn_implementation = "eager"
+    m = Qwen3ForCausalLM(cfg).to(torch.float64).eval()
+    deq = {12: np_ref.q4k_dequant, 13: np_ref.q5k_dequant, 14: np_ref.q6k_dequant}
+
+    def mat(W, t, M, K):
+        return torch.from_numpy(np.ascontiguousarray(deq[t](W, M, K)))
+
+    def vec(a):
+        return torch.from_numpy(np.asarray(a, np.float64))
+    sd = {"model.embed_tokens.weight": mat(model["tok_embd"], model["embd_type"], shape.vocab_size, H),
+          "lm_head.weight": mat(model["output"], model["output_type"], shape.vocab_size, H),
+          "model.norm.weight": vec(model["output_norm"])}
+    names = {"wq": "self_attn.q_proj", "wk": "self_attn.k_proj", "wv": "self_attn.v_proj", "wo": "self_attn.o_proj",
+             "w_gate": "mlp.gate_proj", "w_up": "mlp.up_proj", "w_down": "mlp.down_proj"}
+    for l, L in enumerate(model["layers"]):
+        p = f"model.layers.{l}."
+        for k, n in names.items():
+            M, K = shape.mat_shape(k)
+            sd[p + n + ".weight"] = mat(L[k], L["types"][k], M, K)
+        sd[p + "input_layernorm.weight"] = vec(L["rms_attn"])
+        sd[p + "post_attention_layernorm.weight"] = vec(L["rms_ffn"])
+        sd[p + "self_attn.q_norm.weight"] = vec(L["q_norm"])
+        sd[p + "self_attn.k_norm.weight"] = vec(L["k_norm"])
+    missing, unexpected = m.load_state_dict(sd, strict=False)
+    assert not unexpected and all("rotary" in k for k in missing), (missing, unexpected)
+    return m
+
+
+def test_decoder_oracle_vs_float64_qwen3():
+    """The decoder oracle's layer order (RMSNorm placement, q/k RMSNorm
+    before a neox RoPE with base 1e6, GQA, SwiGLU, residuals, output norm)
+    pinned against an independent float64 Qwen3 forward (transformers'
+    Qwen3ForCausalLM) over the dequantised weights: the logits of the
+    prefill's last row and of three teacher-forced decode steps agree within
+    the quantisation error (q8 activations, int8 KV, fp16 intermediates),
+    while the same forward with the RoPE base off (1e4) -- one plausible
+    misreading -- misses by several times more."""
+    import torch
+    import decoder
+    import decoder_oracle
+    shape = decoder.Shape(**TINY)
+    model = decoder.synth_np(shape, 83)
+    prompt = list(synth.rng(84).integers(0, shape.vocab_size, 40))
+    od = decoder_oracle.OracleDecoder(shape, model, 64)
+    toks = [od.prefill(prompt)]
+    got = [od.logits.copy()]
+    for i in range(3):
+        toks.append(od.step(toks[-1], len(prompt) + i))
+        got.append(od.logits.copy())
+    seq = prompt + toks[:3]
+
+    def ref_logits(theta=None):
+        m = _qwen3_float64(shape, model, theta)
+        with torch.no_grad():
+            lg = m(torch.tensor([seq])).logits[0].numpy()
+        return [lg[len(prompt) - 1 + i] for i in range(4)]
+    want = ref_logits()
+    wrong = ref_logits(1e4)
+    errs = [float(np.abs(g - w).max() / np.abs(w).max()) for g, w in zip(got, want)]
+    miss = [float(np.abs(g - w).max() / np.abs(w).max()) for g, w in zip(got, wrong)]
+    print("oracle vs float64 Qwen3:", errs, "with the RoPE base off:", miss)
+    assert max(errs) < 0.05 and max(errs[1:]) < 0.02, errs
+    assert min(miss) > 4 * max(errs), (errs, miss)
+    assert all(int(np.argmax(w)) == t for w, t in zip(want, toks) if np.sort(w)[-1] - np.sort(w)[-2] >
+               0.1 * np.abs(w).max())
+
+
 # ---- kernels outside the Llama/Qwen decode path ------------------------------
 
 def test_geglu_against_exact_gelu():

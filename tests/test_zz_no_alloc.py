@@ -23,7 +23,10 @@ def _inputs(seed, ctx, H, KV, HD):
 
 
 @pytest.mark.parametrize("first,second", [((32, 8, 128, 4096, 0), (32, 8, 128, 300, 0)),
-                                          ((32, 8, 128, 8192, 512), (16, 4, 64, 40, 0))])
+                                          ((32, 8, 128, 8192, 512), (16, 4, 64, 40, 0)),
+                                          # 64 heads x 128 key ranges: 32 partials per head after the
+                                          # 4-wave grouping (1.06 MB) -- fits the 4 MiB array
+                                          ((64, 8, 128, 8192, 0), (32, 8, 128, 640, 0))])
 def test_noalloc_matches_allocating_entry(dev, first, second):
     for i, (H, KV, HD, ctx, window) in enumerate((first, second)):
         print_case("noalloc", i, H, KV, HD, ctx, window)
@@ -38,8 +41,9 @@ def test_noalloc_matches_allocating_entry(dev, first, second):
 
 
 def test_noalloc_rejects_oversize(dev):
-    # 64 heads x 128 splits x (2 + 128) floats = 4.26 MB > 4 MiB
-    H, KV, HD, ctx = 64, 8, 128, 8192
+    # 256 heads (16 per KV head) x 128 key ranges grouped into 32 partials
+    # of (2 + 128) floats = 4.26 MB > 4 MiB
+    H, KV, HD, ctx = 256, 16, 128, 8192
     q, k, v, ks, vs = _inputs(1, 64, 8, 8, 128)
     out = torch.zeros(H * HD, dtype=torch.int16, device=dev)
     st = jllm.lib().jllm_hip_flash_attention_decode_noalloc(out.data_ptr(), q.data_ptr(), k.data_ptr(),
