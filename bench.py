@@ -181,7 +181,38 @@ def main():
     stage("CPU baseline")
     if not args.skip_cpu:
         out["cpu_baseline"] = cpu_baseline(np, synth, args.cpu_seconds)
+    out["north_star"] = north_star_table(out)
     print(json.dumps(out), flush=True)
+
+
+def north_star_table(out):
+    """BASELINE.json north-star targets next to this run's roofline fractions:
+    GEMV >= 0.70 of HBM peak (the gate/up pair, the whole decode-step set,
+    configs[0]), int8 MMQ >= 0.50 of the int8 MFMA peak at 512 tokens; the
+    decode attention and the end-to-end decode step are held to the same
+    0.70 HBM bar as the GEMV (the north star names HBM GB/s against ~8 TB/s
+    for both).  gap = target - frac."""
+    rows = {}
+
+    def add(name, frac, target, **kw):
+        if frac is None:
+            return
+        rows[name] = dict(frac=round(frac, 4), target=target, gap=round(target - frac, 4), **kw)
+    add("gemv_pair_gate_up", out["roofline"]["frac"], 0.70, unit="HBM")
+    add("gemv_decode_step_set", out["config"]["hbm_frac"], 0.70, unit="HBM")
+    add("gemv_configs0_q4k_9728x2560", out["gemv_q4k_9728x2560"]["hbm_frac"], 0.70, unit="HBM")
+    mmq = out.get("mmq", {})
+    for key, name in (("q4k_M9728_K2560_N512", "mmq_q4k_N512"), ("q6k_M2560_K9728_N512", "mmq_q6k_N512")):
+        if key in mmq:
+            add(name, mmq[key]["frac_int8_peak"], 0.50, unit="int8 MFMA")
+    att = out.get("attention", {})
+    if "ctx8192_win0" in att:
+        add("attention_ctx8192", att["ctx8192_win0"]["hbm_frac"], 0.70, unit="HBM")
+    e2e = out.get("e2e")
+    if e2e:
+        add("e2e_decode", e2e["decode_hbm_frac"], 0.70, unit="HBM", decode_tok_s=e2e["decode_tok_s"],
+            tokens_equal_oracle=e2e["tokens_equal_oracle"], first_near_tie=e2e["first_near_tie"])
+    return rows
 
 
 def measured_traffic():
