@@ -488,6 +488,18 @@ void attn_partial_kernel(AttnArgs a) {
                     }
                 }
             }
+#ifdef JLLM_ATTN_TRACE
+            AT_MARK(3);
+            {
+                const int gw = ((int)blockIdx.y * (int)gridDim.x + (int)blockIdx.x) * W + wv;
+                if (l < 4 && gw < 8192) {
+                    uint64_t tv = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) if (l == i) tv = tr[i];
+                    g_attn_trace[gw * 4 + l] = tv;
+                }
+            }
+#endif
             return;
         }
         if (S == 1) {
