@@ -98,6 +98,12 @@ int jllm_hip_decode_attn_splits(int seq_len) { return attn_splits(seq_len, 8); }
 
 float* jllm_hip_get_splitk_partials(int n_heads, int n_splits, int head_dim) {
     if (n_heads <= 0 || n_splits <= 0 || head_dim <= 0) return nullptr;
+    // the largest the decode kernels use: 256 KV heads x 16, 256 splits, head_dim 128
+    if (n_heads > ATTN_MAX_KV * 16 || n_splits > ATTN_MAX_SPLITS || head_dim > 128) {
+        fprintf(stderr, "[attention] get_splitk_partials(%d, %d, %d): beyond the kernels' limits\n", n_heads,
+                n_splits, head_dim);
+        return nullptr;
+    }
     uint8_t* scratch = (uint8_t*)g_part.get(attn_scratch_bytes(n_heads, n_splits, head_dim));
     return scratch ? (float*)(scratch + ATTN_COUNTER_BYTES) : nullptr;
 }

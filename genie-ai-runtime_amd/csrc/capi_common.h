@@ -41,6 +41,10 @@ struct DeviceScratch {
         if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXDEV) return nullptr;
         std::lock_guard<std::mutex> lk(mu);
         if (bytes > cap[dev]) {
+            if (bytes > ((size_t)1 << 40)) {
+                fprintf(stderr, "[scratch] request of %zu bytes refused (over 1 TiB: an invalid size)\n", bytes);
+                return nullptr;
+            }
             size_t want = (size_t)1 << 20;
             while (want < bytes) want <<= 1;
             void* p = nullptr;

@@ -27,6 +27,16 @@ int check_gemm(const char* tag, const void* y, int type, const uint16_t* x, int 
         fprintf(stderr, "[%s] output and 16-byte aligned activation pointers are required\n", tag);
         return JLLM_ERR_INVALID;
     }
+    // the kernels address the weight matrix and the quantised activation
+    // with 32-bit buffer offsets: refuse shapes whose byte counts would not
+    // fit rather than read a truncated range
+    const int64_t lim = ((int64_t)1 << 31) - 1;
+    const int64_t wbytes = (int64_t)M * (K / 256) * 210, abytes = (int64_t)K * ((N + 63) / 64 * 64) * 2;
+    if (wbytes > lim || abytes > lim) {
+        fprintf(stderr, "[%s] shape M=%d N=%d K=%d exceeds the 2 GiB weight / activation ranges of the kernels\n",
+                tag, M, N, K);
+        return JLLM_ERR_INVALID;
+    }
     return JLLM_OK;
 }
 

@@ -433,6 +433,27 @@ def test_cxx_fp16_to_int8_error_fill_is_byte_exact(dev):
     assert not gs[:rows].any() and (gs[rows:] == 1).all()
 
 
+def test_oversized_requests_refused(dev):
+    """Sizes beyond what the kernels address are refused up front, with no
+    allocation attempt: a GEMM whose quantised activation or weight matrix
+    exceeds the kernels' 2 GiB buffer ranges, a partials buffer beyond the
+    decode kernels' limits (2^30 heads x 2^30 splits once overflowed the
+    scratch size and never returned)."""
+    x = torch.zeros(4096, dtype=torch.int16, device=dev)
+    y = torch.zeros(64, dtype=torch.int16, device=dev)
+    W = torch.zeros(4096, dtype=torch.uint8, device=dev)
+    lib = jllm.lib()
+    for M, N, K in ((64, 1 << 20, 1536), (1 << 22, 64, 2560), (1 << 30, 1 << 30, 256)):
+        for t in (12, 14):
+            st = lib.jllm_hip_gemm_quant_batched(y.data_ptr(), W.data_ptr(), t, x.data_ptr(), M, N, K, None)
+            assert st == -1, (M, N, K, t, st)
+    assert not lib.jllm_hip_get_splitk_partials(1 << 30, 1 << 30, 128)
+    assert not lib.jllm_hip_get_splitk_partials(32, 257, 128)
+    assert not lib.jllm_hip_get_splitk_partials(32, 8, 256)
+    assert lib.jllm_hip_get_splitk_partials(32, 256, 128)
+    torch.cuda.synchronize()
+
+
 SPLITK_CHILD = r"""
 import ctypes, sys
 sys.path[:0] = [sys.argv[1]]
