@@ -216,7 +216,16 @@ bool parse(jllm_hip_gguf* g) {
     }
     if (!c.ok) { fprintf(stderr, "[gguf] truncated file\n"); return false; }
     uint64_t align = 32;
-    if (const KV* a = g->find("general.alignment")) align = a->u ? a->u : 32;
+    if (const KV* a = g->find("general.alignment")) {
+        // the spec's alignment is a power of two (a u32); anything else would
+        // misplace every tensor
+        if (scalar_size(a->type) == 0 || a->type == 6 || a->type == 12 || a->u == 0 || a->u > 65536 ||
+            (a->u & (a->u - 1)) != 0) {
+            fprintf(stderr, "[gguf] general.alignment must be a power of two <= 65536\n");
+            return false;
+        }
+        align = a->u;
+    }
     g->data_start = (c.off + align - 1) / align * align;
     for (const auto& t : g->tensors) {
         if (t.offset % align != 0 || t.offset > g->size || (uint64_t)t.bytes > g->size ||
@@ -486,9 +495,15 @@ int jllm_hip_gguf_writer_add_tensor(jllm_hip_gguf_writer* w, const char* name, i
 
 int jllm_hip_gguf_writer_write(const jllm_hip_gguf_writer* w, const char* path) {
     if (!w || !path) return JLLM_ERR_INVALID;
+    // the alignment the file declares (general.alignment), else the spec's 32
+    uint64_t align = 32;
+    for (const auto& e : w->kv)
+        if (e.key == "general.alignment") {
+            if (e.type != 4 || e.u == 0 || e.u > 65536 || (e.u & (e.u - 1)) != 0) return JLLM_ERR_INVALID;
+            align = e.u;
+        }
     FILE* f = fopen(path, "wb");
     if (!f) return JLLM_ERR_INVALID;
-    const uint64_t align = 32;
     bool ok = true;
     const uint32_t magic = GGUF_MAGIC, version = 3;
     const uint64_t nt = w->tensors.size(), nkv = w->kv.size();
@@ -506,14 +521,21 @@ int jllm_hip_gguf_writer_write(const jllm_hip_gguf_writer* w, const char* path) 
         ok &= wr(f, &t.type, 4) && wr(f, &off, 8);
         off += ((uint64_t)t.bytes + align - 1) / align * align;
     }
-    const uint8_t zeros[32] = {};
+    const uint8_t zeros[256] = {};
+    auto pad_to = [&](uint64_t n) {          // n zero bytes
+        while (ok && n > 0) {
+            const size_t k = n < sizeof(zeros) ? (size_t)n : sizeof(zeros);
+            ok &= wr(f, zeros, k);
+            n -= k;
+        }
+    };
     long pos = ftell(f);
-    ok &= pos >= 0 && wr(f, zeros, (size_t)(((uint64_t)pos + align - 1) / align * align - (uint64_t)pos));
+    ok &= pos >= 0;
+    if (ok) pad_to(((uint64_t)pos + align - 1) / align * align - (uint64_t)pos);
     for (size_t i = 0; i < w->tensors.size(); i++) {
         const size_t b = w->data[i].size();
         ok &= wr(f, w->data[i].data(), b);
-        const size_t pad = (size_t)(((uint64_t)b + align - 1) / align * align - b);
-        ok &= wr(f, zeros, pad);
+        pad_to(((uint64_t)b + align - 1) / align * align - b);
     }
     ok &= fclose(f) == 0;
     return ok ? JLLM_OK : JLLM_ERR_INVALID;

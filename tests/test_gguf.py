@@ -148,6 +148,54 @@ def test_malformed_files_are_rejected(tiny_file, tmp_path, damage):
     assert not jllm.lib().jllm_hip_gguf_open(str(bad).encode())
 
 
+def _write_one_tensor(path, align=None):
+    lib = jllm.lib()
+    w = lib.jllm_hip_gguf_writer_create()
+    try:
+        jllm.check(lib.jllm_hip_gguf_writer_set_str(w, b"general.architecture", b"qwen3"), "arch")
+        if align is not None:
+            jllm.check(lib.jllm_hip_gguf_writer_set_u32(w, b"general.alignment", align), "alignment")
+        a = np.arange(3 * 256, dtype=np.float32)
+        d = (ctypes.c_int64 * 2)(256, 3)
+        jllm.check(lib.jllm_hip_gguf_writer_add_tensor(w, b"t.weight", 0, 2, d, a.ctypes.data_as(ctypes.c_void_p),
+                                                       a.nbytes), "tensor")
+        return lib.jllm_hip_gguf_writer_write(w, str(path).encode()), a
+    finally:
+        lib.jllm_hip_gguf_writer_free(w)
+
+
+def test_alignment_is_honoured_and_validated(tmp_path):
+    """general.alignment (a power of two, per the GGUF spec) places the
+    tensor data; the writer pads to the declared alignment, and a file
+    declaring a non-power-of-two alignment is rejected (it would misplace
+    every tensor)."""
+    lib = jllm.lib()
+    p64 = tmp_path / "a64.gguf"
+    st, a = _write_one_tensor(p64, 64)
+    assert st == 0
+    g = lib.jllm_hip_gguf_open(str(p64).encode())
+    assert g
+    try:
+        data, nbytes = ctypes.c_void_p(), ctypes.c_int64()
+        jllm.check(lib.jllm_hip_gguf_tensor(g, 0, None, None, None, None, ctypes.byref(data), ctypes.byref(nbytes)),
+                   "tensor")
+        got = np.ctypeslib.as_array((ctypes.c_float * (nbytes.value // 4)).from_address(data.value))
+        assert np.array_equal(got, a)
+    finally:
+        lib.jllm_hip_gguf_close(g)
+    buf = bytearray(open(p64, "rb").read())
+    assert (len(buf) - 3 * 256 * 4) % 64 == 0
+    key = b"general.alignment"
+    at = buf.index(key) + len(key) + 4                 # after the key string and the u32 value type
+    assert struct.unpack_from("<I", buf, at)[0] == 64
+    for bad in (48, 0):
+        struct.pack_into("<I", buf, at, bad)
+        path = tmp_path / f"a{bad}.gguf"
+        open(path, "wb").write(bytes(buf))
+        assert not lib.jllm_hip_gguf_open(str(path).encode()), bad
+    assert _write_one_tensor(tmp_path / "w48.gguf", 48)[0] != 0
+
+
 @pytest.mark.gpu
 def test_decoder_from_gguf_matches_in_memory_model(dev, tiny_file):
     import torch
