@@ -546,24 +546,60 @@ void attn_partial_kernel(AttnArgs a) {
     __builtin_amdgcn_wave_barrier();
     if (MT && W > 1) {
         // combine the W waves' states per column, waves in order:
-        // out = sum_w acc_w e^(m_w - M) / sum_w l_w e^(m_w - M), M = max_w m_w
+        // out = sum_w acc_w e^(m_w - M) / sum_w l_w e^(m_w - M), M = max_w m_w.
+        // The per-column quantities (wave weights, denominator, output row)
+        // are formed once per column; then each thread takes 8 consecutive d
+        // of a column: 16-byte LDS reads and one 16-byte store of 8 halves
+        // (the arithmetic per element as written above, in wave order, so the
+        // division and every rounding are those of the per-element form).
         float* sML = (float*)(smem_wg + (size_t)W * wave_lds);     // [W][m[32] | l[32]]
+        float* sF = sML + W * 64;                                  // [W][32] wave weights
+        float* sDen = sF + ATTN_MAX_WAVES * 32;                    // [32] denominators
         if (lg == 0) { sML[wv * 64 + li] = run_m; sML[wv * 64 + 32 + li] = run_l; }
         __syncthreads();
-        for (int e = (int)threadIdx.x; e < GC * hd; e += 64 * W) {
-            const int c = e / hd, d = e % hd;
+        const int t = (int)threadIdx.x;
+        if (t < GC) {
             float M = -FLT_MAX;
-            for (int u = 0; u < W; u++) M = fmaxf(M, sML[u * 64 + c]);
-            float num = 0.0f, den = 0.0f;
+            for (int u = 0; u < W; u++) M = fmaxf(M, sML[u * 64 + t]);
+            float den = 0.0f;
             for (int u = 0; u < W; u++) {
-                const float f = expf(sML[u * 64 + c] - M);
-                const float* so = (const float*)(smem_wg + (size_t)u * wave_lds);
-                num += (so[c * hd + d] + so[(GC + c) * hd + d]) * f;
-                den += sML[u * 64 + 32 + c] * f;
+                const float f = expf(sML[u * 64 + t] - M);
+                sF[u * 32 + t] = f;
+                den += sML[u * 64 + 32 + t] * f;
             }
-            const int ct = c / G, ch = c % G;
-            uint16_t* ot = a.out + (int64_t)(tok0 + ct) * a.n_heads * hd + (int64_t)(pbase + ch) * hd;
-            ot[d] = f32_to_f16_bits(den > 0.0f ? num / den : 0.0f);
+            sDen[t] = den;
+        }
+        __syncthreads();
+        const int nd8 = hd / 8;
+        const bool vec = ((uintptr_t)a.out & 15u) == 0;
+        for (int e = t; e < GC * nd8; e += 64 * W) {
+            const int c = e / nd8, d0 = (e - c * nd8) * 8;
+            float num[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+            for (int u = 0; u < W; u++) {
+                const float f = sF[u * 32 + c];
+                const float* so = (const float*)(smem_wg + (size_t)u * wave_lds);
+                const f32x4a h0 = *(const f32x4a*)&so[c * hd + d0], h1 = *(const f32x4a*)&so[c * hd + d0 + 4];
+                const f32x4a l0 = *(const f32x4a*)&so[(GC + c) * hd + d0], l1 = *(const f32x4a*)&so[(GC + c) * hd + d0 + 4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    num[i] += (h0[i] + l0[i]) * f;
+                    num[4 + i] += (h1[i] + l1[i]) * f;
+                }
+            }
+            const float den = sDen[c];
+            uint32_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                o[i] = (uint32_t)f32_to_f16_bits(den > 0.0f ? num[2 * i] / den : 0.0f) |
+                       ((uint32_t)f32_to_f16_bits(den > 0.0f ? num[2 * i + 1] / den : 0.0f) << 16);
+            const int ct = c / G, ch = c - ct * G;
+            uint16_t* ot = a.out + (int64_t)(tok0 + ct) * a.n_heads * hd + (int64_t)(pbase + ch) * hd + d0;
+            if (vec) {
+                *(u32x4a*)ot = u32x4a{o[0], o[1], o[2], o[3]};
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) { ot[2 * i] = (uint16_t)(o[i] & 0xFFFFu); ot[2 * i + 1] = (uint16_t)(o[i] >> 16); }
+            }
         }
         return;
     }
