@@ -70,14 +70,31 @@ struct DeviceScratch {
 // (DS4 for Q4_K, D4 for Q6_K; Q5_K needs none), then each product runs as
 // jllm_hip_gemm_quant_batched would (fp16 out).  Types and shapes are
 // checked as there.
+// quantized: the activation's codes are already in the quantiser scratch
+// (norm_rows reported so for this x, N, K and these outputs).
 struct GemmOut { uint16_t* y; const void* W; int type; int M; };
-int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uint16_t* x, int N, int K, void* stream);
+int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uint16_t* x, int N, int K, void* stream,
+                          bool quantized = false);
+// Rows of the residual stream whose residual add is left to the next step
+// (gemm_batched_res with `defer`): mode 0: y [N x M] is complete; 1: y holds
+// the product, y = half(y + res) still to do; 2: the product is still S
+// fp32 split-K partials ws [S][N][M], y = half(half(sum) + res) to do.
+struct ResidualRows { uint16_t* y; const uint16_t* res; const float* ws; int S; int mode; };
 // y [N x M] = half(half(a . W^T) + res) with a = x, or, when up is given,
 // a = half(silu(x) * up) (the SwiGLU of gate x and up, formed inside the
 // activation quantiser; act_tmp [N x K] holds it where a path needs it in
 // memory): the engine's projection + residual add (decode.cu:1830-1884).
 int gemm_batched_res(const char* tag, uint16_t* y, const void* W, int type, const uint16_t* x, const uint16_t* up,
-                     uint16_t* act_tmp, const uint16_t* res, int M, int N, int K, void* stream);
+                     uint16_t* act_tmp, const uint16_t* res, int M, int N, int K, void* stream,
+                     ResidualRows* defer = nullptr);
+// completes deferred rows (y [N x M] as gemm_batched_res without defer writes it)
+int residual_finish(const char* tag, const ResidualRows& r, int N, int M, void* stream);
+// The deferred rows completed, then normed [N x H] = RMSNorm(y) with weights
+// w (jllm_hip_fused_rmsnorm_residual's bits), and, for N > 1, the activation
+// codes of the kinds that outs needs, in one pass where the shapes allow
+// (*quantized = true: call gemm_batched_shared_x with quantized = true).
+int norm_rows(const char* tag, const ResidualRows& r, int N, int H, uint16_t* normed, const void* w, bool w_fp32,
+              float eps, const GemmOut* outs, int n, bool* quantized, void* stream);
 
 // The decoder's supported shapes (jllm_hip_decoder_create, jllm_hip_gguf_config):
 // false, with the reason on stderr, for a configuration a later step would reject.

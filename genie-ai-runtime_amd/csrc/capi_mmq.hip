@@ -44,7 +44,7 @@ int check_gemm(const char* tag, const void* y, int type, const uint16_t* x, int 
 // of the right kind, or null for Q5_K) into y.
 int mmq_after_quant(const char* tag, void* y, const void* Wd, int type, const uint16_t* x, const void* codes,
                     const uint32_t* scl, int M, int N, int K, int out_kind, hipStream_t st,
-                    const uint16_t* res = nullptr) {
+                    const uint16_t* res = nullptr, ResidualRows* defer = nullptr) {
     // split-K when the tile grid alone does not cover the chip: partials to
     // the workspace, then one ordered reduction into y
     const int splits = out_kind == 2 ? 1 : mmq_splits(M, N, K, type);
@@ -60,6 +60,11 @@ int mmq_after_quant(const char* tag, void* y, const void* Wd, int type, const ui
     hipError_t e;
     if (type == 13) e = gemm_q5k_launch(dst, (const uint8_t*)Wd, x, M, N, K, kind, splits, st);
     else e = mmq_launch(dst, (const uint8_t*)Wd, type, codes, scl, M, N, K, npad_of(N), kind, splits, st);
+    if (e == hipSuccess && defer && res) {
+        // the residual add (and the split sum) left to the caller's next step
+        *defer = ResidualRows{(uint16_t*)y, res, splits > 1 ? (const float*)dst : nullptr, splits, splits > 1 ? 2 : 1};
+        return launch_status(e, tag);
+    }
     if (e == hipSuccess && splits > 1) e = splitk_reduce_launch(y, (const float*)dst, (int64_t)N * M, splits, out_kind, st, res);
     else if (e == hipSuccess && res) e = vec_add_launch((uint16_t*)y, (const uint16_t*)y, res, (int64_t)N * M, st);
     return launch_status(e, tag);
@@ -116,7 +121,9 @@ int run_mmq(const char* tag, void* y, const void* W, int type, const uint16_t* x
 
 namespace jllm_hip {
 int gemm_batched_res(const char* tag, uint16_t* y, const void* W, int type, const uint16_t* x, const uint16_t* up,
-                     uint16_t* act_tmp, const uint16_t* res, int M, int N, int K, void* stream) {
+                     uint16_t* act_tmp, const uint16_t* res, int M, int N, int K, void* stream,
+                     ResidualRows* defer) {
+    if (defer) *defer = ResidualRows{y, res, nullptr, 0, 0};
     int st = check_gemm(tag, y, type, x, M, N, K, true); if (st) return st;
     if (M == 0 || N == 0) return JLLM_OK;
     if (!res || (up && (!act_tmp || !aligned16(up)))) return JLLM_ERR_INVALID;
@@ -144,10 +151,50 @@ int gemm_batched_res(const char* tag, uint16_t* y, const void* W, int type, cons
         const hipError_t e = quantize_for(type, x, codes, scl, N, K, hs, up);
         if (e != hipSuccess) return launch_status(e, tag);
     }
-    return mmq_after_quant(tag, y, Wd, type, x, codes[k], scl[k], M, N, K, 0, hs, res);
+    return mmq_after_quant(tag, y, Wd, type, x, codes[k], scl[k], M, N, K, 0, hs, res, defer);
 }
 
-int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uint16_t* x, int N, int K, void* stream) {
+int residual_finish(const char* tag, const ResidualRows& r, int N, int M, void* stream) {
+    const int64_t n = (int64_t)N * M;
+    hipStream_t hs = (hipStream_t)stream;
+    if (r.mode == 2) return launch_status(splitk_reduce_launch(r.y, r.ws, n, r.S, 0, hs, r.res), tag);
+    if (r.mode == 1) return launch_status(vec_add_launch(r.y, r.y, r.res, n, hs), tag);
+    return JLLM_OK;
+}
+
+int norm_rows(const char* tag, const ResidualRows& r, int N, int H, uint16_t* normed, const void* w, bool w_fp32,
+              float eps, const GemmOut* outs, int n, bool* quantized, void* stream) {
+    *quantized = false;
+    if (N <= 0) return JLLM_OK;
+    bool need[2] = {false, false};                   // DS4 (Q4_K), D4 (Q6_K)
+    for (int i = 0; i < n; i++) {
+        if (outs[i].M == 0) continue;
+        if (outs[i].type == 12) need[0] = true;
+        if (outs[i].type == 14) need[1] = true;
+    }
+    NormQuantArgs a;
+    a.y = r.y; a.res = r.res; a.ws = r.ws; a.S = r.S; a.mode = r.mode;
+    a.normed = normed; a.w = w; a.eps = eps;
+    a.c8 = nullptr; a.s8 = nullptr; a.c16 = nullptr; a.s16 = nullptr;
+    a.N = N; a.H = H; a.Npad = N > 1 ? npad_of(N) : N;
+    if (N > 1 && H % 256 == 0 && norm_quant_supported(a, w_fp32)) {
+        void* codes[2] = {nullptr, nullptr};
+        uint32_t* scl[2] = {nullptr, nullptr};
+        if (need[0] || need[1]) {
+            int st = q8_scratch(tag, N, H, codes, scl); if (st) return st;
+        }
+        if (need[0]) { a.c8 = codes[0]; a.s8 = scl[0]; }
+        if (need[1]) { a.c16 = codes[1]; a.s16 = scl[1]; }
+        const int st = launch_status(norm_quant_launch(a, w_fp32, (hipStream_t)stream), tag);
+        if (st == JLLM_OK) *quantized = true;
+        return st;
+    }
+    int st = residual_finish(tag, r, N, H, stream); if (st) return st;
+    return jllm_hip_fused_rmsnorm_residual(normed, r.y, nullptr, w, N, H, eps, w_fp32 ? 1 : 0, stream);
+}
+
+int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uint16_t* x, int N, int K, void* stream,
+                          bool quantized) {
     for (int i = 0; i < n; i++) {
         int st = check_gemm(tag, outs[i].y, outs[i].type, x, outs[i].M, N, K, true); if (st) return st;
     }
@@ -169,7 +216,7 @@ int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uin
     }
     if (need[0] || need[1]) {
         int st = q8_scratch(tag, N, K, codes, scl); if (st) return st;
-        for (int k = 0; k < 2; k++) {
+        for (int k = 0; k < 2 && !quantized; k++) {
             if (!need[k]) continue;
             const hipError_t e = quantize_for(k == 0 ? 12 : 14, x, codes, scl, N, K, hs);
             if (e != hipSuccess) return launch_status(e, tag);

@@ -29,6 +29,9 @@ using jllm_hip::launch_status;
 using jllm_hip::GemmOut;
 using jllm_hip::gemm_batched_shared_x;
 using jllm_hip::gemm_batched_res;
+using jllm_hip::norm_rows;
+using jllm_hip::residual_finish;
+using jllm_hip::ResidualRows;
 
 struct jllm_hip_decoder {
     jllm_hip_decoder_config cfg;
@@ -104,15 +107,24 @@ int decode_layer(jllm_hip_decoder* d, int l, int pos, void* st) {
 
 // One layer over N prompt tokens at positions start..start+N-1; xb [N][H]
 // updated in place (transformer_prefill, decode.cu:1760-1884).
-int prefill_layer(jllm_hip_decoder* d, int l, int start, int N, void* st) {
+// One decoder layer over N tokens at positions start.. (the prefill).  The
+// residual adds after the O and down projections are left to the RMSNorm
+// that follows them (norm_rows: split-K sum, residual add, RMSNorm and the
+// activation codes in one pass).  *normed_q: on entry, whether normed and
+// the quantiser scratch already hold the attention RMSNorm of x and its codes
+// (the previous layer's last step); on exit, the same for layer l + 1 when
+// next is set (its attention RMSNorm formed here), else x is complete.
+int prefill_layer(jllm_hip_decoder* d, int l, int start, int N, void* st, bool* normed_q, bool next) {
     const jllm_hip_decoder_config& c = d->cfg;
     const jllm_hip_layer_weights& w = d->lw[l];
     const int H = c.hidden_dim, QD = c.n_heads * c.head_dim, KVD = c.n_kv_heads * c.head_dim, I = c.intermediate_dim;
     const size_t row = (size_t)KVD * (c.kv_int8 ? 1 : 2);
-    TRY(jllm_hip_fused_rmsnorm_residual(d->normed, d->x, nullptr, w.rms_attn, N, H, c.rms_eps, c.norm_fp32, st));
-    // Q, K, V of one quantised activation
     const GemmOut qkv[3] = {{d->q, w.wq, w.type_wq, QD}, {d->k, w.wk, w.type_wk, KVD}, {d->v, w.wv, w.type_wv, KVD}};
-    TRY(gemm_batched_shared_x("decoder", qkv, 3, d->normed, N, H, st));
+    if (!*normed_q)
+        TRY(norm_rows("decoder", ResidualRows{d->x, nullptr, nullptr, 0, 0}, N, H, d->normed, w.rms_attn,
+                      c.norm_fp32 != 0, c.rms_eps, qkv, 3, normed_q, st));
+    // Q, K, V of one quantised activation
+    TRY(gemm_batched_shared_x("decoder", qkv, 3, d->normed, N, H, st, *normed_q));
     TRY(jllm_hip_qk_norm_rope_store_kv(d->q, d->k, d->v, w.q_norm, w.k_norm, c.qk_norm_fp32, c.rms_eps,
                                        layer_k(d, l) + (size_t)start * row, layer_v(d, l) + (size_t)start * row,
                                        layer_ks(d, l) + (size_t)start * c.n_kv_heads,
@@ -122,12 +134,18 @@ int prefill_layer(jllm_hip_decoder* d, int l, int start, int N, void* st) {
                                                  c.n_kv_heads, c.head_dim, c.head_dim, N, start, attn_scale(c),
                                                  c.kv_int8, c.kv_int8 ? layer_ks(d, l) : nullptr,
                                                  c.kv_int8 ? layer_vs(d, l) : nullptr, 0, st));
-    TRY(gemm_batched_res("decoder", d->x2, w.wo, w.type_wo, d->attn, nullptr, nullptr, d->x, H, N, QD, st));
-    TRY(jllm_hip_fused_rmsnorm_residual(d->normed, d->x2, nullptr, w.rms_ffn, N, H, c.rms_eps, c.norm_fp32, st));
+    ResidualRows r;
+    TRY(gemm_batched_res("decoder", d->x2, w.wo, w.type_wo, d->attn, nullptr, nullptr, d->x, H, N, QD, st, &r));
     const GemmOut gu[2] = {{d->gate, w.w_gate, w.type_w_gate, I}, {d->up, w.w_up, w.type_w_up, I}};
-    TRY(gemm_batched_shared_x("decoder", gu, 2, d->normed, N, H, st));
-    TRY(gemm_batched_res("decoder", d->x, w.w_down, w.type_w_down, d->gate, d->up, d->act, d->x2, H, N, I, st));
-    return JLLM_OK;
+    bool q2 = false;
+    TRY(norm_rows("decoder", r, N, H, d->normed, w.rms_ffn, c.norm_fp32 != 0, c.rms_eps, gu, 2, &q2, st));
+    TRY(gemm_batched_shared_x("decoder", gu, 2, d->normed, N, H, st, q2));
+    TRY(gemm_batched_res("decoder", d->x, w.w_down, w.type_w_down, d->gate, d->up, d->act, d->x2, H, N, I, st, &r));
+    *normed_q = false;
+    if (!next) return residual_finish("decoder", r, N, H, st);
+    const jllm_hip_layer_weights& wn = d->lw[l + 1];
+    const GemmOut qkvn[3] = {{d->q, wn.wq, wn.type_wq, QD}, {d->k, wn.wk, wn.type_wk, KVD}, {d->v, wn.wv, wn.type_wv, KVD}};
+    return norm_rows("decoder", r, N, H, d->normed, wn.rms_attn, c.norm_fp32 != 0, c.rms_eps, qkvn, 3, normed_q, st);
 }
 
 // output norm -> lm_head (fp32 logits) -> greedy token into *out
@@ -253,7 +271,9 @@ int jllm_hip_decoder_prefill(jllm_hip_decoder* d, const int32_t* tokens, int N, 
         const int n = N - c0 < d->max_batch ? N - c0 : d->max_batch;
         TRY(jllm_hip_dequant_embedding_rows(d->x, d->mw.tok_embd, d->mw.embd_type, tokens + c0, n, c.hidden_dim,
                                             c.vocab_size, stream));
-        for (int l = 0; l < c.n_layers; l++) TRY(prefill_layer(d, l, start_pos + c0, n, stream));
+        bool normed_q = false;
+        for (int l = 0; l < c.n_layers; l++)
+            TRY(prefill_layer(d, l, start_pos + c0, n, stream, &normed_q, l + 1 < c.n_layers));
         if (c0 + n == N) TRY(head(d, d->x + (size_t)(n - 1) * c.hidden_dim, next_token, stream));
     }
     return JLLM_OK;
@@ -284,7 +304,9 @@ int jllm_hip_decoder_layer(jllm_hip_decoder* d, int layer, uint16_t* x, int N, i
     const size_t bytes = (size_t)N * d->cfg.hidden_dim * 2;
     hipStream_t st = (hipStream_t)stream;
     TRY(launch_status(hipMemcpyAsync(d->x, x, bytes, hipMemcpyDeviceToDevice, st), "decoder"));
-    TRY(N == 1 ? decode_layer(d, layer, start_pos, stream) : prefill_layer(d, layer, start_pos, N, stream));
+    bool normed_q = false;
+    TRY(N == 1 ? decode_layer(d, layer, start_pos, stream)
+               : prefill_layer(d, layer, start_pos, N, stream, &normed_q, false));
     return launch_status(hipMemcpyAsync(x, d->x, bytes, hipMemcpyDeviceToDevice, st), "decoder");
 }
 

@@ -25,6 +25,33 @@ inline size_t mmq_codes_bytes(int K, int Npad) { return (size_t)K * Npad * 2; } 
 inline size_t mmq_codes8_bytes(int K, int Npad) { return (size_t)K * Npad; }        // int8 layout
 inline size_t mmq_scales_bytes(int K, int Npad) { return (size_t)(K / 32) * Npad * 4; }
 
+// RMSNorm + activation quantisation of residual-stream rows y [N][H] in one
+// pass (one workgroup per row of Npad), the residual add that forms y
+// optionally in front: mode 0: y as given; 1: y = half(y + res); 2: y =
+// half(half(sum of the S fp32 partials ws[s][N][H]) + res).  normed =
+// half(y * rrms * w); the codes and scale words of each kind whose codes
+// pointer is non-null (c8/s8: int8 codes, DS4 words -- the Q4_K kernel's;
+// c16/s16: fp16 codes, D4 words -- the Q6_K kernel's).  Every output has the
+// bits of the separate residual add, rmsnorm_launch and quantiser.
+struct NormQuantArgs {
+    uint16_t* y;
+    const uint16_t* res;
+    const float* ws;
+    int S, mode;
+    uint16_t* normed;
+    const void* w;
+    float eps;
+    void* c8;
+    uint32_t* s8;
+    void* c16;
+    uint32_t* s16;
+    int N, H, Npad;
+};
+// whether norm_quant_launch takes these arguments (16-byte aligned rows, H a
+// multiple of 32 and <= 4096, w aligned like rmsnorm_launch's 16-byte path)
+bool norm_quant_supported(const NormQuantArgs& a, bool w_fp32);
+hipError_t norm_quant_launch(const NormQuantArgs& a, bool w_fp32, hipStream_t st);
+
 // out_kind: 0 = fp16 y[N x M], 1 = fp32 y[N x M], 2 = raw int32 sub-block
 // dots [N][M][K/G] (G = 32 for Q4_K, 16 for Q6_K).  splits > 1 (fp32 only):
 // K is cut into `splits` ranges of whole super-blocks and range s writes

@@ -106,36 +106,12 @@ hipError_t quantize_mmq_launch(const uint16_t* x, void* q8, int N, int K, int Np
 // x2 = up), formed here exactly as the SwiGLU kernel rounds them.
 // I8: the codes as int8 bytes [K/256][Npad][256] (the Q4_K kernel's layout)
 // instead of fp16 values.
-template <bool SW, bool I8>
-__global__ __launch_bounds__(256) void quantize_mmq_f16_kernel(const uint16_t* __restrict__ x,
-                                                               const uint16_t* __restrict__ x2,
-                                                               void* __restrict__ codes,
-                                                               uint32_t* __restrict__ scl, int N, int K, int Npad,
-                                                               int ds4) {
-    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;     // (col, kb32, sub), sub fastest
-    const int kb = K / 32;
-    const int64_t nthr = (int64_t)Npad * kb * 4;
-    if (gid >= nthr) return;                                          // whole 4-lane groups exit together
-    const int sub = (int)(gid & 3);
-    const int64_t cb = gid >> 2;
-    const int kb32 = (int)(cb % kb), col = (int)(cb / kb);
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
-    if (col < N) {
-        const int64_t off = (int64_t)col * K + kb32 * 32 + 8 * sub;
-        const u32x4m u = *(const u32x4m*)(x + off);
-        w[0] = u.x; w[1] = u.y; w[2] = u.z; w[3] = u.w;
-        if (SW) {
-            const u32x4m u2 = *(const u32x4m*)(x2 + off);
-            const uint32_t w2[4] = {u2.x, u2.y, u2.z, u2.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                w[e] = (uint32_t)f32_to_f16_bits(silu_mul(f16_bits_to_f32(w[e] & 0xFFFFu), f16_bits_to_f32(w2[e] & 0xFFFFu))) |
-                       ((uint32_t)f32_to_f16_bits(silu_mul(f16_bits_to_f32(w[e] >> 16), f16_bits_to_f32(w2[e] >> 16))) << 16);
-        }
-    }
-    float v[8];
-#pragma unroll
-    for (int e = 0; e < 4; e++) { v[2 * e] = f16_bits_to_f32(w[e] & 0xFFFFu); v[2 * e + 1] = f16_bits_to_f32(w[e] >> 16); }
+// The quantisation of one lane's 8 values v: sub-chunk `sub` (0..3, the
+// lane's index within its aligned group of 4 lanes) of 32-value block kb32
+// of token col.  All 4 lanes of the group call it together.
+template <bool I8>
+__device__ __forceinline__ void quant_chunk(const float (&v)[8], int sub, int kb32, int col, int Npad, void* codes,
+                                            uint32_t* scl, bool ds4) {
     float amax = 0.0f, t[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) { amax = fmaxf(amax, fabsf(v[e])); t[e] = v[e]; }
@@ -173,6 +149,165 @@ __global__ __launch_bounds__(256) void quantize_mmq_f16_kernel(const uint16_t* _
     if (sub == 0)
         scl[(int64_t)kb32 * Npad + col] =
             ds4 ? ((uint32_t)f32_to_f16_bits(d) | ((uint32_t)f32_to_f16_bits(sum) << 16)) : __builtin_bit_cast(uint32_t, d);
+}
+
+template <bool SW, bool I8>
+__global__ __launch_bounds__(256) void quantize_mmq_f16_kernel(const uint16_t* __restrict__ x,
+                                                               const uint16_t* __restrict__ x2,
+                                                               void* __restrict__ codes,
+                                                               uint32_t* __restrict__ scl, int N, int K, int Npad,
+                                                               int ds4) {
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;     // (col, kb32, sub), sub fastest
+    const int kb = K / 32;
+    const int64_t nthr = (int64_t)Npad * kb * 4;
+    if (gid >= nthr) return;                                          // whole 4-lane groups exit together
+    const int sub = (int)(gid & 3);
+    const int64_t cb = gid >> 2;
+    const int kb32 = (int)(cb % kb), col = (int)(cb / kb);
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    if (col < N) {
+        const int64_t off = (int64_t)col * K + kb32 * 32 + 8 * sub;
+        const u32x4m u = *(const u32x4m*)(x + off);
+        w[0] = u.x; w[1] = u.y; w[2] = u.z; w[3] = u.w;
+        if (SW) {
+            const u32x4m u2 = *(const u32x4m*)(x2 + off);
+            const uint32_t w2[4] = {u2.x, u2.y, u2.z, u2.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                w[e] = (uint32_t)f32_to_f16_bits(silu_mul(f16_bits_to_f32(w[e] & 0xFFFFu), f16_bits_to_f32(w2[e] & 0xFFFFu))) |
+                       ((uint32_t)f32_to_f16_bits(silu_mul(f16_bits_to_f32(w[e] >> 16), f16_bits_to_f32(w2[e] >> 16))) << 16);
+        }
+    }
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; e++) { v[2 * e] = f16_bits_to_f32(w[e] & 0xFFFFu); v[2 * e + 1] = f16_bits_to_f32(w[e] >> 16); }
+    quant_chunk<I8>(v, sub, kb32, col, Npad, codes, scl, ds4 != 0);
+}
+
+// RMSNorm and the MMQ activation quantisation of a block of residual-stream
+// rows in one pass, the residual add that produces the rows optionally in
+// front (the decoder's prefill).  One GS-thread workgroup per token row
+// (rows N .. Npad-1: padding, zero codes).  Per row:
+//   MODE 0: v = y (read only);
+//   MODE 1: y = half(y + res) (the residual add of vec_add);
+//   MODE 2: y = half(half(sum_s ws[s]) + res) (splitk_reduce_kernel<2>, the
+//           partials added in order s = 0, 1, ...);
+// then normed = half(v * rrms * w) with the sum of squares taken in the
+// order of rmsnorm_kernel<GS, 8> (thread t: chunks t, t + GS, ...; pairs;
+// wave_sum; for GS = 256 the four wave sums as (0 + 1) + (2 + 3)), and the
+// normed values quantised by quant_chunk for the kinds whose codes pointer
+// is set -- so every output has the bits of the separate kernels.
+template <bool WF32, int GS, int MODE>
+__global__ __launch_bounds__(GS) void norm_quant_kernel(NormQuantArgs a) {
+#pragma clang fp contract(off)
+    __shared__ float red[4];
+    constexpr int MAXC = 2;                              // chunks per thread: dim <= 2 * GS * 8
+    const int t = threadIdx.x, n = blockIdx.x, H = a.H;
+    const bool live = n < a.N;
+    const int64_t off = (int64_t)(live ? n : 0) * H;
+    float v[MAXC][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < MAXC; c++) {
+        const int i = (t + GS * c) * 8;
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[c][e] = 0.0f;
+        if (!live || i >= H) continue;
+        const u32x4m u = *(const u32x4m*)(a.y + off + i);
+        uint32_t w[4] = {u.x, u.y, u.z, u.w};
+        if (MODE == 1) {
+            const u32x4m r = *(const u32x4m*)(a.res + off + i);
+            const uint32_t rr[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                w[e] = (uint32_t)f32_to_f16_bits(f16_bits_to_f32(w[e] & 0xFFFFu) + f16_bits_to_f32(rr[e] & 0xFFFFu)) |
+                       ((uint32_t)f32_to_f16_bits(f16_bits_to_f32(w[e] >> 16) + f16_bits_to_f32(rr[e] >> 16)) << 16);
+        } else if (MODE == 2) {
+            const int64_t nm = (int64_t)a.N * H;
+            f32x4m p0 = *(const f32x4m*)(a.ws + off + i), p1 = *(const f32x4m*)(a.ws + off + i + 4);
+            for (int s = 1; s < a.S; s++) {
+                const f32x4m q0 = *(const f32x4m*)(a.ws + (int64_t)s * nm + off + i);
+                const f32x4m q1 = *(const f32x4m*)(a.ws + (int64_t)s * nm + off + i + 4);
+                p0.x += q0.x; p0.y += q0.y; p0.z += q0.z; p0.w += q0.w;
+                p1.x += q1.x; p1.y += q1.y; p1.z += q1.z; p1.w += q1.w;
+            }
+            const float ps[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+            const u32x4m r = *(const u32x4m*)(a.res + off + i);
+            const uint32_t rr[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                w[e] = (uint32_t)f32_to_f16_bits(round_to_f16(ps[2 * e]) + f16_bits_to_f32(rr[e] & 0xFFFFu)) |
+                       ((uint32_t)f32_to_f16_bits(round_to_f16(ps[2 * e + 1]) + f16_bits_to_f32(rr[e] >> 16)) << 16);
+        }
+        if (MODE != 0) *(u32x4m*)(a.y + off + i) = u32x4m{w[0], w[1], w[2], w[3]};
+#pragma unroll
+        for (int e = 0; e < 4; e++) { v[c][2 * e] = f16_bits_to_f32(w[e] & 0xFFFFu); v[c][2 * e + 1] = f16_bits_to_f32(w[e] >> 16); }
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) ss += v[c][e] * v[c][e] + v[c][e + 1] * v[c][e + 1];
+    }
+    ss = wave_sum(ss);
+    if (GS == 256) {
+        if ((t & 63) == 0) red[t >> 6] = ss;
+        __syncthreads();
+        ss = (red[0] + red[1]) + (red[2] + red[3]);
+    }
+    const float rrms = 1.0f / sqrtf(ss / (float)H + a.eps);
+#pragma unroll
+    for (int c = 0; c < MAXC; c++) {
+        const int ci = t + GS * c, i = ci * 8;
+        if (i >= H) continue;                            // whole 4-lane groups (H % 32 == 0)
+        float q[8];
+        if (live) {
+            float wv[8];
+            if (WF32) {
+                const f32x4m w0 = *(const f32x4m*)((const float*)a.w + i), w1 = *(const f32x4m*)((const float*)a.w + i + 4);
+                wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w; wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+            } else {
+                const u32x4m hw = *(const u32x4m*)((const uint16_t*)a.w + i);
+                const uint32_t h[4] = {hw.x, hw.y, hw.z, hw.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) { wv[2 * e] = f16_bits_to_f32(h[e] & 0xFFFFu); wv[2 * e + 1] = f16_bits_to_f32(h[e] >> 16); }
+            }
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                o[e] = (uint32_t)f32_to_f16_bits(v[c][2 * e] * rrms * wv[2 * e]) |
+                       ((uint32_t)f32_to_f16_bits(v[c][2 * e + 1] * rrms * wv[2 * e + 1]) << 16);
+            *(u32x4m*)(a.normed + off + i) = u32x4m{o[0], o[1], o[2], o[3]};
+#pragma unroll
+            for (int e = 0; e < 4; e++) { q[2 * e] = f16_bits_to_f32(o[e] & 0xFFFFu); q[2 * e + 1] = f16_bits_to_f32(o[e] >> 16); }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) q[e] = 0.0f;
+        }
+        if (a.c8) quant_chunk<true>(q, ci & 3, ci >> 2, n, a.Npad, a.c8, a.s8, true);
+        if (a.c16) quant_chunk<false>(q, ci & 3, ci >> 2, n, a.Npad, a.c16, a.s16, false);
+    }
+}
+
+template <bool WF32, int GS>
+static void norm_quant_go(const NormQuantArgs& a, hipStream_t st) {
+    const dim3 g((unsigned)a.Npad), b(GS);
+    if (a.mode == 0) hipLaunchKernelGGL((norm_quant_kernel<WF32, GS, 0>), g, b, 0, st, a);
+    else if (a.mode == 1) hipLaunchKernelGGL((norm_quant_kernel<WF32, GS, 1>), g, b, 0, st, a);
+    else hipLaunchKernelGGL((norm_quant_kernel<WF32, GS, 2>), g, b, 0, st, a);
+}
+
+bool norm_quant_supported(const NormQuantArgs& a, bool w_fp32) {
+    const uintptr_t al = (uintptr_t)a.y | (uintptr_t)a.normed | (uintptr_t)(a.res ? a.res : a.y) |
+                         (uintptr_t)(a.ws ? a.ws : (const float*)a.y);
+    return a.H > 0 && a.H % 32 == 0 && a.H <= 4096 && a.N >= 0 && a.Npad >= a.N && al % 16 == 0 &&
+           (uintptr_t)a.w % (w_fp32 ? 32 : 16) == 0 && a.mode >= 0 && a.mode <= 2 &&
+           (a.mode != 2 || a.S >= 1);
+}
+
+hipError_t norm_quant_launch(const NormQuantArgs& a, bool w_fp32, hipStream_t st) {
+    if (!norm_quant_supported(a, w_fp32)) return hipErrorInvalidValue;
+    if (a.Npad == 0) return hipSuccess;
+    // the thread count per row of rmsnorm_kernel for this width
+    if (w_fp32) { if (a.H > 1024) norm_quant_go<true, 256>(a, st); else norm_quant_go<true, 64>(a, st); }
+    else        { if (a.H > 1024) norm_quant_go<false, 256>(a, st); else norm_quant_go<false, 64>(a, st); }
+    return hipGetLastError();
 }
 
 hipError_t quantize_mmq_f16_launch(const uint16_t* x, void* codes, uint32_t* scl, int N, int K, int Npad,
