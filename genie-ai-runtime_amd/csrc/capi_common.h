@@ -75,6 +75,16 @@ struct DeviceScratch {
 struct GemmOut { uint16_t* y; const void* W; int type; int M; };
 int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uint16_t* x, int N, int K, void* stream,
                           bool quantized = false);
+// The decoder's prefill Q/K/V of one activation x (normed, quantised
+// already when `quantized`) with the attention front fa (q/k RMSNorm, RoPE,
+// KV-cache store) in the GEMM's epilogue, when the shapes allow it (all
+// three Q4_K, head_dim 128, a grid that needs no split-K): *done = true and
+// every output as gemm_batched_shared_x followed by
+// jllm_hip_qk_norm_rope_store_kv would leave it; else *done = false and
+// nothing ran.
+struct QKPostArgs;
+int qkv_front_prefill(const char* tag, const GemmOut* qkv, const uint16_t* x, int N, int K, bool quantized,
+                      const QKPostArgs& fa, void* stream, bool* done);
 // Rows of the residual stream whose residual add is left to the next step
 // (gemm_batched_res with `defer`): mode 0: y [N x M] is complete; 1: y holds
 // the product, y = half(y + res) still to do; 2: the product is still S

@@ -193,6 +193,38 @@ int norm_rows(const char* tag, const ResidualRows& r, int N, int H, uint16_t* no
     return jllm_hip_fused_rmsnorm_residual(normed, r.y, nullptr, w, N, H, eps, w_fp32 ? 1 : 0, stream);
 }
 
+int qkv_front_prefill(const char* tag, const GemmOut* qkv, const uint16_t* x, int N, int K, bool quantized,
+                      const QKPostArgs& fa, void* stream, bool* done) {
+    *done = false;
+    if (N <= 1 || fa.head_dim != 128 || fa.N != N || (fa.q_norm == nullptr) != (fa.k_norm == nullptr)) return JLLM_OK;
+    const uint8_t* Wm[3];
+    uint16_t* ym[3];
+    int Mm[3];
+    int64_t rtiles = 0;
+    for (int i = 0; i < 3; i++) {
+        if (qkv[i].type != 12 || qkv[i].M <= 0 || qkv[i].M % 128) return JLLM_OK;
+        int st = check_gemm(tag, qkv[i].y, qkv[i].type, x, qkv[i].M, N, K, true); if (st) return st;
+        const void* Wd = device_weight(tag, qkv[i].W);
+        if (!Wd) return JLLM_ERR_POINTER;
+        if (!aligned16(Wd)) return JLLM_ERR_INVALID;
+        Wm[i] = (const uint8_t*)Wd; ym[i] = qkv[i].y; Mm[i] = qkv[i].M;
+        rtiles += qkv[i].M / 128;
+    }
+    if (rtiles * (npad_of(N) / MMQ_TILE_N) < MMQ_MULTI_MIN_TILES) return JLLM_OK;
+    hipStream_t hs = (hipStream_t)stream;
+    void* codes[2] = {nullptr, nullptr};
+    uint32_t* scl[2] = {nullptr, nullptr};
+    int st = q8_scratch(tag, N, K, codes, scl); if (st) return st;
+    if (!quantized) {
+        const hipError_t e = quantize_for(12, x, codes, scl, N, K, hs);
+        if (e != hipSuccess) return launch_status(e, tag);
+    }
+    st = launch_status(mmq_q4k_qkv_front_launch(Wm, ym, Mm, (const uint8_t*)codes[0], scl[0], N, K, npad_of(N), fa,
+                                                hs), tag);
+    if (st == JLLM_OK) *done = true;
+    return st;
+}
+
 int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uint16_t* x, int N, int K, void* stream,
                           bool quantized) {
     for (int i = 0; i < n; i++) {

@@ -24,6 +24,7 @@
 #include <string.h>
 #include <new>
 #include "capi_common.h"
+#include "layer_ops.h"
 
 using jllm_hip::launch_status;
 using jllm_hip::GemmOut;
@@ -32,6 +33,8 @@ using jllm_hip::gemm_batched_res;
 using jllm_hip::norm_rows;
 using jllm_hip::residual_finish;
 using jllm_hip::ResidualRows;
+using jllm_hip::qkv_front_prefill;
+using jllm_hip::QKPostArgs;
 
 struct jllm_hip_decoder {
     jllm_hip_decoder_config cfg;
@@ -123,13 +126,27 @@ int prefill_layer(jllm_hip_decoder* d, int l, int start, int N, void* st, bool* 
     if (!*normed_q)
         TRY(norm_rows("decoder", ResidualRows{d->x, nullptr, nullptr, 0, 0}, N, H, d->normed, w.rms_attn,
                       c.norm_fp32 != 0, c.rms_eps, qkv, 3, normed_q, st));
-    // Q, K, V of one quantised activation
-    TRY(gemm_batched_shared_x("decoder", qkv, 3, d->normed, N, H, st, *normed_q));
-    TRY(jllm_hip_qk_norm_rope_store_kv(d->q, d->k, d->v, w.q_norm, w.k_norm, c.qk_norm_fp32, c.rms_eps,
-                                       layer_k(d, l) + (size_t)start * row, layer_v(d, l) + (size_t)start * row,
-                                       layer_ks(d, l) + (size_t)start * c.n_kv_heads,
-                                       layer_vs(d, l) + (size_t)start * c.n_kv_heads, KVD, c.n_heads, c.n_kv_heads,
-                                       c.head_dim, c.head_dim, start, N, c.rope_theta, c.rope_neox, c.kv_int8, st));
+    // Q, K, V of one quantised activation, then the attention front (q/k
+    // norm, RoPE, KV store) -- in the GEMM's epilogue where the shapes allow
+    QKPostArgs fa;
+    fa.q = d->q; fa.k = d->k; fa.v = d->v; fa.q_norm = w.q_norm; fa.k_norm = w.k_norm;
+    fa.k_dst = layer_k(d, l) + (size_t)start * row; fa.v_dst = layer_v(d, l) + (size_t)start * row;
+    fa.k_scales = c.kv_int8 ? layer_ks(d, l) + (size_t)start * c.n_kv_heads : nullptr;
+    fa.v_scales = c.kv_int8 ? layer_vs(d, l) + (size_t)start * c.n_kv_heads : nullptr;
+    fa.kv_stride = KVD; fa.n_heads = c.n_heads; fa.n_kv = c.n_kv_heads; fa.head_dim = c.head_dim;
+    fa.cache_head_dim = c.head_dim; fa.start_pos = start; fa.N = N; fa.eps = c.rms_eps;
+    fa.norm_fp32 = c.qk_norm_fp32 != 0; fa.neox = c.rope_neox != 0; fa.kv_int8 = c.kv_int8 != 0;
+    jllm_hip::rope_frequencies(fa.fr, c.head_dim, c.rope_theta);
+    bool fused = false;
+    TRY(qkv_front_prefill("decoder", qkv, d->normed, N, H, *normed_q, fa, st, &fused));
+    if (!fused) {
+        TRY(gemm_batched_shared_x("decoder", qkv, 3, d->normed, N, H, st, *normed_q));
+        TRY(jllm_hip_qk_norm_rope_store_kv(d->q, d->k, d->v, w.q_norm, w.k_norm, c.qk_norm_fp32, c.rms_eps,
+                                           fa.k_dst, fa.v_dst, layer_ks(d, l) + (size_t)start * c.n_kv_heads,
+                                           layer_vs(d, l) + (size_t)start * c.n_kv_heads, KVD, c.n_heads,
+                                           c.n_kv_heads, c.head_dim, c.head_dim, start, N, c.rope_theta,
+                                           c.rope_neox, c.kv_int8, st));
+    }
     TRY(jllm_hip_flash_attention_prefill_batched(d->attn, d->q, layer_k(d, l), layer_v(d, l), c.n_heads,
                                                  c.n_kv_heads, c.head_dim, c.head_dim, N, start, attn_scale(c),
                                                  c.kv_int8, c.kv_int8 ? layer_ks(d, l) : nullptr,

@@ -282,20 +282,7 @@ __global__ __launch_bounds__(256) void qk_post_kernel(QKPostArgs a) {
     const int p0 = a.pos_dev ? __builtin_amdgcn_readfirstlane(pd) : a.start_pos;
     const int64_t r0 = a.pos_dev ? p0 : 0;            // cache row of token 0 relative to k_dst / v_dst
     const int pos = p0 + t;
-    float s = 0.0f, c = 1.0f;
-    if (kind < 2) sincosf((float)pos * fq, &s, &c);
-    front_apply(norm != nullptr, w0, w1, hd, a.eps, kind < 2, c, s, v0, v1);
-    if (kind < 2 && act) {
-        uint16_t* dq = kind == 0 ? a.q + t * qs + (int64_t)head * hd : a.k + t * ks + (int64_t)head * hd;
-        dq[i0] = f32_to_f16_bits(v0);
-        dq[i1] = f32_to_f16_bits(v1);
-    }
-    if (kind == 0) return;
-    const int64_t row = (r0 + t) * a.kv_stride + (int64_t)head * a.cache_head_dim;
-    void* cache = kind == 1 ? a.k_dst : a.v_dst;
-    float* sc = kind == 1 ? a.k_scales : a.v_scales;
-    front_store_kv(a.kv_int8 ? (void*)((int8_t*)cache + row) : (void*)((uint16_t*)cache + row),
-                   sc ? sc + (r0 + t) * a.n_kv + head : nullptr, a.kv_int8 != 0, hd, v0, v1, i0, i1, l);
+    front_finish(a, kind, head, t, r0, pos, l, act, i0, i1, v0, v1, w0, w1, fq, qs, ks);
 }
 
 hipError_t qk_post_launch(const QKPostArgs& a, hipStream_t st) {

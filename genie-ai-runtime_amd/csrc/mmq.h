@@ -78,6 +78,18 @@ constexpr int MMQ_MULTI_MIN_TILES = 384;
 hipError_t mmq_q4k_multi_launch(const uint8_t* const* W, void* const* y, const int* M, int nseg, const uint8_t* codes,
                                 const uint32_t* scl, int N, int K, int Npad, hipStream_t st);
 
+// The decoder's prefill Q/K/V (all Q4_K, no split) with the attention front
+// (qk_post_kernel's step: q/k RMSNorm, RoPE, the KV-cache store) run in the
+// tiles' epilogue: head_dim 128 (one workgroup tile = one head), y[0..2] =
+// fa.q / fa.k / fa.v with packed rows, M = heads x 128; fa's other fields as
+// qk_post_launch takes them (start_pos: position of token 0, k_dst / v_dst /
+// scales addressing token 0's row).  Every output has the bits of the plain
+// launch followed by qk_post_launch.
+struct QKPostArgs;
+hipError_t mmq_q4k_qkv_front_launch(const uint8_t* const* W, uint16_t* const* y, const int* M, const uint8_t* codes,
+                                    const uint32_t* scl, int N, int K, int Npad, const QKPostArgs& fa,
+                                    hipStream_t st);
+
 // Split count for an N x M x K GEMM of weight type `type`: ranges of whole
 // super-blocks chosen by a measured cost model (at most 16 ranges for Q4_K /
 // Q5_K, 19 for Q6_K); a function of M, N, K and the type only.

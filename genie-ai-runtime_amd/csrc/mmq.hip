@@ -37,6 +37,7 @@
 // (blockIdx % 8) works on a contiguous range of row tiles.
 #include "kq_common.h"
 #include "mmq.h"
+#include "qk_front.h"
 #include <algorithm>
 
 namespace jllm_hip {
@@ -408,10 +409,12 @@ typedef __attribute__((address_space(3))) void lds_void;
 // distinct 16-byte bank groups
 __host__ __device__ __forceinline__ int swz_b(int tok) { return (tok ^ (tok >> 3)) & 7; }
 
-template <int OUT>   // 0: fp16 y [N][M], 1: fp32 y [N][M], 2: int32 dots [N][M][K/32]
-__global__ __launch_bounds__(MMQ_THREADS, 3)
-void mmq_q4k_kernel(MmqSegs sg, const uint8_t* __restrict__ codes,
-                    const uint32_t* __restrict__ scl, int N, int K, int Npad, int sps) {
+// OUT: 0: fp16 y [N][M], 1: fp32 y [N][M], 2: int32 dots [N][M][K/32], 3:
+// fp16 y of the Q/K/V multi-launch followed by the attention front (fa)
+template <int OUT>
+__device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* __restrict__ codes,
+                                             const uint32_t* __restrict__ scl, int N, int K, int Npad, int sps,
+                                             const QKPostArgs* fa) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[NRING * ST_BYTES];
 
     const int nb = K / QK_K, nst = 2 * nb;
@@ -601,6 +604,46 @@ void mmq_q4k_kernel(MmqSegs sg, const uint8_t* __restrict__ codes,
         __builtin_amdgcn_s_barrier();
     }
     if (OUT == 2) return;
+    if (OUT == 3) {
+        // The tile is one head (128 rows) of q, k or v (segment 0 / 1 / 2)
+        // for 64 tokens.  Its fp16 values (y as the plain launch stores it)
+        // go to LDS, [token][row] with rows padded to FT_LD halves, then
+        // each wave runs the attention front (qk_post_kernel's front_finish)
+        // for 16 tokens: lane l holds the rotary pair (i0, i1); v is also
+        // stored as y.
+        constexpr int FT_LD = 130;
+        static_assert(64 * FT_LD * 2 <= NRING * ST_BYTES, "front tile exceeds the LDS ring");
+        uint16_t* T = (uint16_t*)smem;
+        __builtin_amdgcn_s_waitcnt(0);                 // the ring's last DMA has landed
+        __syncthreads();
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+            for (int v = 0; v < 16; v++)
+                T[(32 * tt + li) * FT_LD + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3)] = f32_to_f16_bits(acc[tt][v]);
+        __syncthreads();
+        const QKPostArgs& a = *fa;
+        const int kind = sgi, head = rt - sg.rt0[sgi];
+        const int64_t qs = (int64_t)a.n_heads * 128, ks = (int64_t)a.n_kv * 128;
+        int i0, i1;
+        front_idx(128, a.neox != 0, l, i0, i1);
+        const void* norm = kind < 2 ? (kind == 0 ? a.q_norm : a.k_norm) : nullptr;
+        float w0 = 0.0f, w1 = 0.0f;
+        front_weights(norm, a.norm_fp32 != 0, true, i0, i1, w0, w1);
+        const float fq = a.fr.f[l];
+        for (int j = 0; j < 16; j++) {
+            const int tl = 16 * w + j, tok = col0 + tl;
+            if (tok >= N) break;                       // uniform across the wave
+            const float v0 = f16_bits_to_f32(T[tl * FT_LD + i0]), v1 = f16_bits_to_f32(T[tl * FT_LD + i1]);
+            if (kind == 2) {
+                uint16_t* yv = (uint16_t*)y + (int64_t)tok * M + row0;
+                yv[i0] = T[tl * FT_LD + i0];
+                yv[i1] = T[tl * FT_LD + i1];
+            }
+            front_finish(a, kind, head, tok, 0, a.start_pos + tok, l, true, i0, i1, v0, v1, w0, w1, fq, qs, ks);
+        }
+        return;
+    }
 #pragma unroll
     for (int tt = 0; tt < 2; tt++) {
         const int tok = col0 + 32 * tt + li;
@@ -613,6 +656,19 @@ void mmq_q4k_kernel(MmqSegs sg, const uint8_t* __restrict__ codes,
             }
         }
     }
+}
+
+template <int OUT>
+__global__ __launch_bounds__(MMQ_THREADS, 3)
+void mmq_q4k_kernel(MmqSegs sg, const uint8_t* __restrict__ codes, const uint32_t* __restrict__ scl, int N, int K,
+                    int Npad, int sps) {
+    mmq_q4k_body<OUT>(sg, codes, scl, N, K, Npad, sps, nullptr);
+}
+
+__global__ __launch_bounds__(MMQ_THREADS, 3)
+void mmq_q4k_front_kernel(MmqSegs sg, const uint8_t* __restrict__ codes, const uint32_t* __restrict__ scl, int N,
+                          int K, int Npad, QKPostArgs fa) {
+    mmq_q4k_body<3>(sg, codes, scl, N, K, Npad, K / QK_K, &fa);
 }
 
 // ---------------------------------------------------------------------------
@@ -937,6 +993,23 @@ hipError_t mmq_q4k_multi_launch(const uint8_t* const* W, void* const* y, const i
     }
     const dim3 grid(sg.rt0[3] * (Npad / TN), 1);
     hipLaunchKernelGGL(mmq_q4k_kernel<0>, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, K / QK_K);
+    return hipGetLastError();
+}
+
+hipError_t mmq_q4k_qkv_front_launch(const uint8_t* const* W, uint16_t* const* y, const int* M, const uint8_t* codes,
+                                    const uint32_t* scl, int N, int K, int Npad, const QKPostArgs& fa,
+                                    hipStream_t st) {
+    if (fa.head_dim != TM || M[0] != fa.n_heads * TM || M[1] != fa.n_kv * TM || M[2] != fa.n_kv * TM ||
+        fa.q != y[0] || fa.k != y[1] || fa.v != y[2] || fa.q_in_stride || fa.kv_in_stride || fa.pos_dev)
+        return hipErrorInvalidValue;
+    MmqSegs sg;
+    sg.rt0[0] = 0;
+    for (int i = 0; i < 3; i++) {
+        sg.W[i] = W[i]; sg.y[i] = y[i]; sg.M[i] = M[i];
+        sg.rt0[i + 1] = sg.rt0[i] + M[i] / TM;
+    }
+    const dim3 grid(sg.rt0[3] * (Npad / TN), 1);
+    hipLaunchKernelGGL(mmq_q4k_front_kernel, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, fa);
     return hipGetLastError();
 }
 

@@ -8,6 +8,7 @@
 // (decode.cu:1441-1478).
 #pragma once
 #include "kq_common.h"
+#include "layer_ops.h"
 
 namespace jllm_hip {
 
@@ -87,6 +88,32 @@ __device__ __forceinline__ void front_store_kv(void* row, float* sc, bool kv_int
         ((uint16_t*)row)[i0] = f32_to_f16_bits(v0);
         ((uint16_t*)row)[i1] = f32_to_f16_bits(v1);
     }
+}
+
+// The rest of the attention-front step of one (token t, head) of kind 0 /
+// 1 / 2 (q / k / v) once the lane's raw pair values v0, v1 and norm weights
+// w0, w1 are in registers: q and k normalised and rotated (position pos,
+// frequency fq) and written back as fp16 into a.q / a.k (row strides qs /
+// ks), k and v stored into the KV cache at row r0 + t.
+__device__ __forceinline__ void front_finish(const QKPostArgs& a, int kind, int head, int t, int64_t r0, int pos,
+                                             int l, bool act, int i0, int i1, float v0, float v1, float w0,
+                                             float w1, float fq, int64_t qs, int64_t ks) {
+    const int hd = a.head_dim;
+    const void* norm = kind < 2 ? (kind == 0 ? a.q_norm : a.k_norm) : nullptr;
+    float s = 0.0f, c = 1.0f;
+    if (kind < 2) sincosf((float)pos * fq, &s, &c);
+    front_apply(norm != nullptr, w0, w1, hd, a.eps, kind < 2, c, s, v0, v1);
+    if (kind < 2 && act) {
+        uint16_t* dq = kind == 0 ? a.q + t * qs + (int64_t)head * hd : a.k + t * ks + (int64_t)head * hd;
+        dq[i0] = f32_to_f16_bits(v0);
+        dq[i1] = f32_to_f16_bits(v1);
+    }
+    if (kind == 0) return;
+    const int64_t row = (r0 + t) * a.kv_stride + (int64_t)head * a.cache_head_dim;
+    void* cache = kind == 1 ? a.k_dst : a.v_dst;
+    float* sc = kind == 1 ? a.k_scales : a.v_scales;
+    front_store_kv(a.kv_int8 ? (void*)((int8_t*)cache + row) : (void*)((uint16_t*)cache + row),
+                   sc ? sc + (r0 + t) * a.n_kv + head : nullptr, a.kv_int8 != 0, hd, v0, v1, i0, i1, l);
 }
 
 }  // namespace jllm_hip

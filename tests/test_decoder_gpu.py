@@ -146,7 +146,7 @@ def test_decoder_rejects_bad_config(dev):
     d.close()
 
 
-@pytest.mark.parametrize("preset,N", [("q4km", 300), ("q4km", 64), ("q5km", 300)])
+@pytest.mark.parametrize("preset,N", [("q4km", 512), ("q4km", 300), ("q4km", 64), ("q5km", 300)])
 def test_decoder_prefill_layer_equals_c_abi_composition(dev, preset, N):
     """One prefill layer of the decoder (whose residual adds, RMSNorms and
     activation quantisation run fused, one pass per norm) is bit-identical to
