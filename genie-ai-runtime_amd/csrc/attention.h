@@ -31,6 +31,13 @@ struct AttnArgs {
     // softmax states are combined in LDS in wave order (decode: into the
     // output, or into the workgroup's partial when n_splits > 1).
     int wsplit;
+    // prefill with several waves per workgroup: when qcodes is set the
+    // output rows are also quantised for the next GEMM, as the MMQ
+    // activation quantiser would from the fp16 output: int8 codes and DS4
+    // words (q_i8) or fp16 codes and D4 words, q_npad token rows
+    void* qcodes = nullptr;
+    uint32_t* qscl = nullptr;
+    int q_npad = 0, q_i8 = 1;
 };
 constexpr int ATTN_MAX_WAVES = 8;
 // measured (512-token prefill, one layer): 1 wave 41.4 us, 2 waves 37.5 us, 4 waves 38.6 us; with the

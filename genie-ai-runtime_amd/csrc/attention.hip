@@ -34,6 +34,7 @@
 #include <string.h>
 #include "kq_common.h"
 #include "attention.h"
+#include "quant_chunk.h"
 
 #ifndef ATTN_RED_XCD
 #define ATTN_RED_XCD 1
@@ -600,6 +601,16 @@ void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) { ot[2 * i] = (uint16_t)(o[i] & 0xFFFFu); ot[2 * i + 1] = (uint16_t)(o[i] >> 16); }
             }
+            if (a.qcodes) {
+                // the 4 lanes of an aligned quad hold the 32 values of one
+                // quantiser block (hd % 32 == 0, nd8 % 4 == 0)
+                float v[8];
+#pragma unroll
+                for (int i = 0; i < 4; i++) { v[2 * i] = f16_bits_to_f32(o[i] & 0xFFFFu); v[2 * i + 1] = f16_bits_to_f32(o[i] >> 16); }
+                const int kb32 = ((pbase + ch) * hd + d0) >> 5, sub = (d0 >> 3) & 3;
+                if (a.q_i8) quant_chunk<true>(v, sub, kb32, tok0 + ct, a.q_npad, a.qcodes, a.qscl, true);
+                else        quant_chunk<false>(v, sub, kb32, tok0 + ct, a.q_npad, a.qcodes, a.qscl, false);
+            }
         }
         return;
     }
@@ -783,6 +794,7 @@ hipError_t attn_launch(const AttnArgs& a, bool kv_int8, hipStream_t st) {
     const bool mt = a.tq > 1;
     const int W = a.wsplit;
     if (W < 1 || W > ATTN_MAX_WAVES) return hipErrorInvalidValue;
+    if (a.qcodes && (!mt || W < 2 || a.head_dim % 32 || !a.qscl || a.q_npad < a.tokens)) return hipErrorInvalidValue;
     const size_t lds = attn_lds_bytes(a.n_heads, a.n_kv, a.head_dim, a.tq, W);
     const bool g4 = !mt && a.n_heads / a.n_kv <= 4;
 #define ATTN_CASE(I8, HDV)                                                                                   \

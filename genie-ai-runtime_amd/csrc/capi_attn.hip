@@ -159,6 +159,17 @@ int jllm_hip_flash_attention_prefill_batched(uint16_t* out, const uint16_t* q, c
                                              int n_heads, int n_kv_heads, int head_dim, int cache_head_dim, int N,
                                              int start_pos, float scale, int kv_int8, const float* k_scales,
                                              const float* v_scales, int window, void* stream) {
+    return jllm_hip::prefill_attention(out, q, k, v, n_heads, n_kv_heads, head_dim, cache_head_dim, N, start_pos, scale,
+                                       kv_int8, k_scales, v_scales, window, nullptr, stream, nullptr);
+}
+}  // extern "C"
+
+namespace jllm_hip {
+int prefill_attention(uint16_t* out, const uint16_t* q, const void* k, const void* v, int n_heads, int n_kv_heads,
+                      int head_dim, int cache_head_dim, int N, int start_pos, float scale, int kv_int8,
+                      const float* k_scales, const float* v_scales, int window, const AttnQuant* quant, void* stream,
+                      bool* quantized) {
+    if (quantized) *quantized = false;
     if (N < 0 || start_pos < 0 || N > 65535) return JLLM_ERR_INVALID;
     if (N == 0) return JLLM_OK;
     int st = attn_check(out, q, k, v, n_heads, n_kv_heads, head_dim, cache_head_dim, start_pos + 1, kv_int8, window);
@@ -172,8 +183,15 @@ int jllm_hip_flash_attention_prefill_batched(uint16_t* out, const uint16_t* q, c
     a.tq = ATTN_MAX_COLUMNS / (n_heads / n_kv_heads);
     if (a.tq < 1) a.tq = 1;
     a.wsplit = ATTN_PREFILL_WAVES;     // (used when tq > 1)
-    return launch_status(attn_launch(a, kv_int8 != 0, (hipStream_t)stream), "attention prefill");
+    const bool q8 = quant && quantized && a.tq > 1 && a.wsplit > 1 && head_dim % 32 == 0;
+    if (q8) { a.qcodes = quant->codes; a.qscl = quant->scl; a.q_npad = quant->npad; a.q_i8 = quant->i8 ? 1 : 0; }
+    const int st2 = launch_status(attn_launch(a, kv_int8 != 0, (hipStream_t)stream), "attention prefill");
+    if (st2 == JLLM_OK && q8) *quantized = true;
+    return st2;
 }
+}  // namespace jllm_hip
+
+extern "C" {
 
 int jllm_hip_fp16_to_int8(int8_t* dst, float* scale_out, const uint16_t* src, int rows, int cols, void* stream) {
     if (rows < 0 || cols <= 0 || (rows > 0 && (!dst || !src))) return JLLM_ERR_INVALID;

@@ -82,6 +82,19 @@ int gemm_batched_shared_x(const char* tag, const GemmOut* outs, int n, const uin
 // every output as gemm_batched_shared_x followed by
 // jllm_hip_qk_norm_rope_store_kv would leave it; else *done = false and
 // nothing ran.
+// The prefill attention (jllm_hip_flash_attention_prefill_batched) whose
+// epilogue also quantises the output rows for the next GEMM when quant is
+// given and the kernel form allows it (*quantized = true: codes[npad
+// rows] as the MMQ activation quantiser writes them, int8 codes + DS4
+// words when i8, else fp16 codes + D4 words).
+struct AttnQuant { void* codes; uint32_t* scl; int npad; bool i8; };
+int prefill_attention(uint16_t* out, const uint16_t* q, const void* k, const void* v, int n_heads, int n_kv_heads,
+                      int head_dim, int cache_head_dim, int N, int start_pos, float scale, int kv_int8,
+                      const float* k_scales, const float* v_scales, int window, const AttnQuant* quant, void* stream,
+                      bool* quantized);
+// the quantiser scratch of an N x K activation for weight type `type` (12
+// or 14; the pointers gemm_batched_res / gemm_batched_shared_x read)
+int q8_codes(const char* tag, int type, int N, int K, AttnQuant* q);
 struct QKPostArgs;
 int qkv_front_prefill(const char* tag, const GemmOut* qkv, const uint16_t* x, int N, int K, bool quantized,
                       const QKPostArgs& fa, void* stream, bool* done);
@@ -96,7 +109,7 @@ struct ResidualRows { uint16_t* y; const uint16_t* res; const float* ws; int S; 
 // memory): the engine's projection + residual add (decode.cu:1830-1884).
 int gemm_batched_res(const char* tag, uint16_t* y, const void* W, int type, const uint16_t* x, const uint16_t* up,
                      uint16_t* act_tmp, const uint16_t* res, int M, int N, int K, void* stream,
-                     ResidualRows* defer = nullptr);
+                     ResidualRows* defer = nullptr, bool quantized = false);
 // completes deferred rows (y [N x M] as gemm_batched_res without defer writes it)
 int residual_finish(const char* tag, const ResidualRows& r, int N, int M, void* stream);
 // The deferred rows completed, then normed [N x H] = RMSNorm(y) with weights

@@ -122,7 +122,7 @@ int run_mmq(const char* tag, void* y, const void* W, int type, const uint16_t* x
 namespace jllm_hip {
 int gemm_batched_res(const char* tag, uint16_t* y, const void* W, int type, const uint16_t* x, const uint16_t* up,
                      uint16_t* act_tmp, const uint16_t* res, int M, int N, int K, void* stream,
-                     ResidualRows* defer) {
+                     ResidualRows* defer, bool quantized) {
     if (defer) *defer = ResidualRows{y, res, nullptr, 0, 0};
     int st = check_gemm(tag, y, type, x, M, N, K, true); if (st) return st;
     if (M == 0 || N == 0) return JLLM_OK;
@@ -148,10 +148,22 @@ int gemm_batched_res(const char* tag, uint16_t* y, const void* W, int type, cons
     const int k = type == 12 ? 0 : 1;
     if (type != 13) {
         st = q8_scratch(tag, N, K, codes, scl); if (st) return st;
-        const hipError_t e = quantize_for(type, x, codes, scl, N, K, hs, up);
-        if (e != hipSuccess) return launch_status(e, tag);
+        if (!quantized || up) {
+            const hipError_t e = quantize_for(type, x, codes, scl, N, K, hs, up);
+            if (e != hipSuccess) return launch_status(e, tag);
+        }
     }
     return mmq_after_quant(tag, y, Wd, type, x, codes[k], scl[k], M, N, K, 0, hs, res, defer);
+}
+
+int q8_codes(const char* tag, int type, int N, int K, AttnQuant* q) {
+    if ((type != 12 && type != 14) || N <= 1 || K <= 0 || K % 256) return JLLM_ERR_INVALID;
+    void* codes[2] = {nullptr, nullptr};
+    uint32_t* scl[2] = {nullptr, nullptr};
+    int st = q8_scratch(tag, N, K, codes, scl); if (st) return st;
+    const int k = type == 12 ? 0 : 1;
+    *q = AttnQuant{codes[k], scl[k], npad_of(N), k == 0};
+    return JLLM_OK;
 }
 
 int residual_finish(const char* tag, const ResidualRows& r, int N, int M, void* stream) {

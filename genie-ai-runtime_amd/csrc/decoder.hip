@@ -35,6 +35,7 @@ using jllm_hip::residual_finish;
 using jllm_hip::ResidualRows;
 using jllm_hip::qkv_front_prefill;
 using jllm_hip::QKPostArgs;
+using jllm_hip::AttnQuant;
 
 struct jllm_hip_decoder {
     jllm_hip_decoder_config cfg;
@@ -147,12 +148,18 @@ int prefill_layer(jllm_hip_decoder* d, int l, int start, int N, void* st, bool* 
                                            c.n_kv_heads, c.head_dim, c.head_dim, start, N, c.rope_theta,
                                            c.rope_neox, c.kv_int8, st));
     }
-    TRY(jllm_hip_flash_attention_prefill_batched(d->attn, d->q, layer_k(d, l), layer_v(d, l), c.n_heads,
-                                                 c.n_kv_heads, c.head_dim, c.head_dim, N, start, attn_scale(c),
-                                                 c.kv_int8, c.kv_int8 ? layer_ks(d, l) : nullptr,
-                                                 c.kv_int8 ? layer_vs(d, l) : nullptr, 0, st));
+    // the attention output quantised for the O GEMM in the attention's
+    // epilogue where the kernel form allows
+    AttnQuant aq;
+    const bool want_q = N > 1 && (w.type_wo == 12 || w.type_wo == 14);
+    if (want_q) TRY(jllm_hip::q8_codes("decoder", w.type_wo, N, QD, &aq));
+    bool oq = false;
+    TRY(jllm_hip::prefill_attention(d->attn, d->q, layer_k(d, l), layer_v(d, l), c.n_heads, c.n_kv_heads, c.head_dim,
+                                    c.head_dim, N, start, attn_scale(c), c.kv_int8,
+                                    c.kv_int8 ? layer_ks(d, l) : nullptr, c.kv_int8 ? layer_vs(d, l) : nullptr, 0,
+                                    want_q ? &aq : nullptr, st, &oq));
     ResidualRows r;
-    TRY(gemm_batched_res("decoder", d->x2, w.wo, w.type_wo, d->attn, nullptr, nullptr, d->x, H, N, QD, st, &r));
+    TRY(gemm_batched_res("decoder", d->x2, w.wo, w.type_wo, d->attn, nullptr, nullptr, d->x, H, N, QD, st, &r, oq));
     const GemmOut gu[2] = {{d->gate, w.w_gate, w.type_w_gate, I}, {d->up, w.w_up, w.type_w_up, I}};
     bool q2 = false;
     TRY(norm_rows("decoder", r, N, H, d->normed, w.rms_ffn, c.norm_fp32 != 0, c.rms_eps, gu, 2, &q2, st));
