@@ -95,6 +95,14 @@ int prefill_attention(uint16_t* out, const uint16_t* q, const void* k, const voi
 // the quantiser scratch of an N x K activation for weight type `type` (12
 // or 14; the pointers gemm_batched_res / gemm_batched_shared_x read)
 int q8_codes(const char* tag, int type, int N, int K, AttnQuant* q);
+// The decoder's prefill gate/up of one activation x (quantised already when
+// `quantized`) with the SwiGLU and its quantisation for the down GEMM of
+// type down_type in the GEMM's epilogue, when the shapes allow it (both
+// Q4_K, equal M, M % 64 == 0, no split-K): *done = true and *act holds the
+// down GEMM's activation codes (pass it as gemm_batched_res's pre); else
+// *done = false and nothing ran.
+int gate_up_swiglu_prefill(const char* tag, const GemmOut* gu, const uint16_t* x, int N, int K, bool quantized,
+                           int down_type, AttnQuant* act, bool* done, void* stream);
 struct QKPostArgs;
 int qkv_front_prefill(const char* tag, const GemmOut* qkv, const uint16_t* x, int N, int K, bool quantized,
                       const QKPostArgs& fa, void* stream, bool* done);
@@ -109,7 +117,7 @@ struct ResidualRows { uint16_t* y; const uint16_t* res; const float* ws; int S; 
 // memory): the engine's projection + residual add (decode.cu:1830-1884).
 int gemm_batched_res(const char* tag, uint16_t* y, const void* W, int type, const uint16_t* x, const uint16_t* up,
                      uint16_t* act_tmp, const uint16_t* res, int M, int N, int K, void* stream,
-                     ResidualRows* defer = nullptr, bool quantized = false);
+                     ResidualRows* defer = nullptr, const AttnQuant* pre = nullptr);
 // completes deferred rows (y [N x M] as gemm_batched_res without defer writes it)
 int residual_finish(const char* tag, const ResidualRows& r, int N, int M, void* stream);
 // The deferred rows completed, then normed [N x H] = RMSNorm(y) with weights

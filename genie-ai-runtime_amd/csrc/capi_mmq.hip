@@ -11,6 +11,7 @@ using namespace jllm_hip;
 namespace {
 DeviceScratch g_q8;     // quantised activations (int8 and fp16 codes + scale words), grown on demand, never freed
 DeviceScratch g_ws;     // split-K fp32 partials [splits][N][M], grown on demand, never freed
+DeviceScratch g_q8b;    // a GEMM epilogue's output codes for the next GEMM (read while g_q8 is), never freed
 
 int npad_of(int N) { return ((N + MMQ_TILE_N - 1) / MMQ_TILE_N) * MMQ_TILE_N; }
 
@@ -122,7 +123,7 @@ int run_mmq(const char* tag, void* y, const void* W, int type, const uint16_t* x
 namespace jllm_hip {
 int gemm_batched_res(const char* tag, uint16_t* y, const void* W, int type, const uint16_t* x, const uint16_t* up,
                      uint16_t* act_tmp, const uint16_t* res, int M, int N, int K, void* stream,
-                     ResidualRows* defer, bool quantized) {
+                     ResidualRows* defer, const AttnQuant* pre) {
     if (defer) *defer = ResidualRows{y, res, nullptr, 0, 0};
     int st = check_gemm(tag, y, type, x, M, N, K, true); if (st) return st;
     if (M == 0 || N == 0) return JLLM_OK;
@@ -146,14 +147,56 @@ int gemm_batched_res(const char* tag, uint16_t* y, const void* W, int type, cons
     void* codes[2] = {nullptr, nullptr};
     uint32_t* scl[2] = {nullptr, nullptr};
     const int k = type == 12 ? 0 : 1;
-    if (type != 13) {
+    if (type != 13 && pre) {
+        if (pre->i8 != (type == 12) || pre->npad != npad_of(N)) return JLLM_ERR_INVALID;
+        codes[k] = pre->codes;
+        scl[k] = pre->scl;
+    } else if (type != 13) {
         st = q8_scratch(tag, N, K, codes, scl); if (st) return st;
-        if (!quantized || up) {
-            const hipError_t e = quantize_for(type, x, codes, scl, N, K, hs, up);
-            if (e != hipSuccess) return launch_status(e, tag);
-        }
+        const hipError_t e = quantize_for(type, x, codes, scl, N, K, hs, up);
+        if (e != hipSuccess) return launch_status(e, tag);
     }
     return mmq_after_quant(tag, y, Wd, type, x, codes[k], scl[k], M, N, K, 0, hs, res, defer);
+}
+
+int gate_up_swiglu_prefill(const char* tag, const GemmOut* gu, const uint16_t* x, int N, int K, bool quantized,
+                           int down_type, AttnQuant* act, bool* done, void* stream) {
+    *done = false;
+    const int M = gu[0].M;
+    if (N <= 1 || gu[0].type != 12 || gu[1].type != 12 || gu[1].M != M || M <= 0 || M % 256 ||
+        (down_type != 12 && down_type != 14))
+        return JLLM_OK;
+    const int Npad = npad_of(N);
+    if ((int64_t)(M / 64) * (Npad / MMQ_TILE_N) < MMQ_MULTI_MIN_TILES) return JLLM_OK;
+    const uint8_t* Wd[2];
+    for (int i = 0; i < 2; i++) {
+        int st = check_gemm(tag, gu[i].y, gu[i].type, x, M, N, K, true); if (st) return st;
+        const void* w = device_weight(tag, gu[i].W);
+        if (!w) return JLLM_ERR_POINTER;
+        if (!aligned16(w)) return JLLM_ERR_INVALID;
+        Wd[i] = (const uint8_t*)w;
+    }
+    hipStream_t hs = (hipStream_t)stream;
+    void* codes[2] = {nullptr, nullptr};
+    uint32_t* scl[2] = {nullptr, nullptr};
+    int st = q8_scratch(tag, N, K, codes, scl); if (st) return st;
+    if (!quantized) {
+        const hipError_t e = quantize_for(12, x, codes, scl, N, K, hs);
+        if (e != hipSuccess) return launch_status(e, tag);
+    }
+    // the down GEMM's codes (K = M) in their own scratch: g_q8 is being read
+    const bool i8 = down_type == 12;
+    const size_t cb = i8 ? mmq_codes8_bytes(M, Npad) : mmq_codes_bytes(M, Npad);
+    uint8_t* o = (uint8_t*)g_q8b.get(cb + mmq_scales_bytes(M, Npad));
+    if (!o) {
+        fprintf(stderr, "[%s] activation scratch allocation failed\n", tag);
+        return JLLM_ERR_NOMEM;
+    }
+    *act = AttnQuant{o, (uint32_t*)(o + cb), Npad, i8};
+    st = launch_status(mmq_q4k_swiglu_launch(Wd[0], Wd[1], M, (const uint8_t*)codes[0], scl[0], N, K, Npad, o,
+                                             (uint32_t*)(o + cb), i8, hs), tag);
+    if (st == JLLM_OK) *done = true;
+    return st;
 }
 
 int q8_codes(const char* tag, int type, int N, int K, AttnQuant* q) {

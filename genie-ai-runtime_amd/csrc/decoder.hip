@@ -159,12 +159,19 @@ int prefill_layer(jllm_hip_decoder* d, int l, int start, int N, void* st, bool* 
                                     c.kv_int8 ? layer_ks(d, l) : nullptr, c.kv_int8 ? layer_vs(d, l) : nullptr, 0,
                                     want_q ? &aq : nullptr, st, &oq));
     ResidualRows r;
-    TRY(gemm_batched_res("decoder", d->x2, w.wo, w.type_wo, d->attn, nullptr, nullptr, d->x, H, N, QD, st, &r, oq));
+    TRY(gemm_batched_res("decoder", d->x2, w.wo, w.type_wo, d->attn, nullptr, nullptr, d->x, H, N, QD, st, &r,
+                         oq ? &aq : nullptr));
     const GemmOut gu[2] = {{d->gate, w.w_gate, w.type_w_gate, I}, {d->up, w.w_up, w.type_w_up, I}};
     bool q2 = false;
     TRY(norm_rows("decoder", r, N, H, d->normed, w.rms_ffn, c.norm_fp32 != 0, c.rms_eps, gu, 2, &q2, st));
-    TRY(gemm_batched_shared_x("decoder", gu, 2, d->normed, N, H, st, q2));
-    TRY(gemm_batched_res("decoder", d->x, w.w_down, w.type_w_down, d->gate, d->up, d->act, d->x2, H, N, I, st, &r));
+    // gate/up with the SwiGLU quantised for the down GEMM in the epilogue
+    // where the shapes allow
+    AttnQuant act;
+    bool swq = false;
+    TRY(jllm_hip::gate_up_swiglu_prefill("decoder", gu, d->normed, N, H, q2, w.type_w_down, &act, &swq, st));
+    if (!swq) TRY(gemm_batched_shared_x("decoder", gu, 2, d->normed, N, H, st, q2));
+    TRY(gemm_batched_res("decoder", d->x, w.w_down, w.type_w_down, d->gate, d->up, d->act, d->x2, H, N, I, st, &r,
+                         swq ? &act : nullptr));
     *normed_q = false;
     if (!next) return residual_finish("decoder", r, N, H, st);
     const jllm_hip_layer_weights& wn = d->lw[l + 1];

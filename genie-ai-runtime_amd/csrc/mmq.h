@@ -90,6 +90,16 @@ hipError_t mmq_q4k_qkv_front_launch(const uint8_t* const* W, uint16_t* const* y,
                                     const uint32_t* scl, int N, int K, int Npad, const QKPostArgs& fa,
                                     hipStream_t st);
 
+// The decoder's prefill gate/up (both Q4_K, M rows each, M % 64 == 0, no
+// split) with the SwiGLU half(silu(gate) * up) of the fp16 products
+// quantised in the epilogue as the down GEMM's activation: act codes and
+// scale words for K = M (int8 + DS4 when act_i8, else fp16 + D4), Npad
+// token rows -- the bits quantize_mmq_f16_launch(gate, .., up) writes from
+// the plain launch's gate and up.
+hipError_t mmq_q4k_swiglu_launch(const uint8_t* gate, const uint8_t* up, int M, const uint8_t* codes,
+                                 const uint32_t* scl, int N, int K, int Npad, void* act_codes, uint32_t* act_scl,
+                                 bool act_i8, hipStream_t st);
+
 // Split count for an N x M x K GEMM of weight type `type`: ranges of whole
 // super-blocks chosen by a measured cost model (at most 16 ranges for Q4_K /
 // Q5_K, 19 for Q6_K); a function of M, N, K and the type only.

@@ -365,12 +365,23 @@ typedef __attribute__((address_space(3))) void lds_void;
 // distinct 16-byte bank groups
 __host__ __device__ __forceinline__ int swz_b(int tok) { return (tok ^ (tok >> 3)) & 7; }
 
+// Codes of the next GEMM's activation written by a GEMM epilogue: int8
+// codes + DS4 words (i8) or fp16 codes + D4 words, Npad token rows
+struct MmqActOut {
+    void* codes;
+    uint32_t* scl;
+    int i8;
+};
+
 // OUT: 0: fp16 y [N][M], 1: fp32 y [N][M], 2: int32 dots [N][M][K/32], 3:
-// fp16 y of the Q/K/V multi-launch followed by the attention front (fa)
+// fp16 y of the Q/K/V multi-launch followed by the attention front (fa), 4:
+// gate (W[0]) and up (W[1]) of equal M, tile rt = rows [64 rt, 64 rt + 64)
+// of both (waves 0-1 gate, 2-3 up), the SwiGLU half(silu(gate) * up) of
+// the fp16 products quantised into ao (the down GEMM's activation)
 template <int OUT>
 __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* __restrict__ codes,
                                              const uint32_t* __restrict__ scl, int N, int K, int Npad, int sps,
-                                             const QKPostArgs* fa) {
+                                             const QKPostArgs* fa, const MmqActOut* ao = nullptr) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[NRING * ST_BYTES];
 
     const int nb = K / QK_K, nst = 2 * nb;
@@ -379,11 +390,13 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
     const int n_rt = sg.rt0[3], n_tt = Npad / TN;
     const int tile = xcd_tile(blockIdx.x, n_rt * n_tt);
     const int rt = tile / n_tt;
-    const int sgi = rt >= sg.rt0[1] ? (rt >= sg.rt0[2] ? 2 : 1) : 0;
+    const int wq = OUT == 4 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
+    const int sgi = OUT == 4 ? (wq >> 1) : (rt >= sg.rt0[1] ? (rt >= sg.rt0[2] ? 2 : 1) : 0);
     void* __restrict__ y = sg.y[sgi];
     const uint8_t* __restrict__ W = sg.W[sgi];
     const int M = sg.M[sgi];
-    const int row0 = (rt - sg.rt0[sgi]) * TM, col0 = (tile % n_tt) * TN;
+    // OUT 4: wave w's rows are 64 rt + 32 (w & 1) + lane (of gate or up)
+    const int row0 = OUT == 4 ? 64 * rt - 64 * (wq >> 1) : (rt - sg.rt0[sgi]) * TM, col0 = (tile % n_tt) * TN;
     const int t = threadIdx.x, w = t >> 6, l = t & 63, li = l & 31, g = l >> 5;
     const int arow = 32 * w + li;                      // this lane's A-operand row
 
@@ -560,6 +573,38 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
         __builtin_amdgcn_s_barrier();
     }
     if (OUT == 2) return;
+    if (OUT == 4) {
+        // fp16 products to LDS [token][64 gate rows | 64 up rows] (rows
+        // padded to 130 halves), then per (token, 8 consecutive rows) the
+        // SwiGLU as the quantiser's SW form rounds it and quant_chunk (the 4
+        // lanes of an aligned quad: one 32-row block)
+        constexpr int FT_LD = 130;
+        static_assert(64 * FT_LD * 2 <= NRING * ST_BYTES, "SwiGLU tile exceeds the LDS ring");
+        uint16_t* T = (uint16_t*)smem;
+        __builtin_amdgcn_s_waitcnt(0);                 // the ring's last DMA has landed
+        __syncthreads();
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+            for (int v = 0; v < 16; v++)
+                T[(32 * tt + li) * FT_LD + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3)] = f32_to_f16_bits(acc[tt][v]);
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int e = t + MMQ_THREADS * j, tl = e >> 3, c8 = e & 7, tok = col0 + tl;
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float gv = f16_bits_to_f32(T[tl * FT_LD + 8 * c8 + i]);
+                const float uv = f16_bits_to_f32(T[tl * FT_LD + 64 + 8 * c8 + i]);
+                v[i] = tok < N ? f16_bits_to_f32(f32_to_f16_bits(silu_mul(gv, uv))) : 0.0f;
+            }
+            const int kb32 = (64 * rt + 8 * c8) >> 5, sub = c8 & 3;
+            if (ao->i8) quant_chunk<true>(v, sub, kb32, tok, Npad, ao->codes, ao->scl, true);
+            else        quant_chunk<false>(v, sub, kb32, tok, Npad, ao->codes, ao->scl, false);
+        }
+        return;
+    }
     if (OUT == 3) {
         // The tile is one head (128 rows) of q, k or v (segment 0 / 1 / 2)
         // for 64 tokens.  Its fp16 values (y as the plain launch stores it)
@@ -625,6 +670,12 @@ __global__ __launch_bounds__(MMQ_THREADS, 3)
 void mmq_q4k_front_kernel(MmqSegs sg, const uint8_t* __restrict__ codes, const uint32_t* __restrict__ scl, int N,
                           int K, int Npad, QKPostArgs fa) {
     mmq_q4k_body<3>(sg, codes, scl, N, K, Npad, K / QK_K, &fa);
+}
+
+__global__ __launch_bounds__(MMQ_THREADS, 3)
+void mmq_q4k_swiglu_kernel(MmqSegs sg, const uint8_t* __restrict__ codes, const uint32_t* __restrict__ scl, int N,
+                           int K, int Npad, MmqActOut ao) {
+    mmq_q4k_body<4>(sg, codes, scl, N, K, Npad, K / QK_K, nullptr, &ao);
 }
 
 // ---------------------------------------------------------------------------
@@ -966,6 +1017,21 @@ hipError_t mmq_q4k_qkv_front_launch(const uint8_t* const* W, uint16_t* const* y,
     }
     const dim3 grid(sg.rt0[3] * (Npad / TN), 1);
     hipLaunchKernelGGL(mmq_q4k_front_kernel, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, fa);
+    return hipGetLastError();
+}
+
+hipError_t mmq_q4k_swiglu_launch(const uint8_t* gate, const uint8_t* up, int M, const uint8_t* codes,
+                                 const uint32_t* scl, int N, int K, int Npad, void* act_codes, uint32_t* act_scl,
+                                 bool act_i8, hipStream_t st) {
+    if (M <= 0 || M % 64 || Npad % TN || Npad < N) return hipErrorInvalidValue;
+    MmqSegs sg;
+    sg.W[0] = gate; sg.W[1] = up; sg.W[2] = up;
+    sg.y[0] = sg.y[1] = sg.y[2] = nullptr;
+    sg.M[0] = M; sg.M[1] = M; sg.M[2] = 0;
+    sg.rt0[0] = 0; sg.rt0[1] = M / 64; sg.rt0[2] = M / 64; sg.rt0[3] = M / 64;
+    MmqActOut ao{act_codes, act_scl, act_i8 ? 1 : 0};
+    const dim3 grid(sg.rt0[3] * (Npad / TN), 1);
+    hipLaunchKernelGGL(mmq_q4k_swiglu_kernel, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, ao);
     return hipGetLastError();
 }
 
