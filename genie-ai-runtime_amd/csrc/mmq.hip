@@ -40,6 +40,7 @@
 #include "qk_front.h"
 #include "quant_chunk.h"
 #include <algorithm>
+#include <stdlib.h>
 
 namespace jllm_hip {
 
@@ -378,16 +379,19 @@ struct MmqActOut {
 // gate (W[0]) and up (W[1]) of equal M, tile rt = rows [64 rt, 64 rt + 64)
 // of both (waves 0-1 gate, 2-3 up), the SwiGLU half(silu(gate) * up) of
 // the fp16 products quantised into ao (the down GEMM's activation)
-template <int OUT>
+template <int OUT, int TT>
 __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* __restrict__ codes,
                                              const uint32_t* __restrict__ scl, int N, int K, int Npad, int sps,
                                              const QKPostArgs* fa, const MmqActOut* ao = nullptr) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[NRING * ST_BYTES];
+    // TT 32-token halves per tile (2: the 128 x 64 tile; 1: 128 x 32, twice
+    // the workgroups for grids that would leave SIMDs idle)
+    constexpr int TNv = 32 * TT, STB = TNv * 128, STBYTES = STB + 4 * TNv * 4;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[NRING * STBYTES];
 
     const int nb = K / QK_K, nst = 2 * nb;
     // split-K: this workgroup's stages [k0, k1) (whole super-blocks)
     const int k0 = 2 * (int)blockIdx.y * sps, k1 = min(nst, k0 + 2 * sps);
-    const int n_rt = sg.rt0[3], n_tt = Npad / TN;
+    const int n_rt = sg.rt0[3], n_tt = Npad / TNv;
     const int tile = xcd_tile(blockIdx.x, n_rt * n_tt);
     const int rt = tile / n_tt;
     const int wq = OUT == 4 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
@@ -396,7 +400,7 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
     const uint8_t* __restrict__ W = sg.W[sgi];
     const int M = sg.M[sgi];
     // OUT 4: wave w's rows are 64 rt + 32 (w & 1) + lane (of gate or up)
-    const int row0 = OUT == 4 ? 64 * rt - 64 * (wq >> 1) : (rt - sg.rt0[sgi]) * TM, col0 = (tile % n_tt) * TN;
+    const int row0 = OUT == 4 ? 64 * rt - 64 * (wq >> 1) : (rt - sg.rt0[sgi]) * TM, col0 = (tile % n_tt) * TNv;
     const int t = threadIdx.x, w = t >> 6, l = t & 63, li = l & 31, g = l >> 5;
     const int arow = 32 * w + li;                      // this lane's A-operand row
 
@@ -410,25 +414,28 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
     // of each 32-byte pair, and the 16-byte block header
     const int voRow = min(row0 + arow, M - 1) * nb * Q4K_BYTES;
     // DMA slots: slot q (16 B) of the codes region is written by lane q % 64 of
-    // wave q / 64 (two instructions per wave); the scale words go as 4-byte
-    // slots, 64 per wave
-    int voB[2];
+    // wave q / 64 (TT instructions per wave); the scale words go as 4-byte
+    // slots, 64 per wave (TT = 1: waves 2, 3 repeat the words of waves 0, 1
+    // -- the same values to the same LDS words -- so that every wave issues
+    // the same loads)
+    int voB[TT];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int q = (2 * w + i) * 64 + l;
+    for (int i = 0; i < TT; i++) {
+        const int q = (TT * w + i) * 64 + l;
         const int tok = q >> 3, pos = q & 7;
         voB[i] = (col0 + tok) * 256 + 16 * (pos ^ swz_b(tok));
     }
-    const int voS = ((w * 64 + l) / TN * Npad + col0 + (w * 64 + l) % TN) * 4;   // word (jl, tok) of the stage
+    const int qw = (w * 64 + l) % (4 * TNv);
+    const int voS = (qw / TNv * Npad + col0 + qw % TNv) * 4;   // word (jl, tok) of the stage
 
-    auto issue_b = [&](int k) {                        // 3 DMA instructions per wave
-        uint8_t* st = smem + (k % NRING) * ST_BYTES;
+    auto issue_b = [&](int k) {                        // TT + 1 DMA instructions per wave
+        uint8_t* st = smem + (k % NRING) * STBYTES;
         const int b = k >> 1, s = k & 1;
 #pragma unroll
-        for (int i = 0; i < 2; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rC, (lds_void*)(st + (2 * w + i) * 1024), 16, voB[i],
+        for (int i = 0; i < TT; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rC, (lds_void*)(st + (TT * w + i) * 1024), 16, voB[i],
                                                      b * Npad * 256 + 128 * s, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rS, (lds_void*)(st + ST_B + w * 256), 4, voS,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rS, (lds_void*)(st + STB + (TT == 2 ? w : (w & 1)) * 256), 4, voS,
                                                  (b * 8 + 4 * s) * Npad * 4, 0, 0);
     };
     // this lane's weight code bytes of stage k: pair 0 and pair 1 (16 B each)
@@ -439,12 +446,12 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
             a[pp] = __builtin_amdgcn_raw_buffer_load_b128(rW, voRow + 16 + 16 * g, b * Q4K_BYTES + 64 * s + 32 * pp, 0);
     };
 
-    f32x16m acc[2];
-    acc[0] = f32x16m{};
-    acc[1] = f32x16m{};
-    int b_c[2];
+    f32x16m acc[TT];
 #pragma unroll
-    for (int tt = 0; tt < 2; tt++) b_c[tt] = g ^ swz_b(32 * tt + li);   // B-read position = 2 * jl ^ b_c
+    for (int tt = 0; tt < TT; tt++) acc[tt] = f32x16m{};
+    int b_c[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) b_c[tt] = g ^ swz_b(32 * tt + li);   // B-read position = 2 * jl ^ b_c
 
     // Scale operands of the current super-block: lane (row, g) holds
     // half(d*sc_j) and half(-dmin*m_j) of its row for the sub-blocks j = 4g ..
@@ -472,15 +479,15 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
     };
 
     auto compute = [&](int k, const u32x4m (&a)[2]) {
-        const uint8_t* st = smem + (k % NRING) * ST_BYTES;
+        const uint8_t* st = smem + (k % NRING) * STBYTES;
         const int b = k >> 1, s = k & 1;
-        const uint32_t* sS = (const uint32_t*)(st + ST_B);
+        const uint32_t* sS = (const uint32_t*)(st + STB);
         const bool mine = g == s;                      // this lane group's K slots belong to the stage
-        uint32_t sw[2][4];
-        i32x4 Bv[2];
+        uint32_t sw[TT][4];
+        i32x4 Bv[TT];
         auto read_b = [&](int jl) {
 #pragma unroll
-            for (int tt = 0; tt < 2; tt++)
+            for (int tt = 0; tt < TT; tt++)
                 Bv[tt] = *(const i32x4*)(st + (32 * tt + li) * 128 + 16 * ((2 * jl) ^ b_c[tt]));
         };
         read_b(0);
@@ -489,12 +496,12 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
             const int j = 4 * s + jl;
             const u32x4m araw = a[jl >> 1];            // low nibbles: sub-block 2p, high: 2p+1
             const i32x4 Ai = __builtin_bit_cast(i32x4, (jl & 1) ? ((araw >> 4u) & 0x0F0F0F0Fu) : (araw & 0x0F0F0F0Fu));
-            i32x16 C[2];
-            f32x16m S[2];
+            i32x16 C[TT];
+            f32x16m S[TT];
 #pragma unroll
-            for (int tt = 0; tt < 2; tt++) {
+            for (int tt = 0; tt < TT; tt++) {
                 if (OUT != 2) {
-                    sw[tt][jl] = sS[jl * TN + 32 * tt + li];               // half d8 | half sum x << 16
+                    sw[tt][jl] = sS[jl * TNv + 32 * tt + li];               // half d8 | half sum x << 16
                     // d8 in K slot jl of this lane group's four (the stage's), zeros elsewhere
                     const uint32_t dv = (jl & 1) ? (sw[tt][jl] << 16) : (sw[tt][jl] & 0xFFFFu);
                     u32x2m bs = u32x2m{0u, 0u};
@@ -507,7 +514,7 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
             if (jl < 3) read_b(jl + 1);
             if (OUT == 2) {
 #pragma unroll
-                for (int tt = 0; tt < 2; tt++)
+                for (int tt = 0; tt < TT; tt++)
 #pragma unroll
                     for (int v = 0; v < 16; v++) {
                         const int r = row0 + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3);
@@ -516,7 +523,7 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
                     }
             } else {
 #pragma unroll
-                for (int tt = 0; tt < 2; tt++)
+                for (int tt = 0; tt < TT; tt++)
 #pragma unroll
                     for (int v = 0; v < 16; v++) acc[tt][v] = __builtin_fmaf(S[tt][v], (float)C[tt][v], acc[tt][v]);
             }
@@ -525,7 +532,7 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
         if (OUT != 2) {
             // min term of the stage's four sub-blocks: sum_j half(-dmin*m_j) * sum x_j
 #pragma unroll
-            for (int tt = 0; tt < 2; tt++) {
+            for (int tt = 0; tt < TT; tt++) {
                 u32x2m bm;
                 bm.x = mine ? ((sw[tt][0] >> 16) | (sw[tt][1] & 0xFFFF0000u)) : 0u;
                 bm.y = mine ? ((sw[tt][2] >> 16) | (sw[tt][3] & 0xFFFF0000u)) : 0u;
@@ -537,8 +544,8 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
     // Stage pipeline (k0 is even, k1 - k0 is even): per iteration, the next
     // stage's weight bytes (+ header) into registers, then stage k+2's
     // activation DMA, then stage k from registers and LDS.  The loads of a
-    // wave complete in issue order, so waiting until only the newest 3 (the
-    // DMA of stage k+2) are outstanding means stage k+1's weights and DMA have
+    // wave complete in issue order, so waiting until only the newest TT + 1
+    // (the DMA of stage k+2) are outstanding means stage k+1's weights and DMA have
     // landed; a plain s_barrier (no memory fence: a fence would wait for the
     // stage k+2 DMA too) then makes every wave's copy visible, and it also
     // orders every wave's reads of the buffer that the next DMA overwrites.
@@ -561,7 +568,7 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
         __builtin_amdgcn_sched_barrier(0);             // keep the DMA the newest loads
         issue_b(min(k + 2, kl));
         compute(k, a0);
-        __builtin_amdgcn_s_waitcnt(0x0F73);            // vmcnt(3): all but stage k+2's DMA
+        __builtin_amdgcn_s_waitcnt(TT == 2 ? 0x0F73 : 0x0F72);   // vmcnt(TT + 1)            // vmcnt(3): all but stage k+2's DMA
         __builtin_amdgcn_s_barrier();
         // odd stage k+1
         hdr = __builtin_amdgcn_raw_buffer_load_b128(rW, voRow, (min(k + 2, kl) >> 1) * Q4K_BYTES, 0);
@@ -569,7 +576,7 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
         __builtin_amdgcn_sched_barrier(0);
         issue_b(min(k + 3, kl));
         compute(k + 1, a1);
-        __builtin_amdgcn_s_waitcnt(0x0F73);
+        __builtin_amdgcn_s_waitcnt(TT == 2 ? 0x0F73 : 0x0F72);   // vmcnt(TT + 1)
         __builtin_amdgcn_s_barrier();
     }
     if (OUT == 2) return;
@@ -579,18 +586,18 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
         // SwiGLU as the quantiser's SW form rounds it and quant_chunk (the 4
         // lanes of an aligned quad: one 32-row block)
         constexpr int FT_LD = 130;
-        static_assert(64 * FT_LD * 2 <= NRING * ST_BYTES, "SwiGLU tile exceeds the LDS ring");
+        static_assert(TNv * FT_LD * 2 <= NRING * STBYTES, "SwiGLU tile exceeds the LDS ring");
         uint16_t* T = (uint16_t*)smem;
         __builtin_amdgcn_s_waitcnt(0);                 // the ring's last DMA has landed
         __syncthreads();
 #pragma unroll
-        for (int tt = 0; tt < 2; tt++)
+        for (int tt = 0; tt < TT; tt++)
 #pragma unroll
             for (int v = 0; v < 16; v++)
                 T[(32 * tt + li) * FT_LD + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3)] = f32_to_f16_bits(acc[tt][v]);
         __syncthreads();
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < TT; j++) {
             const int e = t + MMQ_THREADS * j, tl = e >> 3, c8 = e & 7, tok = col0 + tl;
             float v[8];
 #pragma unroll
@@ -613,12 +620,12 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
         // for 16 tokens: lane l holds the rotary pair (i0, i1); v is also
         // stored as y.
         constexpr int FT_LD = 130;
-        static_assert(64 * FT_LD * 2 <= NRING * ST_BYTES, "front tile exceeds the LDS ring");
+        static_assert(TNv * FT_LD * 2 <= NRING * STBYTES, "front tile exceeds the LDS ring");
         uint16_t* T = (uint16_t*)smem;
         __builtin_amdgcn_s_waitcnt(0);                 // the ring's last DMA has landed
         __syncthreads();
 #pragma unroll
-        for (int tt = 0; tt < 2; tt++)
+        for (int tt = 0; tt < TT; tt++)
 #pragma unroll
             for (int v = 0; v < 16; v++)
                 T[(32 * tt + li) * FT_LD + 32 * w + 8 * (v >> 2) + 4 * g + (v & 3)] = f32_to_f16_bits(acc[tt][v]);
@@ -632,8 +639,8 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
         float w0 = 0.0f, w1 = 0.0f;
         front_weights(norm, a.norm_fp32 != 0, true, i0, i1, w0, w1);
         const float fq = a.fr.f[l];
-        for (int j = 0; j < 16; j++) {
-            const int tl = 16 * w + j, tok = col0 + tl;
+        for (int j = 0; j < TNv / 4; j++) {
+            const int tl = (TNv / 4) * w + j, tok = col0 + tl;
             if (tok >= N) break;                       // uniform across the wave
             const float v0 = f16_bits_to_f32(T[tl * FT_LD + i0]), v1 = f16_bits_to_f32(T[tl * FT_LD + i1]);
             if (kind == 2) {
@@ -646,7 +653,7 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
         return;
     }
 #pragma unroll
-    for (int tt = 0; tt < 2; tt++) {
+    for (int tt = 0; tt < TT; tt++) {
         const int tok = col0 + 32 * tt + li;
 #pragma unroll
         for (int v = 0; v < 16; v++) {
@@ -659,23 +666,42 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
     }
 }
 
-template <int OUT>
+template <int OUT, int TT>
 __global__ __launch_bounds__(MMQ_THREADS, 3)
 void mmq_q4k_kernel(MmqSegs sg, const uint8_t* __restrict__ codes, const uint32_t* __restrict__ scl, int N, int K,
                     int Npad, int sps) {
-    mmq_q4k_body<OUT>(sg, codes, scl, N, K, Npad, sps, nullptr);
+    mmq_q4k_body<OUT, TT>(sg, codes, scl, N, K, Npad, sps, nullptr);
 }
 
+template <int TT>
 __global__ __launch_bounds__(MMQ_THREADS, 3)
 void mmq_q4k_front_kernel(MmqSegs sg, const uint8_t* __restrict__ codes, const uint32_t* __restrict__ scl, int N,
                           int K, int Npad, QKPostArgs fa) {
-    mmq_q4k_body<3>(sg, codes, scl, N, K, Npad, K / QK_K, &fa);
+    mmq_q4k_body<3, TT>(sg, codes, scl, N, K, Npad, K / QK_K, &fa);
 }
 
+template <int TT>
 __global__ __launch_bounds__(MMQ_THREADS, 3)
 void mmq_q4k_swiglu_kernel(MmqSegs sg, const uint8_t* __restrict__ codes, const uint32_t* __restrict__ scl, int N,
                            int K, int Npad, MmqActOut ao) {
-    mmq_q4k_body<4>(sg, codes, scl, N, K, Npad, K / QK_K, nullptr, &ao);
+    mmq_q4k_body<4, TT>(sg, codes, scl, N, K, Npad, K / QK_K, nullptr, &ao);
+}
+
+// 32-token halves per Q4_K workgroup tile for a launch of `waves` waves
+// with 64-token tiles.  The 32-token tile keeps 97-101 VGPRs and 13.5 KB of
+// LDS, so a CU holds 5 of its workgroups instead of 3; it decodes each
+// weight operand for half the tokens.  Measured (us, 64-token / 32-token
+// tiles, quantiser and split-K reduce included): Q/K/V multi-launch 6144 x
+// 2560 at N = 512 (384 tiles) 54.8 / 48.0, with the attention front 51.6 /
+// 43.7; 9728 x 2560 at N = 512 (608) 72.5 / 69.5, at N = 64 30.7 / 29.9;
+// O 2560 x 4096 at N = 512 (160 tiles x 3 ranges) 47.9 / 46.7; gate/up +
+// SwiGLU at N = 512 (1216 tiles) 89.1 / 100.3 -- the smaller tile wins
+// below ~1024 workgroups.  The outputs are the same bits either way.
+int q4k_tt(int64_t waves) {
+#ifdef JLLM_MMQ_TT_DEBUG
+    if (const char* e = getenv("JLLM_MMQ_TT")) return atoi(e) == 1 ? 1 : 2;
+#endif
+    return waves < 4 * 1024 ? 1 : 2;
 }
 
 // ---------------------------------------------------------------------------
@@ -927,9 +953,16 @@ hipError_t mmq_launch(void* y, const uint8_t* W, int type, const void* codes, co
         sg.rt0[0] = 0;
         for (int i = 1; i < 4; i++) sg.rt0[i] = (M + TM - 1) / TM;
         const uint8_t* c8 = (const uint8_t*)codes;
-        if (out_kind == 0) hipLaunchKernelGGL(mmq_q4k_kernel<0>, grid, dim3(MMQ_THREADS), 0, st, sg, c8, scl, N, K, Npad, sps);
-        else if (out_kind == 1) hipLaunchKernelGGL(mmq_q4k_kernel<1>, grid, dim3(MMQ_THREADS), 0, st, sg, c8, scl, N, K, Npad, sps);
-        else hipLaunchKernelGGL(mmq_q4k_kernel<2>, grid, dim3(MMQ_THREADS), 0, st, sg, c8, scl, N, K, Npad, sps);
+        if (q4k_tt((int64_t)tiles * splits * 4) == 1) {
+            const dim3 g1(2 * tiles, splits);
+            if (out_kind == 0) hipLaunchKernelGGL((mmq_q4k_kernel<0, 1>), g1, dim3(MMQ_THREADS), 0, st, sg, c8, scl, N, K, Npad, sps);
+            else if (out_kind == 1) hipLaunchKernelGGL((mmq_q4k_kernel<1, 1>), g1, dim3(MMQ_THREADS), 0, st, sg, c8, scl, N, K, Npad, sps);
+            else hipLaunchKernelGGL((mmq_q4k_kernel<2, 1>), g1, dim3(MMQ_THREADS), 0, st, sg, c8, scl, N, K, Npad, sps);
+        } else {
+            if (out_kind == 0) hipLaunchKernelGGL((mmq_q4k_kernel<0, 2>), grid, dim3(MMQ_THREADS), 0, st, sg, c8, scl, N, K, Npad, sps);
+            else if (out_kind == 1) hipLaunchKernelGGL((mmq_q4k_kernel<1, 2>), grid, dim3(MMQ_THREADS), 0, st, sg, c8, scl, N, K, Npad, sps);
+            else hipLaunchKernelGGL((mmq_q4k_kernel<2, 2>), grid, dim3(MMQ_THREADS), 0, st, sg, c8, scl, N, K, Npad, sps);
+        }
     } else {
         const uint16_t* c16 = (const uint16_t*)codes;
         if (out_kind == 0) hipLaunchKernelGGL(mmq_q6k_kernel<0>, grid, dim3(MMQ_THREADS), 0, st, y, W, c16, scl, M, N, K, Npad, sps);
@@ -999,7 +1032,10 @@ hipError_t mmq_q4k_multi_launch(const uint8_t* const* W, void* const* y, const i
         sg.rt0[i + 1] = sg.rt0[i] + (sg.M[i] + TM - 1) / TM;
     }
     const dim3 grid(sg.rt0[3] * (Npad / TN), 1);
-    hipLaunchKernelGGL(mmq_q4k_kernel<0>, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, K / QK_K);
+    if (q4k_tt((int64_t)grid.x * 4) == 1)
+        hipLaunchKernelGGL((mmq_q4k_kernel<0, 1>), dim3(2 * grid.x), dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, K / QK_K);
+    else
+        hipLaunchKernelGGL((mmq_q4k_kernel<0, 2>), grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, K / QK_K);
     return hipGetLastError();
 }
 
@@ -1016,7 +1052,10 @@ hipError_t mmq_q4k_qkv_front_launch(const uint8_t* const* W, uint16_t* const* y,
         sg.rt0[i + 1] = sg.rt0[i] + M[i] / TM;
     }
     const dim3 grid(sg.rt0[3] * (Npad / TN), 1);
-    hipLaunchKernelGGL(mmq_q4k_front_kernel, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, fa);
+    if (q4k_tt((int64_t)grid.x * 4) == 1)
+        hipLaunchKernelGGL(mmq_q4k_front_kernel<1>, dim3(2 * grid.x), dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, fa);
+    else
+        hipLaunchKernelGGL(mmq_q4k_front_kernel<2>, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, fa);
     return hipGetLastError();
 }
 
@@ -1031,7 +1070,10 @@ hipError_t mmq_q4k_swiglu_launch(const uint8_t* gate, const uint8_t* up, int M, 
     sg.rt0[0] = 0; sg.rt0[1] = M / 64; sg.rt0[2] = M / 64; sg.rt0[3] = M / 64;
     MmqActOut ao{act_codes, act_scl, act_i8 ? 1 : 0};
     const dim3 grid(sg.rt0[3] * (Npad / TN), 1);
-    hipLaunchKernelGGL(mmq_q4k_swiglu_kernel, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, ao);
+    if (q4k_tt((int64_t)grid.x * 4) == 1)
+        hipLaunchKernelGGL(mmq_q4k_swiglu_kernel<1>, dim3(2 * grid.x), dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, ao);
+    else
+        hipLaunchKernelGGL(mmq_q4k_swiglu_kernel<2>, grid, dim3(MMQ_THREADS), 0, st, sg, codes, scl, N, K, Npad, ao);
     return hipGetLastError();
 }
 
