@@ -345,7 +345,8 @@ def bench_e2e(np, torch, dev, n_prompt=512, n_gen=128):
     """random-init Qwen3-4B-shaped decoder in Q4_K_M layout (36 layers,
     Q6_K lm_head and every other ffn_down, fp32 norms ~ 1+N(0,0.02), RoPE base 1e6,
     INT8 KV), the seeded 512-token prompt, then greedy decode to 128 tokens.  TTFT =
-    prefill of the prompt + first-token sampling; decode tok/s over the remaining
+    prefill of the prompt + first-token sampling (median of 5, each from an
+    idle queue); decode tok/s over the remaining
     127 steps.  Everything runs through the decoder's C ABI on one stream.  The
     model and prompt are the ones of the committed oracle generation; after
     the timed run an untimed teacher-forced pass must keep the logits within
@@ -364,6 +365,17 @@ def bench_e2e(np, torch, dev, n_prompt=512, n_gen=128):
     toks = torch.zeros(n_gen, dtype=torch.int32, device=dev)
     d.generate(prompt, 8, toks)                                   # warm-up (code objects, allocations)
     torch.cuda.synchronize()
+    # TTFT: median of 5 prefills of the prompt from an idle queue (each
+    # rewrites the same KV rows); the generation below starts from the last
+    pre = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        d.prefill(prompt, 0, toks[0:1])
+        e1.record()
+        torch.cuda.synchronize()
+        pre.append(e0.elapsed_time(e1))
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     ev[0].record()
     d.prefill(prompt, 0, toks[0:1])
@@ -372,7 +384,7 @@ def bench_e2e(np, torch, dev, n_prompt=512, n_gen=128):
         d.step(toks[i - 1:i], n_prompt + i - 1, toks[i:i + 1])
     ev[2].record()
     torch.cuda.synchronize()
-    ttft = ev[0].elapsed_time(ev[1])
+    ttft = float(np.median(pre))
     dec_ms = ev[1].elapsed_time(ev[2])
     gen = toks.cpu().numpy()
     # untimed check: a teacher-forced pass (the oracle's tokens fed) measures
