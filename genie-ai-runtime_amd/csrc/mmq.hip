@@ -1078,6 +1078,12 @@ hipError_t mmq_q4k_swiglu_launch(const uint8_t* gate, const uint8_t* up, int M, 
 }
 
 int mmq_splits(int M, int N, int K, int type) {
+#ifdef JLLM_MMQ_TT_DEBUG
+    if (const char* e = getenv(type == TYPE_Q6_K ? "JLLM_MMQ_S6" : "JLLM_MMQ_S4")) {
+        const int S = atoi(e), nb0 = K / QK_K, sps0 = (nb0 + S - 1) / S;
+        if (S > 0) return (nb0 + sps0 - 1) / sps0;
+    }
+#endif
     const bool q6 = type == TYPE_Q6_K;
     const int tn = q6 ? Q6_TN : TN;
     const int64_t tiles = (int64_t)((M + TM - 1) / TM) * ((N + tn - 1) / tn);
