@@ -146,18 +146,25 @@ def test_decoder_rejects_bad_config(dev):
     d.close()
 
 
-@pytest.mark.parametrize("preset,N", [("q4km", 512), ("q4km", 300), ("q4km", 64), ("q5km", 300)])
-def test_decoder_prefill_layer_equals_c_abi_composition(dev, preset, N):
+@pytest.mark.parametrize("preset,N,tiny", [("q4km", 512, False), ("q4km", 500, False), ("q4km", 300, False),
+                                           ("q4km", 64, False), ("q5km", 300, False), ("q4km", 40, True)])
+def test_decoder_prefill_layer_equals_c_abi_composition(dev, preset, N, tiny):
     """One prefill layer of the decoder (whose residual adds, RMSNorms and
     activation quantisation run fused, one pass per norm) is bit-identical to
     the same layer composed from the separate C-ABI entry points in the
     reference engine's order (transformer_layer, decode.cu:1760-1884):
     RMSNorm, Q/K/V GEMM, q/k norm + RoPE + KV store, attention, O GEMM,
-    residual add, RMSNorm, gate/up GEMM, SwiGLU, down GEMM, residual add."""
+    residual add, RMSNorm, gate/up GEMM, SwiGLU, down GEMM, residual add.
+    Cases: 512 and 500 tokens take every fused form (RMSNorm rows with the
+    codes, the attention front in the Q/K/V GEMM, the O codes in the
+    attention, the SwiGLU codes in the gate/up GEMM; 500 with a partial
+    last token tile); 300 and 64 tokens the smaller grids without the GEMM
+    epilogue forms; the Q5_K_M-style layer the fp16 GEMM; the tiny shape
+    (hidden 512, head_dim 64) the one-wave RMSNorm rows."""
     import ctypes
     import jllm
-    print_case("prefill layer composition", preset, N)
-    shape = WIDE
+    print_case("prefill layer composition", preset, N, tiny)
+    shape = TINY if tiny else WIDE
     H, QD, KVD, I = shape.hidden_dim, shape.n_heads * shape.head_dim, shape.n_kv_heads * shape.head_dim, \
         shape.intermediate_dim
     model = decoder.to_device(decoder.synth_np(shape, 21, preset), dev)
