@@ -333,6 +333,9 @@ void attn_partial_kernel(AttnArgs a) {
         }
         run_l = run_l * corr + ps;
         run_m = m_new;
+        // no live column's maximum moved: every rescale factor is exactly 1
+        // (e^0), so the accumulators keep their values without the multiply
+        const bool rescale = __builtin_amdgcn_ballot_w64(li < GC && corr != 1.0f) != 0;
         if (li < GC) {
             // keys 8m + 4lg + [0,4) for m = 0..3: four consecutive keys per 8-byte store
 #pragma unroll
@@ -354,6 +357,12 @@ void attn_partial_kernel(AttnArgs a) {
         for (int vv = 0; vv < NLIVE; vv++) {
             const int r = 8 * (vv >> 2) + 4 * lg + (vv & 3);
             cr[vv] = r < 2 * GC ? sMisc[r < GC ? r : r - GC] : 1.0f;
+        }
+        if (rescale) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                for (int vv = 0; vv < NLIVE; vv++) acc[dt][vv] *= cr[vv];
         }
         h8 pa[2];
 #pragma unroll
@@ -378,8 +387,7 @@ void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
                     for (int vv = 0; vv < 16; vv++) vt[vv] = ct[vv];
                 }
-#pragma unroll
-                for (int vv = 0; vv < NLIVE; vv++) acc[dt][vv] *= cr[vv];
+
 #pragma unroll
                 for (int st = 0; st < 2; st++) {
                     h8 vb;
