@@ -524,7 +524,7 @@ __device__ __forceinline__ RoundDesc round_desc(const StreamArgs& a, const Piece
             d.delta = (int)((uintptr_t)start & 15u);
             d.base = start - d.delta;
             d.nrec = (d.delta + d.nblk * BB + 15) & ~15;
-            d.col0 = (pc[i].b0 + f) % nb;
+            d.col0 = (int)((uint32_t)(pc[i].b0 + f) % (uint32_t)nb);     // non-negative: unsigned division
             d.slot0 = pc[i].slot0 + f;
         }
         r -= pc[i].rounds;
