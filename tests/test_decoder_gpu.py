@@ -146,9 +146,11 @@ def test_decoder_rejects_bad_config(dev):
     d.close()
 
 
-@pytest.mark.parametrize("preset,N,tiny", [("q4km", 512, False), ("q4km", 500, False), ("q4km", 300, False),
-                                           ("q4km", 64, False), ("q5km", 300, False), ("q4km", 40, True)])
-def test_decoder_prefill_layer_equals_c_abi_composition(dev, preset, N, tiny):
+@pytest.mark.parametrize("preset,N,tiny,start", [("q4km", 512, False, 0), ("q4km", 500, False, 0),
+                                                 ("q4km", 300, False, 0), ("q4km", 64, False, 0),
+                                                 ("q5km", 300, False, 0), ("q4km", 40, True, 0),
+                                                 ("q4km", 512, False, 512), ("q4km", 64, False, 300)])
+def test_decoder_prefill_layer_equals_c_abi_composition(dev, preset, N, tiny, start):
     """One prefill layer of the decoder (whose residual adds, RMSNorms and
     activation quantisation run fused, one pass per norm) is bit-identical to
     the same layer composed from the separate C-ABI entry points in the
@@ -160,53 +162,71 @@ def test_decoder_prefill_layer_equals_c_abi_composition(dev, preset, N, tiny):
     attention, the SwiGLU codes in the gate/up GEMM; 500 with a partial
     last token tile); 300 and 64 tokens the smaller grids without the GEMM
     epilogue forms; the Q5_K_M-style layer the fp16 GEMM; the tiny shape
-    (hidden 512, head_dim 64) the one-wave RMSNorm rows."""
+    (hidden 512, head_dim 64) the one-wave RMSNorm rows.  With start > 0 a
+    first chunk of `start` tokens fills the KV rows before the checked chunk
+    of N tokens at positions start.. (RoPE positions and KV rows offset, the
+    attention over the earlier rows)."""
     import ctypes
     import jllm
-    print_case("prefill layer composition", preset, N, tiny)
+    print_case("prefill layer composition", preset, N, tiny, start)
     shape = TINY if tiny else WIDE
     H, QD, KVD, I = shape.hidden_dim, shape.n_heads * shape.head_dim, shape.n_kv_heads * shape.head_dim, \
         shape.intermediate_dim
     model = decoder.to_device(decoder.synth_np(shape, 21, preset), dev)
-    d = decoder.Decoder(shape, model, N, max_batch=512)
-    x0 = torch.from_numpy(synth.x_f16(synth.rng(22), N * H).view(np.int16)).to(dev)
+    T = start + N
+    d = decoder.Decoder(shape, model, T, max_batch=512)
+    g = synth.rng(22)
+    xs = [torch.from_numpy(synth.x_f16(g, n * H).view(np.int16)).to(dev) for n in ((start, N) if start else (N,))]
 
     def e(n, dtype=torch.int16):
         return torch.empty(n, dtype=dtype, device=dev)
     for l in (0, 1):                                  # Q6_K and Q4_K down (q4km)
         L = model["layers"][l]
         t = L["types"]
-        xd = x0.clone()
-        d.layer(l, xd, N, 0)
-        kd = d.kv(l, N)
-        # the composition
-        normed, q, k, v, attn, x2, gate, up, act, y = (e(n) for n in (N * H, N * QD, N * KVD, N * KVD, N * QD,
-                                                                      N * H, N * I, N * I, N * I, N * H))
-        kc, vc = e(N * KVD, torch.int8), e(N * KVD, torch.int8)
-        ks, vs = e(N * shape.n_kv_heads, torch.float32), e(N * shape.n_kv_heads, torch.float32)
-        jllm.call("jllm_hip_fused_rmsnorm_residual", normed, x0, None, L["rms_attn"], N, H, shape.rms_eps, 1)
+        kc, vc = e(T * KVD, torch.int8), e(T * KVD, torch.int8)
+        ks, vs = e(T * shape.n_kv_heads, torch.float32), e(T * shape.n_kv_heads, torch.float32)
 
-        def multi(ys, names, x, K):
+        def multi(ys, names, x, n_tok, K):
             n = len(ys)
             yp = (ctypes.c_void_p * n)(*[a.data_ptr() for a in ys])
             wp = (ctypes.c_void_p * n)(*[L[m].data_ptr() for m in names])
             tp = (ctypes.c_int * n)(*[t[m] for m in names])
             mp = (ctypes.c_int * n)(*[shape.mat_shape(m)[0] for m in names])
-            jllm.call("jllm_hip_gemm_quant_batched_multi", yp, wp, tp, mp, n, x, N, K)
-        multi([q, k, v], ["wq", "wk", "wv"], normed, H)
-        jllm.call("jllm_hip_qk_norm_rope_store_kv", q, k, v, L["q_norm"], L["k_norm"], 1, shape.rms_eps, kc, vc, ks,
-                  vs, KVD, shape.n_heads, shape.n_kv_heads, shape.head_dim, shape.head_dim, 0, N, shape.rope_theta,
-                  1, 1)
-        jllm.call("jllm_hip_flash_attention_prefill_batched", attn, q, kc, vc, shape.n_heads, shape.n_kv_heads,
-                  shape.head_dim, shape.head_dim, N, 0, 1.0 / np.sqrt(shape.head_dim), 1, ks, vs, 0)
-        jllm.call("jllm_hip_gemm_quant_batched", x2, L["wo"], t["wo"], attn, H, N, QD)
-        jllm.call("jllm_hip_vec_add", x2, x2, x0, N * H)
-        jllm.call("jllm_hip_fused_rmsnorm_residual", normed, x2, None, L["rms_ffn"], N, H, shape.rms_eps, 1)
-        multi([gate, up], ["w_gate", "w_up"], normed, H)
-        jllm.call("jllm_hip_fused_swiglu", act, gate, up, N, I)
-        jllm.call("jllm_hip_gemm_quant_batched", y, L["w_down"], t["w_down"], act, H, N, I)
-        jllm.call("jllm_hip_vec_add", y, y, x2, N * H)
-        assert np.array_equal(from_dev(kc).reshape(kd[0].shape), kd[0]) and np.array_equal(from_dev(vc).reshape(kd[1].shape), kd[1])
+            jllm.call("jllm_hip_gemm_quant_batched_multi", yp, wp, tp, mp, n, x, n_tok, K)
+
+        def compose(x0, n, p0):
+            normed, q, k, v, attn, x2, gate, up, act, y = (e(m) for m in (n * H, n * QD, n * KVD, n * KVD, n * QD,
+                                                                          n * H, n * I, n * I, n * I, n * H))
+            jllm.call("jllm_hip_fused_rmsnorm_residual", normed, x0, None, L["rms_attn"], n, H, shape.rms_eps, 1)
+            multi([q, k, v], ["wq", "wk", "wv"], normed, n, H)
+            kv_off, sc_off = p0 * KVD, p0 * shape.n_kv_heads
+            jllm.call("jllm_hip_qk_norm_rope_store_kv", q, k, v, L["q_norm"], L["k_norm"], 1, shape.rms_eps,
+                      kc.data_ptr() + kv_off, vc.data_ptr() + kv_off, ks.data_ptr() + 4 * sc_off,
+                      vs.data_ptr() + 4 * sc_off, KVD, shape.n_heads, shape.n_kv_heads, shape.head_dim,
+                      shape.head_dim, p0, n, shape.rope_theta, 1, 1)
+            jllm.call("jllm_hip_flash_attention_prefill_batched", attn, q, kc, vc, shape.n_heads, shape.n_kv_heads,
+                      shape.head_dim, shape.head_dim, n, p0, 1.0 / np.sqrt(shape.head_dim), 1, ks, vs, 0)
+            jllm.call("jllm_hip_gemm_quant_batched", x2, L["wo"], t["wo"], attn, H, n, QD)
+            jllm.call("jllm_hip_vec_add", x2, x2, x0, n * H)
+            jllm.call("jllm_hip_fused_rmsnorm_residual", normed, x2, None, L["rms_ffn"], n, H, shape.rms_eps, 1)
+            multi([gate, up], ["w_gate", "w_up"], normed, n, H)
+            jllm.call("jllm_hip_fused_swiglu", act, gate, up, n, I)
+            jllm.call("jllm_hip_gemm_quant_batched", y, L["w_down"], t["w_down"], act, H, n, I)
+            jllm.call("jllm_hip_vec_add", y, y, x2, n * H)
+            return x2, y
+
+        p0 = 0
+        for x0 in xs:
+            n = x0.numel() // H
+            xd = x0.clone()
+            d.layer(l, xd, n, p0)
+            x2, y = compose(x0, n, p0)
+            p0 += n
+        kd = d.kv(l, T)
+        assert np.array_equal(from_dev(kc).reshape(kd[0].shape), kd[0]) and \
+            np.array_equal(from_dev(vc).reshape(kd[1].shape), kd[1])
+        assert np.array_equal(from_dev(ks).reshape(kd[2].shape), kd[2]) and \
+            np.array_equal(from_dev(vs).reshape(kd[3].shape), kd[3])
         assert np.array_equal(from_dev(x2).view(np.uint16).reshape(N, H), d.act(2, N)), l
         assert np.array_equal(from_dev(y), from_dev(xd)), l
     d.close()
