@@ -81,7 +81,19 @@ def q5km_types(shape, layer):
     return t
 
 
-PRESETS = {"q4km": q4km_types, "q5km": q5km_types}
+def q4km_mixed_types(shape, layer):
+    """Q4_K_M with more Q6_K matrices: attn_v and ffn_down Q6_K on even
+    layers (as llama.cpp's Q4_K_M assigns them on part of the layers), attn_output
+    Q6_K on odd layers -- mixed Q4_K / Q6_K products of one activation."""
+    t = {m: 12 for m in MATS}
+    if layer % 2 == 0:
+        t["wv"] = t["w_down"] = 14
+    else:
+        t["wo"] = 14
+    return t
+
+
+PRESETS = {"q4km": q4km_types, "q5km": q5km_types, "q4km_mixed": q4km_mixed_types}
 
 
 # Block scales chosen so the dequantised weights have mean ~0 and a

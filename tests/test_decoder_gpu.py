@@ -149,7 +149,8 @@ def test_decoder_rejects_bad_config(dev):
 @pytest.mark.parametrize("preset,N,tiny,start", [("q4km", 512, False, 0), ("q4km", 500, False, 0),
                                                  ("q4km", 300, False, 0), ("q4km", 64, False, 0),
                                                  ("q5km", 300, False, 0), ("q4km", 40, True, 0),
-                                                 ("q4km", 512, False, 512), ("q4km", 64, False, 300)])
+                                                 ("q4km", 512, False, 512), ("q4km", 64, False, 300),
+                                                 ("q4km_mixed", 512, False, 0), ("q4km_mixed", 300, False, 0)])
 def test_decoder_prefill_layer_equals_c_abi_composition(dev, preset, N, tiny, start):
     """One prefill layer of the decoder (whose residual adds, RMSNorms and
     activation quantisation run fused, one pass per norm) is bit-identical to
@@ -162,7 +163,9 @@ def test_decoder_prefill_layer_equals_c_abi_composition(dev, preset, N, tiny, st
     attention, the SwiGLU codes in the gate/up GEMM; 500 with a partial
     last token tile); 300 and 64 tokens the smaller grids without the GEMM
     epilogue forms; the Q5_K_M-style layer the fp16 GEMM; the tiny shape
-    (hidden 512, head_dim 64) the one-wave RMSNorm rows.  With start > 0 a
+    (hidden 512, head_dim 64) the one-wave RMSNorm rows; the mixed layers
+    (Q6_K V / O) the fp16 codes of the RMSNorm rows and of the attention
+    output next to the int8 ones.  With start > 0 a
     first chunk of `start` tokens fills the KV rows before the checked chunk
     of N tokens at positions start.. (RoPE positions and KV rows offset, the
     attention over the earlier rows)."""
