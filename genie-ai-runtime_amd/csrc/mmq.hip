@@ -352,12 +352,12 @@ __device__ __forceinline__ f32x16m mfma16(h8m a, h8m b, f32x16m c) {
 // per super-block, its row's 16-byte header) straight into registers one
 // stage ahead.  The activation codes and scale words, shared by the four
 // waves, go from global memory straight to LDS (buffer_load ... lds) in a
-// ring of three stages, two stages ahead; the 16-byte pieces of a token are
+// ring of four stages, a super-block ahead; the 16-byte pieces of a token are
 // XOR-swizzled so the B-operand reads of a wave hit distinct banks.
 constexpr int ST_B = TN * 128;              // activation codes of a stage: 64 tokens x 128 B
 constexpr int ST_S = 4 * TN * 4;            // scale words: 4 sub-blocks x 64 tokens
 constexpr int ST_BYTES = ST_B + ST_S;
-constexpr int NRING = 3;
+constexpr int NRING = 4;
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -541,17 +541,14 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
         }
     };
 
-    // Stage pipeline (k0 is even, k1 - k0 is even): per iteration, the next
-    // stage's weight bytes (+ header) into registers, then stage k+2's
-    // activation DMA, then stage k from registers and LDS.  The loads of a
-    // wave complete in issue order, so waiting until only the newest TT + 1
-    // (the DMA of stage k+2) are outstanding means stage k+1's weights and DMA have
-    // landed; a plain s_barrier (no memory fence: a fence would wait for the
-    // stage k+2 DMA too) then makes every wave's copy visible, and it also
-    // orders every wave's reads of the buffer that the next DMA overwrites.
-    // Past the last stage the loads repeat the last stage (in bounds, into a
-    // ring slot nobody reads), so every iteration has the same load count
-    // and the waits are unconditional.
+    // Stage pipeline (k0 is even, k1 - k0 is even; a stage is half a
+    // super-block, slot k % 4 of the ring).  The loads of a wave complete in
+    // issue order and a plain s_barrier (no memory fence: a fence would wait
+    // for every load in flight) after the DMA has landed makes every wave's
+    // copy visible; it also orders every wave's reads of the slots that the
+    // next DMA overwrites.  Past the last stage the loads repeat the last
+    // stage (in bounds; the same bytes into its own slot), so every
+    // iteration has the same load count and the waits are unconditional.
     u32x4m a0[2], a1[2];
     u32x4m hdr = __builtin_amdgcn_raw_buffer_load_b128(rW, voRow, (k0 >> 1) * Q4K_BYTES, 0);
     load_a(k0, a0);
@@ -559,24 +556,27 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
     issue_b(k0 + 1);
     __builtin_amdgcn_s_waitcnt(0x0F70);                // everything of stage k0 (and k0+1's DMA)
     __builtin_amdgcn_s_barrier();
+    // One workgroup barrier per super-block: both halves of the next
+    // super-block are DMA'd into the other two ring slots while this one is
+    // computed (the A-operand registers are waited for by the compiler).
+    // The barrier's wait vmcnt(3) leaves only the newest header and A loads
+    // (issued after that DMA) in flight.  (One barrier per half super-block
+    // with a ring of three slots: 1-2 % slower, same bits.)
 #pragma unroll 1
     for (int k = k0; k < k1; k += 2) {
-        const int kl = k1 - 1;                         // last stage
-        // even stage k: first half of super-block k/2
+        const int kl = k1 - 1;
         if (OUT != 2) scales(hdr);
         load_a(k + 1, a1);
-        __builtin_amdgcn_sched_barrier(0);             // keep the DMA the newest loads
+        __builtin_amdgcn_sched_barrier(0);
         issue_b(min(k + 2, kl));
+        issue_b(min(k + 3, kl));
+        __builtin_amdgcn_sched_barrier(0);
         compute(k, a0);
-        __builtin_amdgcn_s_waitcnt(TT == 2 ? 0x0F73 : 0x0F72);   // vmcnt(TT + 1)            // vmcnt(3): all but stage k+2's DMA
-        __builtin_amdgcn_s_barrier();
-        // odd stage k+1
         hdr = __builtin_amdgcn_raw_buffer_load_b128(rW, voRow, (min(k + 2, kl) >> 1) * Q4K_BYTES, 0);
         load_a(min(k + 2, kl), a0);
         __builtin_amdgcn_sched_barrier(0);
-        issue_b(min(k + 3, kl));
         compute(k + 1, a1);
-        __builtin_amdgcn_s_waitcnt(TT == 2 ? 0x0F73 : 0x0F72);   // vmcnt(TT + 1)
+        __builtin_amdgcn_s_waitcnt(0x0F73);            // vmcnt(3): the DMA of k+2, k+3 has landed
         __builtin_amdgcn_s_barrier();
     }
     if (OUT == 2) return;
@@ -688,7 +688,7 @@ void mmq_q4k_swiglu_kernel(MmqSegs sg, const uint8_t* __restrict__ codes, const 
 }
 
 // 32-token halves per Q4_K workgroup tile for a launch of `waves` waves
-// with 64-token tiles.  The 32-token tile keeps 97-101 VGPRs and 13.5 KB of
+// with 64-token tiles.  The 32-token tile keeps 97-101 VGPRs and 18 KB of
 // LDS, so a CU holds 5 of its workgroups instead of 3; it decodes each
 // weight operand for half the tokens.  Measured (us, 64-token / 32-token
 // tiles, quantiser and split-K reduce included): Q/K/V multi-launch 6144 x
