@@ -51,6 +51,10 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int AT_KEYS = 32;          // keys per tile (one MFMA column block)
+// LDS row stride of the P' tile (halves): 18 dwords, so the 8-byte writes
+// and reads of lanes (row li, key group lg) spread evenly over the 32 banks
+// (a 16-dword stride put every row on the same 4 banks)
+constexpr int AT_PLD = AT_KEYS + 4;
 constexpr int AT_MAXHD = 128;
 constexpr int AT_MAXG = 16;          // max query heads per KV head
 constexpr int AT_MAXS = ATTN_MAX_SPLITS;   // max splits
@@ -129,7 +133,7 @@ size_t attn_scratch_bytes(int n_heads, int n_splits, int head_dim) {
 // LDS of one wave (P' tile, per-key scales, then its final hi/lo rows)
 __host__ __device__ size_t attn_wave_lds_bytes(int n_heads, int n_kv, int head_dim, int tq) {
     const int G = n_heads / n_kv * tq;                                // columns of a wave
-    const size_t loop = (size_t)32 * AT_KEYS * 2 + 96 * 4;            // P' rows (fp16) + corr/ks/vs
+    const size_t loop = (size_t)32 * AT_PLD * 2 + 96 * 4;            // P' rows (fp16) + corr/ks/vs
     const size_t outb = (size_t)((2 * G + 7) & ~7) * head_dim * 4;   // final hi/lo rows (fp32, >= 8 rows)
     return ((loop > outb ? loop : outb) + 15) & ~(size_t)15;
 }
@@ -226,8 +230,8 @@ void attn_partial_kernel(AttnArgs a) {
     if (first < kv1) load_tile(first, rk, rv, ksn, vsn);
     __builtin_amdgcn_sched_barrier(0);
 
-    _Float16* sP = (_Float16*)smem;                              // [32 rows][32 keys]
-    float* sMisc = (float*)(smem + 32 * AT_KEYS * 2);            // corr[32] | ks[32] | vs[32]
+    _Float16* sP = (_Float16*)smem;                              // [32 rows][AT_PLD: 32 keys + pad]
+    float* sMisc = (float*)(smem + 32 * AT_PLD * 2);            // corr[32] | ks[32] | vs[32]
 
     // q operand: lane (head li, lg), step st -> d = lg*half + 8*st + [0, 8)
     // (every lane loads a valid row -- its column's head modulo G -- so the
@@ -239,7 +243,7 @@ void attn_partial_kernel(AttnArgs a) {
                                            lg * half + 8 * st);
         qa[st] = __builtin_bit_cast(h8, li < GC ? qv : u32x4a{0u, 0u, 0u, 0u});
     }
-    for (int i = l; i < 32 * AT_KEYS; i += 64) sP[i] = (_Float16)0.0f;
+    for (int i = l; i < 32 * AT_PLD; i += 64) sP[i] = (_Float16)0.0f;
 
     // identity operands of the V transpose.  int8: lane (col li, lg) holds
     // B[16lg + i][li] = (16lg + i == li).  fp16: two K = 16 halves, lane
@@ -341,8 +345,8 @@ void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
             for (int m4 = 0; m4 < 4; m4++) {
                 const int key0 = 8 * m4 + 4 * lg;
-                *(u32x2a*)&sP[li * AT_KEYS + key0] = u32x2a{hi2[2 * m4], hi2[2 * m4 + 1]};
-                *(u32x2a*)&sP[(GC + li) * AT_KEYS + key0] = u32x2a{lo2[2 * m4], lo2[2 * m4 + 1]};
+                *(u32x2a*)&sP[li * AT_PLD + key0] = u32x2a{hi2[2 * m4], hi2[2 * m4 + 1]};
+                *(u32x2a*)&sP[(GC + li) * AT_PLD + key0] = u32x2a{lo2[2 * m4], lo2[2 * m4 + 1]};
             }
             if (lg == 0) sMisc[li] = corr;
         }
@@ -367,8 +371,8 @@ void attn_partial_kernel(AttnArgs a) {
         h8 pa[2];
 #pragma unroll
         for (int st = 0; st < 2; st++) {
-            const u32x2a lo4 = *(const u32x2a*)&sP[li * AT_KEYS + 16 * st + 4 * lg];
-            const u32x2a hi4 = *(const u32x2a*)&sP[li * AT_KEYS + 16 * st + 8 + 4 * lg];
+            const u32x2a lo4 = *(const u32x2a*)&sP[li * AT_PLD + 16 * st + 4 * lg];
+            const u32x2a hi4 = *(const u32x2a*)&sP[li * AT_PLD + 16 * st + 8 + 4 * lg];
             pa[st] = __builtin_bit_cast(h8, u32x4a{lo4.x, lo4.y, hi4.x, hi4.y});
         }
 #pragma unroll

@@ -5,6 +5,8 @@
   lmhead: the Q6_K lm_head GEMV (151936 x 2560, fp32 out), 4 distinct copies
   e2e   : the Qwen3-4B-shaped Q4_K_M decoder (36 layers, INT8 KV): prefill
           of a 512-token prompt, then 32 greedy decode steps
+  attnp : INT8-KV prefill attention of 512 tokens at position 0 (32 q / 8 KV
+          heads, head_dim 128), 5 calls
   copy  : a plain device-to-device copy of 256 MiB (calibrates FETCH_SIZE /
           WRITE_SIZE against a known byte count)
   mmq   : the Q4_K prefill GEMM 9728 x 2560 at N = 512 tokens (fp16 out), 5 calls
@@ -85,6 +87,14 @@ def main(mode):
                               s, s, 0)
             torch.cuda.synchronize()
             del caches
+    elif mode == "attnp":
+        H, KV, HD, N = 32, 8, 128, 512
+        q = up(synth.x_f16(g, N * H * HD))
+        out = torch.empty(N * H * HD, dtype=torch.int16, device=dev)
+        k, v, s = up(synth.kv_int8(g, N, KV, HD)), up(synth.kv_int8(g, N, KV, HD)), up(synth.kv_scales(g, N, KV))
+        for _ in range(5):
+            jllm.call("jllm_hip_flash_attention_prefill_batched", out, q, k, v, H, KV, HD, HD, N, 0, 0.0884, 1,
+                      s, s, 0)
     elif mode == "copy":
         a = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
         b = torch.empty_like(a)
