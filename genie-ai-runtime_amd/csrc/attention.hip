@@ -298,9 +298,14 @@ void attn_partial_kernel(AttnArgs a) {
         float mx = -FLT_MAX;
 #pragma unroll
         for (int vv = 0; vv < 16; vv++) sc[vv] *= kscl[vv];
-        // key masks only where a tile can hold dead keys (uniform branch):
-        // prefill columns, or a decode tile of fewer than AT_KEYS keys
-        if (MT || n < AT_KEYS) {
+        // key masks only where a tile can hold dead keys (uniform branch): a
+        // prefill tile that reaches past the first column's causal bound or
+        // below the last column's window start, or a tile of fewer than
+        // AT_KEYS keys (a live key keeps its score either way, so skipping
+        // the masks of a full tile changes no bit)
+        const bool full = n == AT_KEYS && (!MT || (p0 + AT_KEYS <= aseq + tok0 &&
+                                                   (a.window <= 0 || p0 >= aseq + tok0 + ntok - 1 - a.window)));
+        if (!full) {
 #pragma unroll
             for (int vv = 0; vv < 16; vv++) {
                 const int key = 8 * (vv >> 2) + 4 * lg + (vv & 3);
