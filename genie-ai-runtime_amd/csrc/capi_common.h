@@ -123,7 +123,8 @@ int residual_finish(const char* tag, const ResidualRows& r, int N, int M, void* 
 // The deferred rows completed, then normed [N x H] = RMSNorm(y) with weights
 // w (jllm_hip_fused_rmsnorm_residual's bits), and, for N > 1, the activation
 // codes of the kinds that outs needs, in one pass where the shapes allow
-// (*quantized = true: call gemm_batched_shared_x with quantized = true).
+// (*quantized = true: call gemm_batched_shared_x with quantized = true; the
+// fp16 rows are then written only when an output reads them, i.e. Q5_K).
 int norm_rows(const char* tag, const ResidualRows& r, int N, int H, uint16_t* normed, const void* w, bool w_fp32,
               float eps, const GemmOut* outs, int n, bool* quantized, void* stream);
 

@@ -222,10 +222,12 @@ int norm_rows(const char* tag, const ResidualRows& r, int N, int H, uint16_t* no
     *quantized = false;
     if (N <= 0) return JLLM_OK;
     bool need[2] = {false, false};                   // DS4 (Q4_K), D4 (Q6_K)
+    bool need_f16 = false;                           // an output reads the fp16 rows (Q5_K)
     for (int i = 0; i < n; i++) {
         if (outs[i].M == 0) continue;
         if (outs[i].type == 12) need[0] = true;
-        if (outs[i].type == 14) need[1] = true;
+        else if (outs[i].type == 14) need[1] = true;
+        else need_f16 = true;
     }
     NormQuantArgs a;
     a.y = r.y; a.res = r.res; a.ws = r.ws; a.S = r.S; a.mode = r.mode;
@@ -240,6 +242,7 @@ int norm_rows(const char* tag, const ResidualRows& r, int N, int H, uint16_t* no
         }
         if (need[0]) { a.c8 = codes[0]; a.s8 = scl[0]; }
         if (need[1]) { a.c16 = codes[1]; a.s16 = scl[1]; }
+        if (!need_f16) a.normed = nullptr;          // every consumer reads the codes: no fp16 rows
         const int st = launch_status(norm_quant_launch(a, w_fp32, (hipStream_t)stream), tag);
         if (st == JLLM_OK) *quantized = true;
         return st;

@@ -29,8 +29,9 @@ inline size_t mmq_scales_bytes(int K, int Npad) { return (size_t)(K / 32) * Npad
 // pass (one workgroup per row of Npad), the residual add that forms y
 // optionally in front: mode 0: y as given; 1: y = half(y + res); 2: y =
 // half(half(sum of the S fp32 partials ws[s][N][H]) + res).  normed =
-// half(y * rrms * w); the codes and scale words of each kind whose codes
-// pointer is non-null (c8/s8: int8 codes, DS4 words -- the Q4_K kernel's;
+// half(y * rrms * w) (not written when normed is null); the codes and scale
+// words of each kind whose codes pointer is non-null (c8/s8: int8 codes, DS4
+// words -- the Q4_K kernel's;
 // c16/s16: fp16 codes, D4 words -- the Q6_K kernel's).  Every output has the
 // bits of the separate residual add, rmsnorm_launch and quantiser.
 struct NormQuantArgs {

@@ -231,7 +231,7 @@ __global__ __launch_bounds__(GS) void norm_quant_kernel(NormQuantArgs a) {
             for (int e = 0; e < 4; e++)
                 o[e] = (uint32_t)f32_to_f16_bits(v[c][2 * e] * rrms * wv[2 * e]) |
                        ((uint32_t)f32_to_f16_bits(v[c][2 * e + 1] * rrms * wv[2 * e + 1]) << 16);
-            *(u32x4m*)(a.normed + off + i) = u32x4m{o[0], o[1], o[2], o[3]};
+            if (a.normed) *(u32x4m*)(a.normed + off + i) = u32x4m{o[0], o[1], o[2], o[3]};
 #pragma unroll
             for (int e = 0; e < 4; e++) { q[2 * e] = f16_bits_to_f32(o[e] & 0xFFFFu); q[2 * e + 1] = f16_bits_to_f32(o[e] >> 16); }
         } else {
