@@ -42,11 +42,13 @@ struct AttnArgs {
 constexpr int ATTN_MAX_WAVES = 8;
 // measured (512-token prefill, one layer): 1 wave 41.4 us, 2 waves 37.5 us, 4 waves 38.6 us; with the
 // token blocks dispatched last-first: 2 waves 36.1 us, 4 waves 36.8 us, 8 waves 52.7 us
-// (with the combination's per-column weights formed once: 1 / 2 / 3 / 4 waves 39.0 / 29.0 / 31.3 / 29.7 us)
-constexpr int ATTN_PREFILL_WAVES = 2;
+// (with the combination's per-column weights formed once: 1 / 2 / 3 / 4 waves 39.0 / 29.0 / 31.3 / 29.7 us;
+// with 32 columns per wave (P' high / low as two A operands): 1 / 2 / 3 / 4 / 6 / 8 waves
+// 38.7 / 23.4 / 20.8 / 19.0 / 25.7 / 24.8 us)
+constexpr int ATTN_PREFILL_WAVES = 4;
 
 constexpr int ATTN_MAX_SPLITS = 256;
-constexpr int ATTN_MAX_COLUMNS = 16;   // (token, head) columns per wave
+constexpr int ATTN_MAX_COLUMNS = 32;   // (token, head) columns per prefill wave
 int attn_splits(int seq_len, int n_kv);
 // waves per decode workgroup for n_splits key ranges
 int attn_decode_waves(int n_splits);

@@ -133,8 +133,9 @@ size_t attn_scratch_bytes(int n_heads, int n_splits, int head_dim) {
 // LDS of one wave (P' tile, per-key scales, then its final hi/lo rows)
 __host__ __device__ size_t attn_wave_lds_bytes(int n_heads, int n_kv, int head_dim, int tq) {
     const int G = n_heads / n_kv * tq;                                // columns of a wave
-    const size_t loop = (size_t)32 * AT_PLD * 2 + 96 * 4;            // P' rows (fp16) + corr/ks/vs
-    const size_t outb = (size_t)((2 * G + 7) & ~7) * head_dim * 4;   // final hi/lo rows (fp32, >= 8 rows)
+    const bool ps = tq > 1;                                          // prefill: one row per column
+    const size_t loop = (size_t)(ps ? 64 : 32) * AT_PLD * 2 + 96 * 4; // P' rows (fp16) + corr/ks/vs
+    const size_t outb = (size_t)(((ps ? G : 2 * G) + 7) & ~7) * head_dim * 4;   // final rows (fp32, >= 8)
     return ((loop > outb ? loop : outb) + 15) & ~(size_t)15;
 }
 // a workgroup of W waves: W wave regions, then (m, l) of each wave's columns
@@ -145,7 +146,7 @@ __host__ __device__ size_t attn_lds_bytes(int n_heads, int n_kv, int head_dim, i
 
 // One wave per (KV head, split[, block of tq query tokens]).  The wave's
 // "columns" are its (token, head) pairs: column c = token tok0 + c / G, head
-// kvh * G + c % G, GC = tq * G <= 16 of them; each has its own causal bound
+// kvh * G + c % G, GC = tq * G <= 32 of them; each has its own causal bound
 // (and window), so one key tile serves tq tokens.  Lane (li = lane & 31,
 // lg = lane >> 5); below, "head li" means column li.
 //   Q.K^T : C = K.q^T (rows = the tile's 32 keys, cols = query heads, K = d);
@@ -154,8 +155,10 @@ __host__ __device__ size_t attn_lds_bytes(int n_heads, int n_kv, int head_dim, i
 //           V rows (K = d) and B = the identity, C = V lands in the MFMA
 //           output layout, i.e. lane (d = li, lg) holds 16 keys of column d
 //           (int8: one v_mfma_i32_32x32x32_i8 per 32 d, exact)
-//   P.V   : A = P'  (rows = heads, high parts then low parts; K = keys in the
-//           order the transpose delivers them), B = those V columns
+//   P.V   : A = P'  (decode: rows = heads, high parts then low parts;
+//           prefill: rows = columns, the high and the low parts as two A
+//           operands into the same accumulator; K = keys in the order the
+//           transpose delivers them), B = those V columns
 // The K and V rows of the next tile are loaded into registers while the
 // current tile is computed.
 // MT: several query tokens per wave (per-column causal bounds); the
@@ -171,6 +174,11 @@ void attn_partial_kernel(AttnArgs a) {
     constexpr int NDT = HD / 32;                        // 32-wide d chunks
     constexpr int VW = NDT * EB;                        // V: 16-byte chunks per lane
     constexpr int NST = half / 8;                       // Q.K^T MFMA steps
+    // prefill (MT): the high and low fp16 parts of P' are two A operands
+    // accumulating into the same accumulator row, one row per column, so a
+    // wave serves 32 columns; decode keeps a row for each (2 x G rows)
+    constexpr bool PS = MT;
+    constexpr int PROWS = PS ? 64 : 32;                 // P' tile rows in LDS
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_wg[];
     const int W = a.wsplit;
     const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -231,7 +239,7 @@ void attn_partial_kernel(AttnArgs a) {
     __builtin_amdgcn_sched_barrier(0);
 
     _Float16* sP = (_Float16*)smem;                              // [32 rows][AT_PLD: 32 keys + pad]
-    float* sMisc = (float*)(smem + 32 * AT_PLD * 2);            // corr[32] | ks[32] | vs[32]
+    float* sMisc = (float*)(smem + PROWS * AT_PLD * 2);         // corr[32] | ks[32] | vs[32]
 
     // q operand: lane (head li, lg), step st -> d = lg*half + 8*st + [0, 8)
     // (every lane loads a valid row -- its column's head modulo G -- so the
@@ -243,7 +251,7 @@ void attn_partial_kernel(AttnArgs a) {
                                            lg * half + 8 * st);
         qa[st] = __builtin_bit_cast(h8, li < GC ? qv : u32x4a{0u, 0u, 0u, 0u});
     }
-    for (int i = l; i < 32 * AT_PLD; i += 64) sP[i] = (_Float16)0.0f;
+    for (int i = l; i < PROWS * AT_PLD; i += 64) sP[i] = (_Float16)0.0f;
 
     // identity operands of the V transpose.  int8: lane (col li, lg) holds
     // B[16lg + i][li] = (16lg + i == li).  fp16: two K = 16 halves, lane
@@ -351,7 +359,7 @@ void attn_partial_kernel(AttnArgs a) {
             for (int m4 = 0; m4 < 4; m4++) {
                 const int key0 = 8 * m4 + 4 * lg;
                 *(u32x2a*)&sP[li * AT_PLD + key0] = u32x2a{hi2[2 * m4], hi2[2 * m4 + 1]};
-                *(u32x2a*)&sP[(GC + li) * AT_PLD + key0] = u32x2a{lo2[2 * m4], lo2[2 * m4 + 1]};
+                *(u32x2a*)&sP[((PS ? 32 : GC) + li) * AT_PLD + key0] = u32x2a{lo2[2 * m4], lo2[2 * m4 + 1]};
             }
             if (lg == 0) sMisc[li] = corr;
         }
@@ -365,7 +373,7 @@ void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
         for (int vv = 0; vv < NLIVE; vv++) {
             const int r = 8 * (vv >> 2) + 4 * lg + (vv & 3);
-            cr[vv] = r < 2 * GC ? sMisc[r < GC ? r : r - GC] : 1.0f;
+            cr[vv] = PS ? (r < GC ? sMisc[r] : 1.0f) : (r < 2 * GC ? sMisc[r < GC ? r : r - GC] : 1.0f);
         }
         if (rescale) {
 #pragma unroll
@@ -373,12 +381,17 @@ void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
                 for (int vv = 0; vv < NLIVE; vv++) acc[dt][vv] *= cr[vv];
         }
-        h8 pa[2];
+        h8 pa[2], pl[2];
 #pragma unroll
         for (int st = 0; st < 2; st++) {
             const u32x2a lo4 = *(const u32x2a*)&sP[li * AT_PLD + 16 * st + 4 * lg];
             const u32x2a hi4 = *(const u32x2a*)&sP[li * AT_PLD + 16 * st + 8 + 4 * lg];
             pa[st] = __builtin_bit_cast(h8, u32x4a{lo4.x, lo4.y, hi4.x, hi4.y});
+            if (PS) {
+                const u32x2a a4 = *(const u32x2a*)&sP[(32 + li) * AT_PLD + 16 * st + 4 * lg];
+                const u32x2a b4 = *(const u32x2a*)&sP[(32 + li) * AT_PLD + 16 * st + 8 + 4 * lg];
+                pl[st] = __builtin_bit_cast(h8, u32x4a{a4.x, a4.y, b4.x, b4.y});
+            }
         }
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
@@ -407,6 +420,7 @@ void attn_partial_kernel(AttnArgs a) {
                         vb[e + 1] = h2[1];
                     }
                     acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[st], vb, acc[dt], 0, 0, 0);
+                    if (PS) acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl[st], vb, acc[dt], 0, 0, 0);
                 }
             }
         }
@@ -557,7 +571,7 @@ void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
         for (int vv = 0; vv < 16; vv++) {
             const int r = 8 * (vv >> 2) + 4 * lg + (vv & 3);
-            if (r < 2 * GC) sO[r * hd + 32 * dt + li] = acc[dt][vv];
+            if (r < (PS ? GC : 2 * GC)) sO[r * hd + 32 * dt + li] = acc[dt][vv];
         }
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
@@ -597,7 +611,8 @@ void attn_partial_kernel(AttnArgs a) {
                 const float f = sF[u * 32 + c];
                 const float* so = (const float*)(smem_wg + (size_t)u * wave_lds);
                 const f32x4a h0 = *(const f32x4a*)&so[c * hd + d0], h1 = *(const f32x4a*)&so[c * hd + d0 + 4];
-                const f32x4a l0 = *(const f32x4a*)&so[(GC + c) * hd + d0], l1 = *(const f32x4a*)&so[(GC + c) * hd + d0 + 4];
+                f32x4a l0 = f32x4a{0.0f, 0.0f, 0.0f, 0.0f}, l1 = l0;
+                if (!PS) { l0 = *(const f32x4a*)&so[(GC + c) * hd + d0]; l1 = *(const f32x4a*)&so[(GC + c) * hd + d0 + 4]; }
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     num[i] += (h0[i] + l0[i]) * f;
@@ -638,7 +653,7 @@ void attn_partial_kernel(AttnArgs a) {
             const float il = __shfl(inv_l, c, 64);
             const int ct = MT ? c / G : 0, ch = MT ? c % G : c;
             uint16_t* ot = a.out + (int64_t)(tok0 + ct) * a.n_heads * hd + (int64_t)(pbase + ch) * hd;
-            ot[d] = f32_to_f16_bits((sO[c * hd + d] + sO[(GC + c) * hd + d]) * il);
+            ot[d] = f32_to_f16_bits((PS ? sO[c * hd + d] : sO[c * hd + d] + sO[(GC + c) * hd + d]) * il);
         }
         return;
     }
@@ -805,7 +820,7 @@ extern "C" int jllm_hip_attn_trace_read(uint64_t* host) {
 
 hipError_t attn_launch(const AttnArgs& a, bool kv_int8, hipStream_t st) {
     if (a.tokens < 1 || a.tq < 1 || (a.tokens > 1 && a.n_splits != 1) || (a.n_splits > 1 && a.tq != 1) ||
-        (a.n_heads / a.n_kv) * a.tq > AT_MAXG)
+        (a.n_heads / a.n_kv) * a.tq > (a.tq > 1 ? ATTN_MAX_COLUMNS : AT_MAXG))
         return hipErrorInvalidValue;
     dim3 grid(a.n_kv, a.n_splits, (a.tokens + a.tq - 1) / a.tq);
     const bool mt = a.tq > 1;
