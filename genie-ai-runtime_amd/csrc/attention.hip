@@ -27,8 +27,10 @@
 // needs one cross-lane step); the V tile is transposed by an identity MFMA
 // (int8: v_mfma_i32_32x32x32_i8 against I, exact) and P.V runs as
 // v_mfma_f32_32x32x16_f16 with the fp32 probabilities (times vs) split into
-// a high and a low fp16 part stacked as extra rows of the A operand, so the
-// P.V products keep ~22 bits.
+// a high and a low fp16 part, so the P.V products keep ~22 bits: in decode
+// the two parts are extra rows of the A operand (2 x G rows), in prefill two
+// A operands accumulating into the same rows, so a prefill wave serves 32
+// columns (8 tokens x 4 heads).
 #include <float.h>
 #include <stdlib.h>
 #include <string.h>
