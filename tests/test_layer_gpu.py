@@ -247,7 +247,8 @@ def _close(got, want):
 
 @pytest.mark.parametrize("H,KV,hd,start,N,window", [(32, 8, 128, 0, 1, 0), (32, 8, 128, 0, 40, 0),
                                                      (32, 8, 128, 100, 64, 0), (32, 8, 128, 0, 512, 0),
-                                                     (16, 2, 64, 30, 33, 16), (8, 8, 96, 0, 17, 0)])
+                                                     (16, 2, 64, 30, 33, 16), (8, 8, 96, 0, 17, 0),
+                                                     (32, 2, 128, 7, 41, 0), (24, 8, 128, 0, 70, 32)])
 def test_prefill_attention(dev, H, KV, hd, start, N, window):
     print_case("prefill_attn", H, KV, hd, start, N, window)
     g = synth.rng(start + N + hd)
