@@ -203,13 +203,13 @@ def test_embedding_rows_bit_exact(dev, t):
     assert np.array_equal(from_dev(one, np.uint16), oracle.embed_row(W, t, 123, hidden))
 
 
-@pytest.mark.parametrize("n", [151936, 1000, 7])
+@pytest.mark.parametrize("n", [151936, 1000, 7, 4099, 262144, 262145])
 def test_argmax(dev, n):
     print_case("argmax", n)
     g = synth.rng(n)
     x = g.standard_normal(n).astype(np.float32)
     out = torch.zeros(1, dtype=torch.int32, device=dev)
-    for case in range(6):
+    for case in range(7):
         if case == 1:
             x[n // 3] = x[n - 1] = 50.0                      # tie: the lower index wins
         if case == 2:
@@ -226,6 +226,12 @@ def test_argmax(dev, n):
                     x[i] = 60.0
         if case == 5:
             x = np.full(n, -np.inf, np.float32)              # no finite value: index 0
+        if case == 6:
+            # ties in different workgroups and waves, the highest index first
+            x = g.standard_normal(n).astype(np.float32)
+            for i in (4 * (1024 * 9 + 700) + 2, 4 * (1024 * 3 + 5) + 1, 4 * 1000 + 3, 4 * 70):
+                if i < n:
+                    x[i] = 70.0
         jllm.call("jllm_hip_argmax_f32", out, to_dev(x), n)
         assert int(from_dev(out)[0]) == oracle.argmax(x), case
 
