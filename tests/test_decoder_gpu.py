@@ -131,6 +131,42 @@ def test_decoder_chunked_prefill_and_generate_bit_identical(dev):
     d.close()
 
 
+def test_decoder_prefill_chunk_of_one_token(dev):
+    """A prefill whose last chunk holds one token (40 = 3 x 13 + 1): that
+    chunk's layers take the single-row forms (the products of one row are
+    the reference's GEMVs, whose O / down activations are not q8_1-quantised)
+    at start 39 against KV written by the batched chunks.  Its logits match
+    the oracle prefilled in the same chunks within the decoder bar (the
+    whole-prompt prefill differs by the GEMV-vs-MMQ activation rounding, ~2 %
+    on this shape), and the KV rows of the batched chunks are the bytes of the
+    whole-prompt prefill."""
+    print_case("decoder chunk of one")
+    import oracle
+    oracle.set_threads(min(16, os.cpu_count() or 1))
+    shape = TINY
+    model_np = decoder.synth_np(shape, 7)
+    model = decoder.to_device(model_np, dev)
+    prompt = synth.rng(8).integers(0, shape.vocab_size, 40).astype(np.int32)
+    res = []
+    for max_batch in (64, 13):
+        d = decoder.Decoder(shape, model, 48, max_batch=max_batch)
+        t = torch.zeros(1, dtype=torch.int32, device=dev)
+        d.prefill(_tok(prompt, dev), 0, t)
+        res.append((int(from_dev(t)[0]), from_dev(d.logits()), d.kv(0, 39) + d.kv(1, 39)))
+        d.close()
+    (_, _, kv0), (t1, lg1, kv1) = res
+    for a, b in zip(kv0, kv1):
+        assert np.array_equal(a, b)
+    orc = decoder_oracle.OracleDecoder(shape, model_np, 48)
+    for c0 in range(0, 40, 13):
+        want_tok = orc.prefill(list(prompt[c0:c0 + 13]), c0)
+    want = orc.logits
+    assert _rel(lg1, want) <= TOL, _rel(lg1, want)
+    top2 = np.sort(want)[-2:]
+    if top2[1] - top2[0] > TOL * np.abs(want).max():
+        assert t1 == want_tok
+
+
 def test_decoder_rejects_bad_config(dev):
     shape = TINY
     model = decoder.to_device(decoder.synth_np(shape, 9), dev)
