@@ -461,7 +461,6 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
     // stage's four sum x_j in their slots.
     h4m As = h4m{}, Am = h4m{};
     auto scales = [&](const u32x4m hdr) {
-        const float d = f16_bits_to_f32(hdr.x & 0xFFFFu), dmin = f16_bits_to_f32(hdr.x >> 16);
         // the 6-bit (sc, m) of sub-blocks 4g .. 4g+3, one per byte (get_scale_min_k4 layout)
         uint32_t SC, MM;
         if (g == 0) {
@@ -471,11 +470,21 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
             SC = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
             MM = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
         }
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            As[q] = (_Float16)(d * (float)((SC >> (8 * q)) & 0xFFu));     // half(d*sc), as the reference rounds it
-            Am[q] = (_Float16)(-dmin * (float)((MM >> (8 * q)) & 0xFFu));
-        }
+        // half(d*sc) and half(-dmin*m) as the reference rounds them, in packed
+        // fp16: the bytes become the halves 1024 + v (a byte permute against
+        // 0x64 bytes), minus 1024 is v exactly, and one fp16 multiply rounds
+        // the exact product d*v once -- the same half as the fp32 product
+        // (exact: 11 x 6 bits) converted to fp16
+        const uint32_t hi = 0x64646464u;
+        const h4m k1024 = h4m{(_Float16)1024.0f, (_Float16)1024.0f, (_Float16)1024.0f, (_Float16)1024.0f};
+        const h4m scv = __builtin_bit_cast(h4m, u32x2m{__builtin_amdgcn_perm(hi, SC, 0x04010400u),
+                                                        __builtin_amdgcn_perm(hi, SC, 0x04030402u)}) - k1024;
+        const h4m mv = __builtin_bit_cast(h4m, u32x2m{__builtin_amdgcn_perm(hi, MM, 0x04010400u),
+                                                       __builtin_amdgcn_perm(hi, MM, 0x04030402u)}) - k1024;
+        const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)(hdr.x & 0xFFFFu));
+        const _Float16 mh = -__builtin_bit_cast(_Float16, (uint16_t)(hdr.x >> 16));
+        As = scv * h4m{dh, dh, dh, dh};
+        Am = mv * h4m{mh, mh, mh, mh};
     };
 
     auto compute = [&](int k, const u32x4m (&a)[2]) {
