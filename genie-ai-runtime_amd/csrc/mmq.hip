@@ -775,7 +775,9 @@ void mmq_q6k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const u
     const int n_rt = (M + TM - 1) / TM, n_tt = (Npad + Q6_TN - 1) / Q6_TN;
     const int tile = xcd_tile(blockIdx.x, n_rt * n_tt);
     const int row0 = (tile / n_tt) * TM, col0 = (tile % n_tt) * Q6_TN;
-    const int t = threadIdx.x, w = t >> 6, l = t & 63, li = l & 31, g = l >> 5;
+    // w is wave-uniform: read into a scalar register, so the DMA's scalar
+    // offsets that use it need no per-lane (waterfall) loop
+    const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63, li = l & 31, g = l >> 5;
     const int arow = 32 * w + li;
 
     const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0,
