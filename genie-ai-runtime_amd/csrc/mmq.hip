@@ -401,7 +401,9 @@ __device__ __forceinline__ void mmq_q4k_body(const MmqSegs& sg, const uint8_t* _
     const int M = sg.M[sgi];
     // OUT 4: wave w's rows are 64 rt + 32 (w & 1) + lane (of gate or up)
     const int row0 = OUT == 4 ? 64 * rt - 64 * (wq >> 1) : (rt - sg.rt0[sgi]) * TM, col0 = (tile % n_tt) * TNv;
-    const int t = threadIdx.x, w = t >> 6, l = t & 63, li = l & 31, g = l >> 5;
+    // w in a scalar register: the LDS addresses and row offsets derived from
+    // it stay scalar (9728 x 2560 at N = 512 63.5 -> 58.4 us)
+    const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63, li = l & 31, g = l >> 5;
     const int arow = 32 * w + li;                      // this lane's A-operand row
 
     const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0,
@@ -777,6 +779,8 @@ void mmq_q6k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const u
     const int row0 = (tile / n_tt) * TM, col0 = (tile % n_tt) * Q6_TN;
     // w is wave-uniform: read into a scalar register, so the DMA's scalar
     // offsets that use it need no per-lane (waterfall) loop
+    // w in a scalar register: the LDS addresses and row offsets derived from
+    // it stay scalar (9728 x 2560 at N = 512 63.5 -> 58.4 us)
     const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63, li = l & 31, g = l >> 5;
     const int arow = 32 * w + li;
 
