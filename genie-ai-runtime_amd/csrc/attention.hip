@@ -700,7 +700,7 @@ void attn_reduce_kernel(uint16_t* __restrict__ out, const float* __restrict__ pa
     __shared__ float sW[AT_MAXS];
     __shared__ float sRed[AT_RED_THREADS / 64];
     __shared__ float sSum[AT_RED_THREADS / 64][AT_MAXHD];
-    const int h = red_head(n_heads, n_kv), t = threadIdx.x, w = t >> 6, l = t & 63;
+    const int h = red_head(n_heads, n_kv), t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
     const float* pm = part + (int64_t)h * S;
     const float* pl = part + (int64_t)n_heads * S + (int64_t)h * S;
     const float* pacc = part + (int64_t)n_heads * S * 2 + (int64_t)h * S * hd;

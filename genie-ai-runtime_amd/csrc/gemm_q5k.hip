@@ -131,7 +131,7 @@ void gemm_q5k_kernel(void* __restrict__ y, const uint8_t* __restrict__ W, const 
     const int n_rt = (M + TM - 1) / TM, n_tt = (N + TN - 1) / TN;
     const int tile = xcd_tile_q5(blockIdx.x, n_rt * n_tt);
     const int row0 = (tile / n_tt) * TM, col0 = (tile % n_tt) * TN;
-    const int t = threadIdx.x, w = t >> 6, l = t & 63, li = l & 31, kg = l >> 5;
+    const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63, li = l & 31, kg = l >> 5;
 
     const uint8_t* wrow = W + (int64_t)min(row0 + 32 * w + li, M - 1) * nb * Q5K_BYTES;   // rows past M re-read the last
     const int xtok = t >> 2, xq = t & 3;

@@ -248,7 +248,7 @@ __global__ __launch_bounds__(256) void qk_post_kernel(QKPostArgs a) {
                  "s"(a.kv_int8), "s"(a.q_in_stride), "s"(a.kv_in_stride), "s"(a.pos_dev));
     const int hd = a.head_dim;
     const int slots = a.n_heads + 2 * a.n_kv;
-    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int gw = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);   // wave-uniform: scalar
     const int l = threadIdx.x & 63;
     if (gw >= slots * a.N) return;                      // whole wave exits together
     const int t = gw / slots, slot = gw % slots;
