@@ -137,7 +137,9 @@ __host__ __device__ size_t attn_wave_lds_bytes(int n_heads, int n_kv, int head_d
     const int G = n_heads / n_kv * tq;                                // columns of a wave
     const bool ps = tq > 1;                                          // prefill: one row per column
     const size_t loop = (size_t)(ps ? 64 : 32) * AT_PLD * 2 + 96 * 4; // P' rows (fp16) + corr/ks/vs
-    const size_t outb = (size_t)(((ps ? G : 2 * G) + 7) & ~7) * head_dim * 4;   // final rows (fp32, >= 8)
+    // final rows (fp32, >= 8); prefill: all 32 rows of the accumulator layout,
+    // so the epilogue stores them without a per-row predicate
+    const size_t outb = (size_t)(ps ? 32 : ((2 * G + 7) & ~7)) * head_dim * 4;
     return ((loop > outb ? loop : outb) + 15) & ~(size_t)15;
 }
 // a workgroup of W waves: W wave regions, then (m, l) of each wave's columns
@@ -573,7 +575,7 @@ void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
         for (int vv = 0; vv < 16; vv++) {
             const int r = 8 * (vv >> 2) + 4 * lg + (vv & 3);
-            if (r < (PS ? GC : 2 * GC)) sO[r * hd + 32 * dt + li] = acc[dt][vv];
+            if (PS || r < 2 * GC) sO[r * hd + 32 * dt + li] = acc[dt][vv];   // PS: rows >= GC are never read
         }
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
