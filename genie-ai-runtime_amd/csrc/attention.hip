@@ -433,15 +433,22 @@ void attn_partial_kernel(AttnArgs a) {
     // the next tile's rows load into (rk, rv) while the current one (a copy)
     // is computed
     // wave wv of W takes tiles wv, wv + W, ... of the workgroup's key range
-    for (int p0 = first; p0 < kv1; p0 += stride) {
+    // (the last tile is computed straight from the load registers: no copy,
+    // and Q.K^T starts once the K rows have landed)
+    int p0 = first;
+    for (; p0 + stride < kv1; p0 += stride) {
         u32x4a ck[KW], cv[VW];
 #pragma unroll
         for (int c = 0; c < KW; c++) ck[c] = rk[c];
 #pragma unroll
         for (int c = 0; c < VW; c++) cv[c] = rv[c];
         const float ksc = ksn * a.scale, vsc = vsn;
-        if (p0 + stride < kv1) load_tile(p0 + stride, rk, rv, ksn, vsn);
+        load_tile(p0 + stride, rk, rv, ksn, vsn);
         tile(p0, ck, cv, ksc, vsc);
+        if (p0 == first) AT_MARK(1);
+    }
+    if (p0 < kv1) {
+        tile(p0, rk, rv, ksn * a.scale, vsn);
         if (p0 == first) AT_MARK(1);
     }
     AT_MARK(2);
